@@ -1,0 +1,162 @@
+/* nlgpu.h -- C ABI of the MI355X (gfx950) implementation of nelisp-gpu's
+ * quantized-LLM kernel path.
+ *
+ * Everything here is plain C: device pointers are `void*` / typed pointers,
+ * sizes are integers, streams are opaque `void*` (a hipStream_t; NULL means
+ * the library's own stream).  No HIP or torch type appears in a signature, so
+ * the CLI hosts (vkserver, vkrun, vkmatmul, vksoftmax, vkcompute) and any
+ * FFI (ctypes, cgo, an Emacs module) can bind it directly.
+ *
+ * Every function returns NLG_OK (0) on success and NLG_ERR (1) on failure,
+ * with a message available from nlg_last_error().  No function exits the
+ * process; the CLI hosts decide what a failure means for them.
+ *
+ * Reference interfaces replaced (paths under zawatton/nelisp-gpu):
+ *   device bring-up        host/vkserver.c:213-245 (init_vulkan),
+ *                          host/vkcompute.c:90-100 (NELISP_GPU_DEVICE policy)
+ *   buffers                host/vkserver.c:126-149 (make_buffer_ex),
+ *                          :169-205 (staged_write), :207-211 (write_buffer)
+ *   kernel by name         host/vkserver.c:247-272 (get_kernel),
+ *                          :312-322 (record + submit one dispatch)
+ *   fused batch / compiled host/vkserver.c:437-506 (handle_batch),
+ *                          :511-604 (handle_compile / handle_run_compiled)
+ *   kernel semantics       lisp/nelisp-gpu-kernels.el (one entry per name)
+ */
+#ifndef NLGPU_H
+#define NLGPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NLG_OK 0
+#define NLG_ERR 1
+
+/* ------------------------------------------------------------------------
+ * Device, memory, streams
+ * ---------------------------------------------------------------------- */
+
+/* Select and initialise the GPU.  device < 0 applies the reference policy:
+ * env NELISP_GPU_DEVICE if set, else device 0 (every MI355X is discrete).
+ * Replaces host/vkserver.c:213-245 and host/vkcompute.c:90-100.  Idempotent. */
+int nlg_init(int device);
+/* Release the library's stream, staging and graph objects. */
+int nlg_shutdown(void);
+/* Message for the most recent failure on this thread ("" if none). */
+const char *nlg_last_error(void);
+/* Marketing name of the active device (e.g. "AMD Instinct MI355X"). */
+int nlg_device_name(char *buf, size_t len);
+/* Number of compute units and the active device's gfx name. */
+int nlg_device_info(int *num_cu, char *arch, size_t arch_len);
+
+/* Device memory, zero-filled.  Replaces make_buffer_ex (vkserver.c:126-149):
+ * every buffer lives in HBM (no HOST_VISIBLE fallback is needed with 288 GB).
+ * Returns NULL on failure. */
+void *nlg_malloc(size_t bytes);
+int nlg_free(void *dev);
+/* Synchronous copies (host memory may be pageable).  Replaces write_buffer /
+ * staged_write (vkserver.c:169-211) and the map-and-fwrite read-back
+ * (vkserver.c:325-330). */
+int nlg_upload(void *dev_dst, const void *host_src, size_t bytes);
+int nlg_download(void *host_dst, const void *dev_src, size_t bytes);
+int nlg_copy_d2d(void *dev_dst, const void *dev_src, size_t bytes, void *stream);
+/* Zero `bytes` of device memory with a fill kernel (safe inside a captured
+ * graph, unlike a runtime memset).  Replaces vkCmdFillBuffer (vkserver.c:554-556). */
+int nlg_zero(void *dev, size_t bytes, void *stream);
+/* Read `bytes` at `offset` of `path` into device memory through pinned
+ * staging.  *missing receives the number of bytes the file could not supply
+ * (the tail of dev is then zero).  Replaces handle_upload_file's
+ * fread+staged_write (vkserver.c:371-410). */
+int nlg_upload_file(void *dev_dst, const char *path, uint64_t offset, size_t bytes,
+                    size_t *missing);
+
+void *nlg_stream_create(void);
+int nlg_stream_destroy(void *stream);
+int nlg_stream_sync(void *stream);
+/* The library's default stream (what NULL means). */
+void *nlg_default_stream(void);
+
+/* Device-side timing: events recorded on a stream. */
+void *nlg_event_create(void);
+int nlg_event_destroy(void *ev);
+int nlg_event_record(void *ev, void *stream);
+int nlg_event_elapsed_ms(void *start, void *stop, float *ms);
+
+/* ------------------------------------------------------------------------
+ * Kernels by name: the lisp/nelisp-gpu-kernels.el ABI
+ * ---------------------------------------------------------------------- */
+
+/* One buffer binding: a device pointer and its length in 4-byte elements
+ * (the reference's "float count"; packed words ride in the same slots). */
+typedef struct {
+  void *ptr;
+  uint32_t nfloats;
+} nlg_buffer;
+
+/* Number of kernel names the library implements, their names, and the
+ * binding/push-constant counts each expects (Appendix-A order of
+ * lisp/nelisp-gpu-kernels.el :buffers and :push). */
+int nlg_kernel_count(void);
+const char *nlg_kernel_name(int index);
+int nlg_kernel_lookup(const char *name);
+int nlg_kernel_abi(const char *name, uint32_t *nbuf, uint32_t *npush);
+
+/* Run kernel `name` as the reference would run `groups` workgroups of 64
+ * invocations: every invocation gid < min(domain, 64*groups) does the work
+ * its DSL body defines.  Buffers are checked against the extents the push
+ * constants imply before anything is launched (status NLG_ERR, nothing run, if
+ * a buffer is short); data-dependent indices (POS, TOK, TABLE) are bounds-
+ * checked on the device (out-of-range reads give 0, writes are dropped).
+ * Replaces get_kernel (vkserver.c:247-272) plus one vkCmdDispatch
+ * (vkserver.c:312-322, vkrun.c:117-123). */
+int nlg_dispatch(const char *name, const nlg_buffer *bufs, uint32_t nbuf,
+                 const uint32_t *push, uint32_t npush, uint32_t groups, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Graphs: a recorded sequence of launches replayed with one call.
+ * Replaces OP_COMPILE / OP_RUN_COMPILED / OP_FREE_COMPILED
+ * (vkserver.c:511-615).  Capture is stream capture: everything launched on
+ * `stream` between begin and end is recorded, not executed.
+ * ---------------------------------------------------------------------- */
+int nlg_graph_begin(void *stream);
+int nlg_graph_end(void *stream, void **graph_exec);
+int nlg_graph_launch(void *graph_exec, void *stream);
+int nlg_graph_destroy(void *graph_exec);
+
+/* ------------------------------------------------------------------------
+ * Typed hot path (device pointers)
+ * ---------------------------------------------------------------------- */
+
+/* Per-row absmax int8 quantisation + packing.  gamma[r] = max|x[r,:]| / 127;
+ * lane = uint(|x/gamma| + 0.5) clamped to 127, negatives stored as 256-lane;
+ * four lanes per u32 word, lane l in bits 8l..8l+7; ng = ceil(cols/4) words
+ * per row.  Bit-identical to `pack-act-rows` (lisp/nelisp-gpu-kernels.el:884-932). */
+int nlg_pack_act_rows(const float *x, uint32_t *xq, float *gamma, uint32_t seq,
+                      uint32_t cols, void *stream);
+
+/* Ternary 2-bit weights x int8 activations, int32 accumulation, fp32 epilogue:
+ *   acc[s,o] = sum_c decode(W[o,c]) * int8(xq[s,c])         (exact int32)
+ *   y[s,o]   = bias[o] + (beta[b] * gamma[s]) * (float)acc  (IEEE, no FMA)
+ * with b = o when beta_per_row, else 0.  W is the reference's 2-bit format:
+ * row-major, wng = ceil(cols/16) u32 words per row, field f of a word in bits
+ * 2f..2f+1, 00->0 01->+1 11->-1 10->-2 (ternary-rows, kernels.el:700-746).
+ * The accumulation and epilogue are bitlinear-dp4a-1f's (kernels.el:619-634)
+ * on the 2-bit weights unpacked to int8 lanes.  bias may be NULL (zero).
+ * Requires cols <= 131072 (int32 headroom of the x64-scaled partial sums). */
+int nlg_ternary_linear_i8(const uint32_t *xq, const float *gamma, const uint32_t *w2,
+                          const float *bias, const float *beta, int beta_per_row,
+                          float *y, uint32_t seq, uint32_t out, uint32_t cols,
+                          void *stream);
+
+/* Row softmax, numerically stable (row max subtracted), in place when
+ * c == a.  Semantics of `softmax` (kernels.el:28-42). */
+int nlg_softmax_rows(const float *a, float *c, uint32_t rows, uint32_t cols, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NLGPU_H */

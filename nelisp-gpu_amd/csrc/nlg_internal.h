@@ -1,0 +1,179 @@
+// nlg_internal.h -- shared declarations of libnlgpu's HIP translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nlgpu.h"
+
+// ---------------------------------------------------------------- host side
+
+// Record a failure message for nlg_last_error(); always returns NLG_ERR.
+int nlg_fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+// NULL -> the library stream.  Requires nlg_init() (done lazily).
+hipStream_t nlg_stream(void *s);
+// Ensure the device is initialised (nlg_init(-1) on first use).
+int nlg_ensure_init(void);
+int nlg_num_cu(void);
+
+#define NLG_HIP(call)                                                              \
+  do {                                                                             \
+    hipError_t _e = (call);                                                        \
+    if (_e != hipSuccess)                                                          \
+      return nlg_fail("%s failed: %s (%s:%d)", #call, hipGetErrorString(_e),     \
+                      __FILE__, __LINE__);                                         \
+  } while (0)
+
+// Check a launch that just happened.
+#define NLG_LAUNCHED(what)                                                         \
+  do {                                                                             \
+    hipError_t _e = hipGetLastError();                                             \
+    if (_e != hipSuccess)                                                          \
+      return nlg_fail("launch of %s failed: %s", (what), hipGetErrorString(_e));   \
+  } while (0)
+
+// A kernel reachable by name: validates buffers against the extents its
+// push constants imply, then launches on `st`.
+typedef int (*nlg_launcher)(const nlg_buffer *b, const uint32_t *p, uint32_t groups,
+                            hipStream_t st);
+
+// Buffer i must hold at least `need` elements (need computed in 64 bits).
+int nlg_need(const nlg_buffer *b, int i, uint64_t need, const char *kname);
+
+// min(domain, 64*groups): how many invocations of a local-64 kernel do work.
+static inline uint64_t nlg_domain(uint64_t domain, uint32_t groups, uint32_t local = 64) {
+  uint64_t lim = (uint64_t)groups * local;
+  return domain < lim ? domain : lim;
+}
+
+// grid size for n items with `per` items per block, at least 1.
+static inline uint32_t nlg_blocks(uint64_t n, uint64_t per) {
+  uint64_t b = (n + per - 1) / per;
+  if (b == 0) b = 1;
+  if (b > 0x7fffffffull) b = 0x7fffffffull;
+  return (uint32_t)b;
+}
+
+// ---------------------------------------------------------------- device side
+
+// (uint f) of the DSL: OpConvertFToS into a uint (lisp/nelisp-gpu-compile.el:327).
+// Truncation toward zero; NaN -> 0 and out-of-range saturates (undefined in
+// SPIR-V; the CPU restatement uses the same convention).
+__device__ __forceinline__ uint32_t nlg_f2u(float f) {
+  if (!(f == f)) return 0u;
+  if (f >= 2147483648.0f) return 0x7fffffffu;
+  if (f <= -2147483648.0f) return 0x80000000u;
+  return (uint32_t)(int32_t)f;
+}
+
+// Wave64 reductions on DPP.  Lanes 0..63 must all be active.  Each returns
+// the full-wave result in every lane (read back from lane 63).
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int nlg_dpp(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
+}
+
+__device__ __forceinline__ int nlg_wave_sum_i32(int v) {
+  v += nlg_dpp<0xB1>(v);        // quad_perm [1,0,3,2]
+  v += nlg_dpp<0x4E>(v);        // quad_perm [2,3,0,1]
+  v += nlg_dpp<0x124>(v);       // row_ror:4
+  v += nlg_dpp<0x128>(v);       // row_ror:8   -> every lane holds its row's sum
+  v += nlg_dpp<0x142, 0xa>(v);  // row_bcast:15 into rows 1,3
+  v += nlg_dpp<0x143, 0xc>(v);  // row_bcast:31 into rows 2,3
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+__device__ __forceinline__ float nlg_fdpp_add(float v, int x) { return v + __int_as_float(x); }
+
+__device__ __forceinline__ float nlg_wave_sum_f32(float v) {
+  v = v + __int_as_float(nlg_dpp<0xB1>(__float_as_int(v)));
+  v = v + __int_as_float(nlg_dpp<0x4E>(__float_as_int(v)));
+  v = v + __int_as_float(nlg_dpp<0x124>(__float_as_int(v)));
+  v = v + __int_as_float(nlg_dpp<0x128>(__float_as_int(v)));
+  v = v + __int_as_float(nlg_dpp<0x142, 0xa>(__float_as_int(v)));
+  v = v + __int_as_float(nlg_dpp<0x143, 0xc>(__float_as_int(v)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Max over the wave of values that are never NaN; lanes in rows masked off by
+// the broadcast steps receive 0 from the DPP move, so the identity used for
+// those steps must be handled: callers pass values >= `floor` and floor is
+// what masked lanes compare against.
+__device__ __forceinline__ float nlg_fmax_nn(float a, float b) { return b > a ? b : a; }
+
+__device__ __forceinline__ float nlg_wave_max_f32(float v) {
+  // rotations keep every lane valid, so no identity is needed for them
+  v = nlg_fmax_nn(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0xB1, 0xf, 0xf, false)));
+  v = nlg_fmax_nn(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x4E, 0xf, 0xf, false)));
+  v = nlg_fmax_nn(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x124, 0xf, 0xf, false)));
+  v = nlg_fmax_nn(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x128, 0xf, 0xf, false)));
+  // masked rows keep `old` = their own value, so max(v, v) = v there
+  v = nlg_fmax_nn(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x142, 0xa, 0xf, false)));
+  v = nlg_fmax_nn(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x143, 0xc, 0xf, false)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Block-wide (blockDim.x multiple of 64, <= 1024) sum / max through LDS.
+// `scratch` needs blockDim.x/64 floats.  Every thread gets the result.
+__device__ __forceinline__ float nlg_block_sum_f32(float v, float *scratch) {
+  v = nlg_wave_sum_f32(v);
+  const int nw = blockDim.x >> 6, w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[w] = v;
+  __syncthreads();
+  float t = 0.0f;
+  for (int i = 0; i < nw; i++) t = t + scratch[i];
+  return t;
+}
+__device__ __forceinline__ float nlg_block_max_f32(float v, float *scratch) {
+  v = nlg_wave_max_f32(v);
+  const int nw = blockDim.x >> 6, w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[w] = v;
+  __syncthreads();
+  float t = scratch[0];
+  for (int i = 1; i < nw; i++) t = nlg_fmax_nn(t, scratch[i]);
+  return t;
+}
+
+// ---------------------------------------------------------------- launchers
+// One per kernel name (Appendix A of the survey, lisp/nelisp-gpu-kernels.el).
+#define NLG_DECL(fn) int fn(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st)
+NLG_DECL(L_vadd);
+NLG_DECL(L_add2);
+NLG_DECL(L_mul);
+NLG_DECL(L_scale);
+NLG_DECL(L_causal_mask);
+NLG_DECL(L_silu);
+NLG_DECL(L_silu_mul);
+NLG_DECL(L_rmsnorm_fwd);
+NLG_DECL(L_embed_gather);
+NLG_DECL(L_cache_append);
+NLG_DECL(L_cache_append_b);
+NLG_DECL(L_qkv_append);
+NLG_DECL(L_decode_rope);
+NLG_DECL(L_decode_rope_b);
+NLG_DECL(L_rope_apply);
+NLG_DECL(L_rope_half);
+NLG_DECL(L_softmax);
+NLG_DECL(L_rmsnorm_istd);
+NLG_DECL(L_rmsnorm_heads);
+NLG_DECL(L_pack_act_rows);
+NLG_DECL(L_quant_act);
+NLG_DECL(L_dp4a_dot);
+NLG_DECL(L_bitlinear_dp4a);
+NLG_DECL(L_bitlinear_dp4a_1f);
+NLG_DECL(L_bitlinear_dp4a_rows);
+NLG_DECL(L_ternary_rows);
+NLG_DECL(L_bitlinear_packed);
+NLG_DECL(L_bitlinear_packed_v);
+NLG_DECL(L_matmul);
+NLG_DECL(L_matmul_tiled);
+NLG_DECL(L_matmul_reg);
+NLG_DECL(L_linear);
+NLG_DECL(L_attn_scores);
+NLG_DECL(L_attn_context);
+NLG_DECL(L_decode_attn);
+NLG_DECL(L_decode_attn_b);
+NLG_DECL(L_attn_causal_gqa);
+NLG_DECL(L_ternary_i8);

@@ -1,0 +1,614 @@
+// nlg_ternary.hip -- int8 activation quantisation and the ternary / int8
+// linears: the decode GEMV at the centre of the hot path.
+//
+// Formats (lisp/nelisp-gpu-kernels.el):
+//   activations  pack-act-rows (:884-932): per row gamma = amax/127 and four
+//                signed int8 lanes per u32 word, lane l = column 4w+l.
+//   2-bit weights ternary-rows (:700-746): 16 fields per u32, field f in bits
+//                2f..2f+1, decoded by sign extension: 00 0, 01 +1, 11 -1, 10 -2.
+//   int8 weights bitlinear-dp4a-1f (:619-634): four int8 lanes per u32.
+//
+// The 2-bit x int8 decode GEMV (nlg_ternary_linear_i8): a wave owns R output
+// rows; each lane streams 16-byte chunks (4 words = 64 weights) of those rows
+// with one global_load_dwordx4 per row, so a wave reads 1 KiB of contiguous
+// row per instruction.  A field moved to bits 6..7 of its byte reads, as a
+// signed int8, exactly 64x its decoded value (00->0, 01->64, 10->-128,
+// 11->-64), so `(w << (6-2s)) & 0xC0C0C0C0` turns fields s, s+4, s+8, s+12
+// of a word into a dot4 operand with no sign fix-up.  The matching
+// activation bytes are gathered with v_perm_b32 (a 4x4 byte transpose per
+// 16 columns, done once per wave and reused for every row).  The int32 sum
+// is therefore 64x the exact accumulator and `>> 6` recovers it exactly;
+// the fp32 epilogue is bitlinear-dp4a-1f's, evaluated without contraction.
+#include "nlg_internal.h"
+
+// ------------------------------------------------------------ quantisation
+
+// |v| as the DSL computes it: (when (< v 0.0) (set av (- 0.0 v))).
+__device__ __forceinline__ float dsl_abs(float v) { return v < 0.0f ? 0.0f - v : v; }
+
+// One lane of pack-act-rows (kernels.el:912-926): returns the stored byte.
+__device__ __forceinline__ uint32_t pack_lane(float v, float gamma) {
+  float q = 0.0f;
+  if (gamma > 0.0f) q = v / gamma;
+  uint32_t neg = 0;
+  float aq = q;
+  if (q < 0.0f) {
+    neg = 1;
+    aq = 0.0f - q;
+  }
+  uint32_t ri = nlg_f2u(aq + 0.5f);
+  if (ri > 127u) ri = 127u;
+  return neg ? (256u - ri) % 256u : ri;
+}
+
+// One workgroup per row.  Pass 1: amax (order-free: the DSL max never
+// selects a NaN and starts from 0).  Pass 2: one packed word per thread-step.
+template <bool VEC4>
+__global__ __launch_bounds__(256) void k_pack_act_rows(const float *__restrict__ x,
+                                                       uint32_t *__restrict__ xq,
+                                                       float *__restrict__ gamma, uint32_t rows,
+                                                       uint32_t cols, uint32_t ng) {
+  __shared__ float red[4];
+  const uint32_t row = blockIdx.x;
+  if (row >= rows) return;
+  const float *xr = x + (size_t)row * cols;
+  float amax = 0.0f;
+  if (VEC4) {
+    const float4 *x4 = (const float4 *)xr;
+    for (uint32_t c = threadIdx.x; c < cols / 4; c += blockDim.x) {
+      float4 v = x4[c];
+      float a;
+      a = dsl_abs(v.x); amax = a > amax ? a : amax;
+      a = dsl_abs(v.y); amax = a > amax ? a : amax;
+      a = dsl_abs(v.z); amax = a > amax ? a : amax;
+      a = dsl_abs(v.w); amax = a > amax ? a : amax;
+    }
+  } else {
+    for (uint32_t c = threadIdx.x; c < cols; c += blockDim.x) {
+      float a = dsl_abs(xr[c]);
+      amax = a > amax ? a : amax;
+    }
+  }
+  amax = nlg_block_max_f32(amax, red);
+  const float g = amax / 127.0f;
+  if (threadIdx.x == 0) gamma[row] = g;
+  uint32_t *q = xq + (size_t)row * ng;
+  for (uint32_t w = threadIdx.x; w < ng; w += blockDim.x) {
+    uint32_t word = 0;
+    if (VEC4 && 4 * w + 3 < cols) {
+      float4 v = ((const float4 *)xr)[w];
+      word = pack_lane(v.x, g) | (pack_lane(v.y, g) << 8) | (pack_lane(v.z, g) << 16) |
+             (pack_lane(v.w, g) << 24);
+    } else {
+      for (uint32_t l = 0; l < 4; l++) {
+        uint32_t c = 4 * w + l;
+        if (c < cols) word |= pack_lane(xr[c], g) << (8 * l);
+      }
+    }
+    q[w] = word;
+  }
+}
+
+static int launch_pack_act(const float *x, uint32_t *xq, float *gamma, uint32_t rows, uint32_t cols,
+                           uint32_t ng, hipStream_t st) {
+  if (!rows) return NLG_OK;
+  bool v4 = (cols % 4 == 0) && (((uintptr_t)x & 15) == 0);
+  if (v4)
+    hipLaunchKernelGGL(k_pack_act_rows<true>, dim3(rows), dim3(256), 0, st, x, xq, gamma, rows,
+                       cols, ng);
+  else
+    hipLaunchKernelGGL(k_pack_act_rows<false>, dim3(rows), dim3(256), 0, st, x, xq, gamma, rows,
+                       cols, ng);
+  NLG_LAUNCHED("pack-act-rows");
+  return NLG_OK;
+}
+
+extern "C" int nlg_pack_act_rows(const float *x, uint32_t *xq, float *gamma, uint32_t seq,
+                                 uint32_t cols, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  return launch_pack_act(x, xq, gamma, seq, cols, (cols + 3) / 4, nlg_stream(stream));
+}
+
+// pack-act-rows by name: X XQ GAMMA; push (seq cols ng)
+int L_pack_act_rows(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
+  const uint32_t seq = p[0], cols = p[1], ng = p[2];
+  const uint64_t rows = nlg_domain(seq, groups);
+  if (nlg_need(b, 0, rows * cols, "pack-act-rows") || nlg_need(b, 1, rows * ng, "pack-act-rows") ||
+      nlg_need(b, 2, rows, "pack-act-rows"))
+    return NLG_ERR;
+  return launch_pack_act((const float *)b[0].ptr, (uint32_t *)b[1].ptr, (float *)b[2].ptr,
+                         (uint32_t)rows, cols, ng, st);
+}
+
+// quant-act (kernels.el:527-547): fake quantisation, gamma*sgn*min(round,127).
+__global__ __launch_bounds__(256) void k_quant_act(const float *__restrict__ x, float *__restrict__ xq,
+                                                   uint32_t rows, uint32_t cols) {
+  __shared__ float red[4];
+  const uint32_t row = blockIdx.x;
+  if (row >= rows) return;
+  const float *xr = x + (size_t)row * cols;
+  float amax = 0.0f;
+  for (uint32_t c = threadIdx.x; c < cols; c += blockDim.x) {
+    float a = dsl_abs(xr[c]);
+    amax = a > amax ? a : amax;
+  }
+  amax = nlg_block_max_f32(amax, red);
+  const float g = amax / 127.0f;
+  __syncthreads();  // in place: every read of the row precedes any write
+  for (uint32_t c = threadIdx.x; c < cols; c += blockDim.x) {
+    float v = xr[c], out = 0.0f;
+    if (g > 0.0f) {
+      float q = v / g, sgn = 1.0f, aq = q;
+      if (q < 0.0f) {
+        sgn = -1.0f;
+        aq = 0.0f - q;
+      }
+      uint32_t ri = nlg_f2u(aq + 0.5f);
+      float rf = (float)ri;
+      if (rf > 127.0f) rf = 127.0f;
+      out = __fmul_rn(g, __fmul_rn(sgn, rf));
+    }
+    xq[(size_t)row * cols + c] = out;
+  }
+}
+
+int L_quant_act(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
+  const uint32_t seq = p[0], cols = p[1];
+  const uint64_t rows = nlg_domain(seq, groups);
+  if (nlg_need(b, 0, rows * cols, "quant-act") || nlg_need(b, 1, rows * cols, "quant-act"))
+    return NLG_ERR;
+  if (!rows) return NLG_OK;
+  hipLaunchKernelGGL(k_quant_act, dim3((uint32_t)rows), dim3(256), 0, st, (const float *)b[0].ptr,
+                     (float *)b[1].ptr, (uint32_t)rows, cols);
+  NLG_LAUNCHED("quant-act");
+  return NLG_OK;
+}
+
+// ------------------------------------------------------ 2-bit x int8 GEMV
+
+// 4x4 byte transpose: X[k] holds columns 4k..4k+3 of a 16-column group;
+// Y[s] byte k = X[k] byte s = column 4k+s, the order the masked weight
+// bytes of field group s come in.
+__device__ __forceinline__ void xpose4(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
+                                       uint32_t &y0, uint32_t &y1, uint32_t &y2, uint32_t &y3) {
+  const uint32_t a = __builtin_amdgcn_perm(x1, x0, 0x05010400u);  // x0.b0 x1.b0 x0.b1 x1.b1
+  const uint32_t b = __builtin_amdgcn_perm(x1, x0, 0x07030602u);  // x0.b2 x1.b2 x0.b3 x1.b3
+  const uint32_t c = __builtin_amdgcn_perm(x3, x2, 0x05010400u);  // x2.b0 x3.b0 x2.b1 x3.b1
+  const uint32_t d = __builtin_amdgcn_perm(x3, x2, 0x07030602u);  // x2.b2 x3.b2 x2.b3 x3.b3
+  y0 = __builtin_amdgcn_perm(c, a, 0x05040100u);
+  y1 = __builtin_amdgcn_perm(c, a, 0x07060302u);
+  y2 = __builtin_amdgcn_perm(d, b, 0x05040100u);
+  y3 = __builtin_amdgcn_perm(d, b, 0x07060302u);
+}
+
+// 64 x (sum over the 16 fields of w of decode(field) * x[column]).
+__device__ __forceinline__ int wdot(uint32_t w, uint32_t y0, uint32_t y1, uint32_t y2, uint32_t y3,
+                                    int acc) {
+  acc = __builtin_amdgcn_sdot4((int)((w << 6) & 0xC0C0C0C0u), (int)y0, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)((w << 4) & 0xC0C0C0C0u), (int)y1, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)((w << 2) & 0xC0C0C0C0u), (int)y2, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)(w & 0xC0C0C0C0u), (int)y3, acc, false);
+  return acc;
+}
+
+struct TernArgs {
+  const uint32_t *xq;    // [seq x ng]
+  const float *gamma;    // [seq]
+  const uint32_t *w2;    // [out x wng]
+  const float *bias;     // [out] or null
+  const float *beta;     // [1] or [out]
+  float *y;              // [seq x out]
+  uint32_t seq, out, cols, ng, wng;
+  int beta_per_row;
+};
+
+__device__ __forceinline__ void tern_store(const TernArgs &a, uint32_t s, uint32_t o, int acc64) {
+  const float acc = (float)(acc64 >> 6);  // exact: acc64 is a multiple of 64
+  const float bo = a.bias ? a.bias[o] : 0.0f;
+  const float be = a.beta[a.beta_per_row ? o : 0];
+  // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
+  a.y[(size_t)s * a.out + o] = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, a.gamma[s]), acc));
+}
+
+// FAST path: cols % 16 == 0 (so rows are whole 16-byte chunks and the
+// activation rows are 16-byte aligned).  R rows per wave, ST tokens per block
+// (blockIdx.y picks the token tile).
+template <int R, int ST>
+__global__ __launch_bounds__(256) void k_tern_i8_fast(TernArgs a) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const uint32_t row0 = wave * R;
+  if (row0 >= a.out) return;  // wave-uniform
+  const uint32_t s0 = blockIdx.y * ST;
+  const uint32_t nchunk = a.wng >> 2;  // 4 words per chunk
+  const uint4 *wrow[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    uint32_t row = row0 + r < a.out ? row0 + r : a.out - 1;  // tail rows: read a real row, discard
+    wrow[r] = (const uint4 *)(a.w2 + (size_t)row * a.wng);
+  }
+  int acc[R][ST];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int s = 0; s < ST; s++) acc[r][s] = 0;
+
+  // Lanes leave this loop at different trips and reconverge after it, so the
+  // DPP reductions below run with the full wave active.
+  for (uint32_t c = lane; c < nchunk; c += 64) {
+    const bool valid = true;
+    uint4 wv[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) wv[r] = wrow[r][c];
+#pragma unroll
+    for (int s = 0; s < ST; s++) {
+      const uint32_t tok = s0 + s;
+      if (ST > 1 && tok >= a.seq) break;
+      uint4 xv[4];
+      const uint4 *xr = (const uint4 *)(a.xq + (size_t)tok * a.ng) + 4 * c;
+#pragma unroll
+      for (int j = 0; j < 4; j++) xv[j] = valid ? xr[j] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        uint32_t y0, y1, y2, y3;
+        xpose4(xv[j].x, xv[j].y, xv[j].z, xv[j].w, y0, y1, y2, y3);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          const uint32_t w = j == 0 ? wv[r].x : j == 1 ? wv[r].y : j == 2 ? wv[r].z : wv[r].w;
+          acc[r][s] = wdot(w, y0, y1, y2, y3, acc[r][s]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < ST; s++) {
+    const uint32_t tok = s0 + s;
+    if (ST > 1 && tok >= a.seq) break;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int tot = nlg_wave_sum_i32(acc[r][s]);
+      if (lane == r && row0 + r < a.out) tern_store(a, tok, row0 + r, tot);
+    }
+  }
+}
+
+// GENERAL path: any cols.  One 2-bit word (16 columns) per lane-step, scalar
+// loads; fields at or beyond `cols` are masked off and activation words past
+// ng read as zero.
+template <int R>
+__global__ __launch_bounds__(256) void k_tern_i8_any(TernArgs a) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const uint32_t row0 = wave * R;
+  if (row0 >= a.out) return;
+  const uint32_t tok = blockIdx.y;
+  int acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) acc[r] = 0;
+  const uint32_t *xr = a.xq + (size_t)tok * a.ng;
+  for (uint32_t j = lane; j < a.wng; j += 64) {
+    const bool valid = true;
+    uint32_t mask = 0xffffffffu;
+    const uint32_t c0 = 16 * j;
+    if (c0 + 16 > a.cols) mask = c0 >= a.cols ? 0u : ((1u << (2 * (a.cols - c0))) - 1u);
+    uint32_t x4[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) x4[k] = (valid && 4 * j + k < a.ng) ? xr[4 * j + k] : 0u;
+    uint32_t y0, y1, y2, y3;
+    xpose4(x4[0], x4[1], x4[2], x4[3], y0, y1, y2, y3);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint32_t row = row0 + r < a.out ? row0 + r : a.out - 1;
+      const uint32_t w = valid ? (a.w2[(size_t)row * a.wng + j] & mask) : 0u;
+      acc[r] = wdot(w, y0, y1, y2, y3, acc[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int tot = nlg_wave_sum_i32(acc[r]);
+    if (lane == r && row0 + r < a.out) tern_store(a, tok, row0 + r, tot);
+  }
+}
+
+// Launch geometry.  rows_per_wave in {1,2,4,8}, waves_per_block in {1,2,4}.
+static int tern_launch(const TernArgs &a, int rows_per_wave, int waves_per_block, hipStream_t st) {
+  if (!a.seq || !a.out) return NLG_OK;
+  if (a.cols > 131072) return nlg_fail("ternary linear: cols %u > 131072", a.cols);
+  const bool fast = (a.cols % 16 == 0) && (((uintptr_t)a.w2 & 15) == 0) &&
+                    (((uintptr_t)a.xq & 15) == 0);
+  const uint32_t threads = 64u * (uint32_t)waves_per_block;
+  const uint64_t rows_per_block = (uint64_t)rows_per_wave * waves_per_block;
+  dim3 blk(threads);
+#define TERN_FAST(RR, SS)                                                                     \
+  hipLaunchKernelGGL((k_tern_i8_fast<RR, SS>),                                               \
+                     dim3(nlg_blocks(a.out, rows_per_block), (a.seq + SS - 1) / SS), blk, 0, st, a)
+#define TERN_FAST_R(RR)                     \
+  do {                                      \
+    if (a.seq == 1) TERN_FAST(RR, 1);       \
+    else if (a.seq <= 2) TERN_FAST(RR, 2);  \
+    else if (a.seq <= 4) TERN_FAST(RR, 4);  \
+    else TERN_FAST(RR, 8);                  \
+  } while (0)
+#define TERN_ANY(RR) \
+  hipLaunchKernelGGL((k_tern_i8_any<RR>), dim3(nlg_blocks(a.out, rows_per_block), a.seq), blk, 0, st, a)
+  if (fast) {
+    switch (rows_per_wave) {
+      case 1: TERN_FAST_R(1); break;
+      case 2: TERN_FAST_R(2); break;
+      case 8: TERN_FAST_R(8); break;
+      default: TERN_FAST_R(4); break;
+    }
+  } else {
+    switch (rows_per_wave) {
+      case 1: TERN_ANY(1); break;
+      case 2: TERN_ANY(2); break;
+      case 8: TERN_ANY(8); break;
+      default: TERN_ANY(4); break;
+    }
+  }
+#undef TERN_FAST
+#undef TERN_FAST_R
+#undef TERN_ANY
+  NLG_LAUNCHED("ternary linear i8");
+  return NLG_OK;
+}
+
+static void tern_default_geometry(uint32_t out, uint32_t seq, int *rpw, int *wpb) {
+  // Enough waves to give every SIMD of 256 CUs work at decode shapes.
+  (void)seq;
+  *wpb = 4;
+  *rpw = out >= 4096 ? 4 : (out >= 1024 ? 2 : 1);
+}
+
+extern "C" int nlg_ternary_linear_i8_cfg(const uint32_t *xq, const float *gamma, const uint32_t *w2,
+                                         const float *bias, const float *beta, int beta_per_row,
+                                         float *y, uint32_t seq, uint32_t out, uint32_t cols,
+                                         int rows_per_wave, int waves_per_block, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (rows_per_wave != 1 && rows_per_wave != 2 && rows_per_wave != 4 && rows_per_wave != 8)
+    return nlg_fail("rows_per_wave must be 1, 2, 4 or 8");
+  if (waves_per_block < 1 || waves_per_block > 4) return nlg_fail("waves_per_block must be 1..4");
+  TernArgs a{xq, gamma, w2, bias, beta, y, seq, out, cols, (cols + 3) / 4, (cols + 15) / 16,
+             beta_per_row};
+  return tern_launch(a, rows_per_wave, waves_per_block, nlg_stream(stream));
+}
+
+extern "C" int nlg_ternary_linear_i8(const uint32_t *xq, const float *gamma, const uint32_t *w2,
+                                     const float *bias, const float *beta, int beta_per_row,
+                                     float *y, uint32_t seq, uint32_t out, uint32_t cols,
+                                     void *stream) {
+  int rpw, wpb;
+  tern_default_geometry(out, seq, &rpw, &wpb);
+  return nlg_ternary_linear_i8_cfg(xq, gamma, w2, bias, beta, beta_per_row, y, seq, out, cols, rpw,
+                                   wpb, stream);
+}
+
+// "ternary-i8" by name (an extension with no reference counterpart: the
+// composite the reference expresses as pack-act-rows + bitlinear-dp4a-1f on
+// unpacked weights).  AP WP BIAS BETA GAMMA Y; push (seq out cols).
+int L_ternary_i8(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
+  const uint32_t seq = p[0], out = p[1], cols = p[2];
+  const uint32_t ng = (cols + 3) / 4, wng = (cols + 15) / 16;
+  const uint64_t n = nlg_domain((uint64_t)seq * out, groups);
+  if (n != (uint64_t)seq * out)
+    return nlg_fail("ternary-i8: groups must cover seq*out (partial grids unsupported)");
+  const char *k = "ternary-i8";
+  if (nlg_need(b, 0, (uint64_t)seq * ng, k) || nlg_need(b, 1, (uint64_t)out * wng, k) ||
+      nlg_need(b, 2, out, k) || nlg_need(b, 3, 1, k) || nlg_need(b, 4, seq, k) ||
+      nlg_need(b, 5, (uint64_t)seq * out, k))
+    return NLG_ERR;
+  TernArgs a{(const uint32_t *)b[0].ptr, (const float *)b[4].ptr, (const uint32_t *)b[1].ptr,
+             (const float *)b[2].ptr, (const float *)b[3].ptr, (float *)b[5].ptr, seq, out, cols,
+             ng, wng, 0};
+  int rpw, wpb;
+  tern_default_geometry(out, seq, &rpw, &wpb);
+  return tern_launch(a, rpw, wpb, st);
+}
+
+// ------------------------------------------------------ int8-lane linears
+
+// bitlinear-dp4a-1f / -rows / bitlinear-dp4a: one wave per output (s, o),
+// lanes stride over the ng words; int32 sums are exact in any order.
+// CARRY: words arrive as two f32 halves lo + hi*65536 (bitlinear-dp4a).
+template <bool CARRY>
+__global__ __launch_bounds__(256) void k_dp4a_rows(const float *ap, const float *ahi, const float *wp,
+                                                   const float *whi, const float *bias, const float *beta,
+                                                   const float *gamma, float *y, uint32_t n_out,
+                                                   uint32_t out, uint32_t ng, int per_row) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t wave = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (wave >= n_out) return;
+  const uint32_t idx = (uint32_t)wave, s = idx / out, o = idx % out;
+  const uint32_t ab = s * ng, wb = o * ng;
+  int acc = 0;
+  for (uint32_t g = lane; g < ((ng + 63) & ~63u); g += 64) {
+    if (g < ng) {
+      uint32_t a_, w_;
+      if (CARRY) {
+        a_ = nlg_f2u(ap[ab + g]) + nlg_f2u(ahi[ab + g]) * 65536u;
+        w_ = nlg_f2u(wp[wb + g]) + nlg_f2u(whi[wb + g]) * 65536u;
+      } else {
+        a_ = __float_as_uint(ap[ab + g]);
+        w_ = __float_as_uint(wp[wb + g]);
+      }
+      acc = __builtin_amdgcn_sdot4((int)a_, (int)w_, acc, false);
+    }
+  }
+  acc = nlg_wave_sum_i32(acc);
+  if (lane == 0)
+    y[idx] = __fadd_rn(bias[o], __fmul_rn(__fmul_rn(beta[per_row ? o : 0], gamma[s]), (float)acc));
+}
+
+static int dp4a_common(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st,
+                       bool carry, int per_row, const char *k) {
+  const uint32_t seq = p[0], out = p[1], ng = p[2];
+  const uint64_t n = nlg_domain((uint64_t)seq * out, groups);
+  if (!n) return NLG_OK;
+  const uint64_t srows = (n + out - 1) / out;  // tokens touched
+  const int ia = 0, iw = carry ? 2 : 1, ib = carry ? 4 : 2, ibe = carry ? 5 : 3,
+            ig = carry ? 6 : 4, iy = carry ? 7 : 5;
+  if (nlg_need(b, ia, srows * ng, k) || nlg_need(b, iw, (uint64_t)out * ng, k) ||
+      nlg_need(b, ib, out, k) || nlg_need(b, ibe, per_row ? out : 1, k) ||
+      nlg_need(b, ig, srows, k) || nlg_need(b, iy, n, k))
+    return NLG_ERR;
+  if (carry && (nlg_need(b, 1, srows * ng, k) || nlg_need(b, 3, (uint64_t)out * ng, k)))
+    return NLG_ERR;
+  const float *a0 = (const float *)b[ia].ptr, *w0 = (const float *)b[iw].ptr;
+  const float *a1 = carry ? (const float *)b[1].ptr : nullptr;
+  const float *w1 = carry ? (const float *)b[3].ptr : nullptr;
+  if (carry)
+    hipLaunchKernelGGL(k_dp4a_rows<true>, dim3(nlg_blocks(n, 4)), dim3(256), 0, st, a0, a1, w0, w1,
+                       (const float *)b[ib].ptr, (const float *)b[ibe].ptr,
+                       (const float *)b[ig].ptr, (float *)b[iy].ptr, (uint32_t)n, out, ng, per_row);
+  else
+    hipLaunchKernelGGL(k_dp4a_rows<false>, dim3(nlg_blocks(n, 4)), dim3(256), 0, st, a0, a1, w0, w1,
+                       (const float *)b[ib].ptr, (const float *)b[ibe].ptr,
+                       (const float *)b[ig].ptr, (float *)b[iy].ptr, (uint32_t)n, out, ng, per_row);
+  NLG_LAUNCHED(k);
+  return NLG_OK;
+}
+
+int L_bitlinear_dp4a_1f(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
+  return dp4a_common(b, p, groups, st, false, 0, "bitlinear-dp4a-1f");
+}
+int L_bitlinear_dp4a_rows(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
+  return dp4a_common(b, p, groups, st, false, 1, "bitlinear-dp4a-rows");
+}
+int L_bitlinear_dp4a(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
+  return dp4a_common(b, p, groups, st, true, 0, "bitlinear-dp4a");
+}
+
+// dp4a-dot (kernels.el:587-600)
+__global__ void k_dp4a_dot(const float *alo, const float *ahi, const float *blo, const float *bhi,
+                           float *out, uint32_t n) {
+  uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    uint32_t a = nlg_f2u(alo[i]) + nlg_f2u(ahi[i]) * 65536u;
+    uint32_t c = nlg_f2u(blo[i]) + nlg_f2u(bhi[i]) * 65536u;
+    out[i] = (float)__builtin_amdgcn_sdot4((int)a, (int)c, 0, false);
+  }
+}
+int L_dp4a_dot(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
+  const uint64_t n = nlg_domain(p[0], groups);
+  for (int i = 0; i < 5; i++)
+    if (nlg_need(b, i, n, "dp4a-dot")) return NLG_ERR;
+  if (!n) return NLG_OK;
+  hipLaunchKernelGGL(k_dp4a_dot, dim3(nlg_blocks(n, 256)), dim3(256), 0, st, (const float *)b[0].ptr,
+                     (const float *)b[1].ptr, (const float *)b[2].ptr, (const float *)b[3].ptr,
+                     (float *)b[4].ptr, (uint32_t)n);
+  NLG_LAUNCHED("dp4a-dot");
+  return NLG_OK;
+}
+
+// ------------------------------------------------------ f32-activation linears
+
+// ternary-rows (kernels.el:700-746): f32 activations, 2-bit weights, one
+// scale per 128-column block.  One wave per output; lane-partial sums are
+// scaled per word by the word's block beta (reassociated: tolerance parity).
+__global__ __launch_bounds__(256) void k_ternary_rows(const float *x, const uint32_t *wp,
+                                                      const float *bias, const float *beta, float *y,
+                                                      uint32_t n_out, uint32_t out, uint32_t cols,
+                                                      uint32_t nblk, uint32_t wng) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t wave = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (wave >= n_out) return;
+  const uint32_t idx = (uint32_t)wave, s = idx / out, o = idx % out;
+  const float *xr = x + (size_t)s * cols;
+  const uint32_t *wr = wp + (size_t)o * wng;
+  // the reference visits words wi = b*8 + w < wng for b < nblk only
+  const uint32_t nw = wng < 8u * nblk ? wng : 8u * nblk;
+  float acc = 0.0f;
+  for (uint32_t wi = lane; wi < ((nw + 63) & ~63u); wi += 64) {
+    if (wi < nw) {
+      const uint32_t w = wr[wi];
+      float part = 0.0f;
+#pragma unroll
+      for (uint32_t f = 0; f < 16; f++) {
+        const uint32_t i = wi * 16 + f;
+        if (i < cols) {
+          const float sv = (float)((int32_t)(w << (30 - 2 * f)) >> 30);
+          part = __fadd_rn(part, __fmul_rn(sv, xr[i]));
+        }
+      }
+      acc = __fadd_rn(acc, __fmul_rn(beta[(size_t)o * nblk + wi / 8], part));
+    }
+  }
+  acc = nlg_wave_sum_f32(acc);
+  if (lane == 0) y[idx] = __fadd_rn(bias[o], acc);
+}
+
+int L_ternary_rows(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
+  const uint32_t seq = p[0], out = p[1], cols = p[2], nblk = p[3], wng = p[4];
+  const uint64_t n = nlg_domain((uint64_t)seq * out, groups);
+  if (!n) return NLG_OK;
+  const uint64_t srows = (n + out - 1) / out;
+  const uint32_t nw = wng < 8u * nblk ? wng : 8u * nblk;
+  const char *k = "ternary-rows";
+  uint64_t xneed = srows ? (srows - 1) * cols + (uint64_t)(nw * 16 < cols ? nw * 16 : cols) : 0;
+  if (nlg_need(b, 0, xneed, k) || nlg_need(b, 1, (uint64_t)(out - 1) * wng + nw, k) ||
+      nlg_need(b, 2, out, k) || nlg_need(b, 3, (uint64_t)out * nblk, k) || nlg_need(b, 4, n, k))
+    return NLG_ERR;
+  hipLaunchKernelGGL(k_ternary_rows, dim3(nlg_blocks(n, 4)), dim3(256), 0, st,
+                     (const float *)b[0].ptr, (const uint32_t *)b[1].ptr, (const float *)b[2].ptr,
+                     (const float *)b[3].ptr, (float *)b[4].ptr, (uint32_t)n, out, cols, nblk, wng);
+  NLG_LAUNCHED(k);
+  return NLG_OK;
+}
+
+// bitlinear-packed / -v (kernels.el:992-1040): base-4 codes tern+1, pk per
+// f32 value read with (uint f).  One wave per output.
+__global__ __launch_bounds__(256) void k_bitlinear_packed(const float *x, const float *wpk,
+                                                          const float *bias, const float *beta,
+                                                          float *y, uint32_t n_out, uint32_t in,
+                                                          uint32_t out, uint32_t pk, uint32_t fcount,
+                                                          int per_row) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t wave = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (wave >= n_out) return;
+  const uint32_t idx = (uint32_t)wave, s = idx / out, o = idx % out;
+  const float be = beta[per_row ? o : 0];
+  const float *xr = x + (size_t)s * in;
+  const float *wr = wpk + (size_t)o * fcount;
+  float acc = 0.0f;
+  for (uint32_t f = lane; f < ((fcount + 63) & ~63u); f += 64) {
+    if (f < fcount) {
+      uint32_t packed = nlg_f2u(wr[f]);
+      const uint32_t i0 = f * pk;
+      for (uint32_t z = 0; z < pk; z++) {
+        const uint32_t i = i0 + z;
+        if (i < in) {
+          const float tern = __fsub_rn((float)(packed % 4u), 1.0f);
+          acc = __fadd_rn(acc, __fmul_rn(xr[i], __fmul_rn(be, tern)));
+        }
+        packed = packed / 4u;
+      }
+    }
+  }
+  acc = nlg_wave_sum_f32(acc);
+  if (lane == 0) y[idx] = __fadd_rn(bias[o], acc);
+}
+
+static int packed_common(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st,
+                         int per_row, const char *k) {
+  const uint32_t seq = p[0], in = p[1], out = p[2], pk = p[3], fcount = p[4];
+  const uint64_t n = nlg_domain((uint64_t)seq * out, groups);
+  if (!n) return NLG_OK;
+  const uint64_t srows = (n + out - 1) / out;
+  uint64_t used = (uint64_t)fcount * pk < in ? (uint64_t)fcount * pk : in;
+  if (nlg_need(b, 0, srows ? (srows - 1) * in + used : 0, k) ||
+      nlg_need(b, 1, (uint64_t)out * fcount, k) || nlg_need(b, 2, out, k) ||
+      nlg_need(b, 3, per_row ? out : 1, k) || nlg_need(b, 4, n, k))
+    return NLG_ERR;
+  hipLaunchKernelGGL(k_bitlinear_packed, dim3(nlg_blocks(n, 4)), dim3(256), 0, st,
+                     (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr,
+                     (const float *)b[3].ptr, (float *)b[4].ptr, (uint32_t)n, in, out, pk, fcount,
+                     per_row);
+  NLG_LAUNCHED(k);
+  return NLG_OK;
+}
+int L_bitlinear_packed(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
+  return packed_common(b, p, groups, st, 0, "bitlinear-packed");
+}
+int L_bitlinear_packed_v(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
+  return packed_common(b, p, groups, st, 1, "bitlinear-packed-v");
+}

@@ -1,0 +1,333 @@
+"""Python binding of libnlgpu, the MI355X implementation of nelisp-gpu's
+quantized-LLM kernel path.
+
+This is a thin ctypes layer over the C ABI in include/nlgpu.h: device
+buffers, kernels by reference name (`dispatch`), the typed hot path
+(`pack_act_rows`, `ternary_linear_i8`, `softmax_rows`), events and graphs.
+It loads the in-tree ``lib/libnlgpu.so`` and raises if it is missing -- there
+is no CPU fallback anywhere in this module.
+
+It also holds the data-format helpers a caller needs: packing ternary
+weights into the reference's 2-bit layout (test/ternary-kernel-test.el:40-50,
+lisp/nelisp-gpu-kernels.el:700-746) and a seeded counter-based generator
+(SplitMix64) for reproducible synthetic inputs.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Iterable, Optional, Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libnlgpu.so")
+BIN_DIR = os.path.join(HERE, "bin")
+
+
+class NlgError(RuntimeError):
+    pass
+
+
+class Buffer(C.Structure):
+    _fields_ = [("ptr", C.c_void_p), ("nfloats", C.c_uint32)]
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded libnlgpu (raises NlgError if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise NlgError(f"{LIB_PATH} is missing: build it first (python -c "
+                       f"'import __graft_entry__; __graft_entry__.build()')")
+    L = C.CDLL(LIB_PATH)
+    vp, u32, i32, sz = C.c_void_p, C.c_uint32, C.c_int, C.c_size_t
+    f32p, u32p = C.POINTER(C.c_float), C.POINTER(C.c_uint32)
+    sigs = {
+        "nlg_init": (i32, [i32]),
+        "nlg_shutdown": (i32, []),
+        "nlg_last_error": (C.c_char_p, []),
+        "nlg_device_name": (i32, [C.c_char_p, sz]),
+        "nlg_device_info": (i32, [C.POINTER(i32), C.c_char_p, sz]),
+        "nlg_malloc": (vp, [sz]),
+        "nlg_free": (i32, [vp]),
+        "nlg_upload": (i32, [vp, vp, sz]),
+        "nlg_download": (i32, [vp, vp, sz]),
+        "nlg_copy_d2d": (i32, [vp, vp, sz, vp]),
+        "nlg_zero": (i32, [vp, sz, vp]),
+        "nlg_upload_file": (i32, [vp, C.c_char_p, C.c_uint64, sz, C.POINTER(sz)]),
+        "nlg_stream_create": (vp, []),
+        "nlg_stream_destroy": (i32, [vp]),
+        "nlg_stream_sync": (i32, [vp]),
+        "nlg_default_stream": (vp, []),
+        "nlg_event_create": (vp, []),
+        "nlg_event_destroy": (i32, [vp]),
+        "nlg_event_record": (i32, [vp, vp]),
+        "nlg_event_elapsed_ms": (i32, [vp, vp, C.POINTER(C.c_float)]),
+        "nlg_kernel_count": (i32, []),
+        "nlg_kernel_name": (C.c_char_p, [i32]),
+        "nlg_kernel_lookup": (i32, [C.c_char_p]),
+        "nlg_kernel_abi": (i32, [C.c_char_p, C.POINTER(u32), C.POINTER(u32)]),
+        "nlg_dispatch": (i32, [C.c_char_p, C.POINTER(Buffer), u32, C.POINTER(u32), u32, u32, vp]),
+        "nlg_graph_begin": (i32, [vp]),
+        "nlg_graph_end": (i32, [vp, C.POINTER(vp)]),
+        "nlg_graph_launch": (i32, [vp, vp]),
+        "nlg_graph_destroy": (i32, [vp]),
+        "nlg_pack_act_rows": (i32, [vp, vp, vp, u32, u32, vp]),
+        "nlg_ternary_linear_i8": (i32, [vp, vp, vp, vp, vp, i32, vp, u32, u32, u32, vp]),
+        "nlg_ternary_linear_i8_cfg": (i32, [vp, vp, vp, vp, vp, i32, vp, u32, u32, u32, i32, i32, vp]),
+        "nlg_softmax_rows": (i32, [vp, vp, u32, u32, vp]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name)
+        fn.restype, fn.argtypes = res, args
+    _lib = L
+    return L
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise NlgError(f"{what}: {lib().nlg_last_error().decode()}")
+
+
+def init(device: int = -1) -> None:
+    _check(lib().nlg_init(device), "nlg_init")
+
+
+def device_name() -> str:
+    b = C.create_string_buffer(256)
+    _check(lib().nlg_device_name(b, 256), "nlg_device_name")
+    return b.value.decode()
+
+
+def device_info() -> tuple[int, str]:
+    n = C.c_int(0)
+    b = C.create_string_buffer(64)
+    _check(lib().nlg_device_info(C.byref(n), b, 64), "nlg_device_info")
+    return n.value, b.value.decode()
+
+
+# ------------------------------------------------------------------ memory
+
+class DeviceArray:
+    """A device allocation of `nbytes`; element count in 4-byte slots is
+    what kernels by name see (the reference's float count)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = lib().nlg_malloc(max(self.nbytes, 4))
+        if not p:
+            raise NlgError(f"nlg_malloc({nbytes}): {lib().nlg_last_error().decode()}")
+        self.ptr = p
+
+    @property
+    def nfloats(self) -> int:
+        return self.nbytes // 4
+
+    def upload(self, arr: np.ndarray, offset: int = 0) -> "DeviceArray":
+        a = np.ascontiguousarray(arr)
+        if offset + a.nbytes > self.nbytes:
+            raise NlgError("upload past the end of the buffer")
+        _check(lib().nlg_upload(self.ptr + offset, a.ctypes.data, a.nbytes), "nlg_upload")
+        return self
+
+    def download(self, dtype=np.float32, count: Optional[int] = None, offset: int = 0) -> np.ndarray:
+        dt = np.dtype(dtype)
+        n = (self.nbytes - offset) // dt.itemsize if count is None else int(count)
+        out = np.empty(n, dtype=dt)
+        _check(lib().nlg_download(out.ctypes.data, self.ptr + offset, out.nbytes), "nlg_download")
+        return out
+
+    def zero(self, stream=None) -> None:
+        _check(lib().nlg_zero(self.ptr, self.nbytes, stream), "nlg_zero")
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().nlg_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def as_buffer(self, nfloats: Optional[int] = None) -> Buffer:
+        return Buffer(self.ptr, self.nfloats if nfloats is None else int(nfloats))
+
+
+def to_device(arr: np.ndarray) -> DeviceArray:
+    a = np.ascontiguousarray(arr)
+    return DeviceArray(a.nbytes).upload(a)
+
+
+def sync(stream=None) -> None:
+    _check(lib().nlg_stream_sync(stream), "nlg_stream_sync")
+
+
+# ------------------------------------------------------------------ kernels
+
+def kernel_names() -> list[str]:
+    L = lib()
+    return [L.nlg_kernel_name(i).decode() for i in range(L.nlg_kernel_count())]
+
+
+def kernel_abi(name: str) -> tuple[int, int]:
+    nb, npu = C.c_uint32(0), C.c_uint32(0)
+    _check(lib().nlg_kernel_abi(name.encode(), C.byref(nb), C.byref(npu)), "nlg_kernel_abi")
+    return nb.value, npu.value
+
+
+def dispatch(name: str, bufs: Sequence, push: Iterable[int], groups: int, stream=None,
+             check: bool = True) -> int:
+    """Run kernel `name` (reference ABI).  bufs: DeviceArray or (DeviceArray, nfloats)."""
+    arr = (Buffer * max(len(bufs), 1))()
+    for i, b in enumerate(bufs):
+        if isinstance(b, tuple):
+            arr[i] = b[0].as_buffer(b[1])
+        else:
+            arr[i] = b.as_buffer()
+    pv = [int(p) & 0xFFFFFFFF for p in push]
+    parr = (C.c_uint32 * max(len(pv), 1))(*pv)
+    rc = lib().nlg_dispatch(name.encode(), arr, len(bufs), parr, len(pv), int(groups), stream)
+    if check:
+        _check(rc, f"dispatch {name}")
+    return rc
+
+
+def last_error() -> str:
+    return lib().nlg_last_error().decode()
+
+
+def pack_act_rows(x: DeviceArray, xq: DeviceArray, gamma: DeviceArray, seq: int, cols: int,
+                  stream=None) -> None:
+    _check(lib().nlg_pack_act_rows(x.ptr, xq.ptr, gamma.ptr, seq, cols, stream), "pack_act_rows")
+
+
+def ternary_linear_i8(xq, gamma, w2, bias, beta, y, seq, out, cols, beta_per_row=False,
+                      stream=None, rows_per_wave: int = 0, waves_per_block: int = 0) -> None:
+    L = lib()
+    bp = bias.ptr if bias is not None else None
+    if rows_per_wave:
+        rc = L.nlg_ternary_linear_i8_cfg(xq.ptr, gamma.ptr, w2.ptr, bp, beta.ptr, int(beta_per_row),
+                                         y.ptr, seq, out, cols, rows_per_wave, waves_per_block or 4,
+                                         stream)
+    else:
+        rc = L.nlg_ternary_linear_i8(xq.ptr, gamma.ptr, w2.ptr, bp, beta.ptr, int(beta_per_row),
+                                     y.ptr, seq, out, cols, stream)
+    _check(rc, "ternary_linear_i8")
+
+
+def softmax_rows(a: DeviceArray, c: DeviceArray, rows: int, cols: int, stream=None) -> None:
+    _check(lib().nlg_softmax_rows(a.ptr, c.ptr, rows, cols, stream), "softmax_rows")
+
+
+# ------------------------------------------------------------- events, graphs
+
+class Event:
+    def __init__(self):
+        self.ev = lib().nlg_event_create()
+        if not self.ev:
+            raise NlgError(last_error())
+
+    def record(self, stream=None) -> None:
+        _check(lib().nlg_event_record(self.ev, stream), "event_record")
+
+    def elapsed_ms(self, later: "Event") -> float:
+        ms = C.c_float(0)
+        _check(lib().nlg_event_elapsed_ms(self.ev, later.ev, C.byref(ms)), "event_elapsed")
+        return ms.value
+
+    def __del__(self):
+        try:
+            lib().nlg_event_destroy(self.ev)
+        except Exception:
+            pass
+
+
+def graph_begin(stream=None) -> None:
+    _check(lib().nlg_graph_begin(stream), "graph_begin")
+
+
+def graph_end(stream=None):
+    g = C.c_void_p()
+    _check(lib().nlg_graph_end(stream, C.byref(g)), "graph_end")
+    return g.value
+
+
+def graph_launch(g, stream=None) -> None:
+    _check(lib().nlg_graph_launch(g, stream), "graph_launch")
+
+
+def graph_destroy(g) -> None:
+    lib().nlg_graph_destroy(g)
+
+
+# ------------------------------------------------------------- data formats
+
+def pack_ternary(trits: np.ndarray) -> np.ndarray:
+    """Pack an [out, cols] array of {-1,0,+1} (or -2) into the reference's
+    2-bit words: 16 fields per u32, field f in bits 2f..2f+1, codes
+    +1 -> 01, -1 -> 11, 0 -> 00, -2 -> 10 (test/ternary-kernel-test.el:40-50).
+    Returns uint32 [out, ceil(cols/16)]."""
+    t = np.asarray(trits)
+    out, cols = t.shape
+    wng = (cols + 15) // 16
+    codes = np.zeros((out, wng * 16), dtype=np.uint32)
+    codes[:, :cols] = (t.astype(np.int64) & 3).astype(np.uint32)
+    codes = codes.reshape(out, wng, 16)
+    shifts = (2 * np.arange(16, dtype=np.uint32))
+    return np.bitwise_or.reduce(codes << shifts, axis=2).astype(np.uint32)
+
+
+def unpack_ternary(words: np.ndarray, cols: int) -> np.ndarray:
+    """Inverse of pack_ternary, decoding by sign extension as ternary-rows
+    does (lisp/nelisp-gpu-kernels.el:728-743): 00 0, 01 +1, 11 -1, 10 -2."""
+    w = np.asarray(words, dtype=np.uint32)
+    out, wng = w.shape
+    f = np.arange(16, dtype=np.uint32)
+    codes = (w[:, :, None] >> (2 * f)) & 3
+    vals = np.where(codes >= 2, codes.astype(np.int64) - 4, codes.astype(np.int64)).astype(np.int8)
+    return vals.reshape(out, wng * 16)[:, :cols]
+
+
+_M64 = (1 << 64) - 1
+
+
+def splitmix64(seed: int, n: int) -> np.ndarray:
+    """n outputs of SplitMix64 with state seed + (i+1)*golden (counter-based,
+    so any slice is reproducible independently)."""
+    with np.errstate(over="ignore"):
+        i = np.arange(1, n + 1, dtype=np.uint64)
+        z = np.uint64(seed & _M64) + i * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def uniform(seed: int, n: int) -> np.ndarray:
+    """float64 in [0, 1) from the top 53 bits."""
+    return (splitmix64(seed, n) >> np.uint64(11)).astype(np.float64) * (1.0 / (1 << 53))
+
+
+def normal(seed: int, n: int, sigma: float = 1.0) -> np.ndarray:
+    """float32 N(0, sigma^2) by Box-Muller in double."""
+    m = (n + 1) // 2
+    u = uniform(seed, 2 * m)
+    u1 = 1.0 - u[:m]  # (0, 1]
+    u2 = u[m:]
+    r = np.sqrt(-2.0 * np.log(u1))
+    z = np.concatenate([r * np.cos(2 * np.pi * u2), r * np.sin(2 * np.pi * u2)])[:n]
+    return (sigma * z).astype(np.float32)
+
+
+def trits(seed: int, shape) -> np.ndarray:
+    """{-1, 0, +1} with probabilities {0.25, 0.5, 0.25}."""
+    n = int(np.prod(shape))
+    u = uniform(seed, n)
+    t = np.where(u < 0.25, -1, np.where(u < 0.75, 0, 1)).astype(np.int8)
+    return t.reshape(shape)

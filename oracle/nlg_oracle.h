@@ -1,0 +1,61 @@
+/* nlg_oracle.h -- CPU restatement of nelisp-gpu's hot-path kernels.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the
+ * MI355X kernels and the CPU baseline timed by bench.py; it is never linked
+ * into, loaded by, or called from the product library (libnlgpu) or the CLI
+ * hosts.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it.
+ *
+ * Each kernel is restated from its DSL body in lisp/nelisp-gpu-kernels.el
+ * (line cited per function in nlg_oracle.c), following the op semantics of
+ * lisp/nelisp-gpu-compile.el: uint arithmetic wraps mod 2^32, integer
+ * compares are unsigned, float ops are single IEEE operations evaluated in
+ * the body's order with no contraction (built with -ffp-contract=off),
+ * `(uint f)` truncates toward zero, and every float reduction is serial in
+ * index order.  Buffer access is robust: a read past a buffer's end gives 0
+ * and a write past it is dropped (Vulkan robustBufferAccess), so a malformed
+ * request can never crash the checker.
+ */
+#ifndef NLG_ORACLE_H
+#define NLG_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Run kernel `name` over `groups` workgroups of 64 invocations (256 for
+ * matmul-tiled), exactly as its DSL body would.  bufs[i] has sizes[i]
+ * 4-byte elements.  Returns 0, or 1 for an unknown name or a wrong number of
+ * buffers/push constants. */
+int or_dispatch(const char *name, float **bufs, const uint32_t *sizes, uint32_t nbuf,
+                const uint32_t *push, uint32_t npush, uint32_t groups);
+int or_kernel_count(void);
+const char *or_kernel_name(int i);
+int or_kernel_abi(const char *name, uint32_t *nbuf, uint32_t *npush);
+
+/* The composite ternary x int8 linear (see nlgpu.h nlg_ternary_linear_i8):
+ * 2-bit fields unpacked to int8 lanes, then bitlinear-dp4a-1f's int32 sdot
+ * accumulation and fp32 epilogue.  bias may be NULL. */
+void or_ternary_linear_i8(const uint32_t *xq, const float *gamma, const uint32_t *w2,
+                          const float *bias, const float *beta, int beta_per_row, float *y,
+                          uint32_t seq, uint32_t out, uint32_t cols);
+/* Same, returning the exact int32 accumulators instead of y. */
+void or_ternary_acc_i8(const uint32_t *xq, const uint32_t *w2, int32_t *acc, uint32_t seq,
+                       uint32_t out, uint32_t cols);
+/* pack-act-rows over `seq` rows of `cols` (kernels.el:884-932). */
+void or_pack_act_rows(const float *x, uint32_t *xq, float *gamma, uint32_t seq, uint32_t cols);
+/* softmax over rows (kernels.el:28-42); c may equal a. */
+void or_softmax_rows(const float *a, float *c, uint32_t rows, uint32_t cols);
+
+/* Number of OpenMP threads the parallel loops use (1 when built without
+ * OpenMP); set_threads(0) keeps the runtime default. */
+int or_threads(void);
+void or_set_threads(int n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

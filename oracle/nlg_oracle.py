@@ -1,0 +1,124 @@
+"""ctypes binding of the CPU restatement (libnlg_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: the checker the MI355X kernels are compared with,
+and the CPU baseline bench.py times.  Only tests/, __graft_entry__.smoke()
+and bench.py's cpu_baseline leg import this module; the product library and
+hosts never load it.  See nlg_oracle.c for the per-kernel citations of
+lisp/nelisp-gpu-kernels.el.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libnlg_oracle.so")
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+        L = C.CDLL(LIB_PATH)
+        vp, u32, i32 = C.c_void_p, C.c_uint32, C.c_int
+        L.or_dispatch.restype = i32
+        L.or_dispatch.argtypes = [C.c_char_p, C.POINTER(C.c_void_p), C.POINTER(u32), u32,
+                                  C.POINTER(u32), u32, u32]
+        L.or_kernel_count.restype = i32
+        L.or_kernel_name.restype = C.c_char_p
+        L.or_kernel_name.argtypes = [i32]
+        L.or_kernel_abi.restype = i32
+        L.or_kernel_abi.argtypes = [C.c_char_p, C.POINTER(u32), C.POINTER(u32)]
+        L.or_ternary_linear_i8.restype = None
+        L.or_ternary_linear_i8.argtypes = [vp, vp, vp, vp, vp, i32, vp, u32, u32, u32]
+        L.or_ternary_acc_i8.restype = None
+        L.or_ternary_acc_i8.argtypes = [vp, vp, vp, u32, u32, u32]
+        L.or_pack_act_rows.restype = None
+        L.or_pack_act_rows.argtypes = [vp, vp, vp, u32, u32]
+        L.or_softmax_rows.restype = None
+        L.or_softmax_rows.argtypes = [vp, vp, u32, u32]
+        L.or_threads.restype = i32
+        L.or_set_threads.argtypes = [i32]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data if a is not None else None
+
+
+def kernel_names() -> list[str]:
+    L = lib()
+    return [L.or_kernel_name(i).decode() for i in range(L.or_kernel_count())]
+
+
+def kernel_abi(name: str) -> tuple[int, int]:
+    nb, npu = C.c_uint32(0), C.c_uint32(0)
+    if lib().or_kernel_abi(name.encode(), C.byref(nb), C.byref(npu)):
+        raise KeyError(name)
+    return nb.value, npu.value
+
+
+def dispatch(name: str, bufs: Sequence[np.ndarray], push: Sequence[int], groups: int) -> None:
+    """Run kernel `name` over numpy buffers in place.  Each buffer must be a
+    C-contiguous 4-byte-element array (float32 or uint32 views); the same
+    array may appear twice (in-place kernels)."""
+    n = len(bufs)
+    ptrs = (C.c_void_p * max(n, 1))()
+    sizes = (C.c_uint32 * max(n, 1))()
+    for i, b in enumerate(bufs):
+        assert b.flags["C_CONTIGUOUS"] and b.dtype.itemsize == 4, (name, i)
+        ptrs[i] = b.ctypes.data
+        sizes[i] = b.size
+    pv = [int(p) & 0xFFFFFFFF for p in push]
+    parr = (C.c_uint32 * max(len(pv), 1))(*pv)
+    if lib().or_dispatch(name.encode(), ptrs, sizes, n, parr, len(pv), int(groups)):
+        raise ValueError(f"oracle: bad dispatch {name}")
+
+
+def pack_act_rows(x: np.ndarray, seq: int, cols: int):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ng = (cols + 3) // 4
+    xq = np.zeros(seq * ng, dtype=np.uint32)
+    gamma = np.zeros(seq, dtype=np.float32)
+    lib().or_pack_act_rows(_p(x), _p(xq), _p(gamma), seq, cols)
+    return xq, gamma
+
+
+def ternary_acc_i8(xq: np.ndarray, w2: np.ndarray, seq: int, out: int, cols: int) -> np.ndarray:
+    acc = np.zeros(seq * out, dtype=np.int32)
+    lib().or_ternary_acc_i8(_p(np.ascontiguousarray(xq, np.uint32)),
+                            _p(np.ascontiguousarray(w2, np.uint32)), _p(acc), seq, out, cols)
+    return acc
+
+
+def ternary_linear_i8(xq, gamma, w2, bias, beta, seq, out, cols, beta_per_row=False) -> np.ndarray:
+    y = np.zeros(seq * out, dtype=np.float32)
+    b = np.ascontiguousarray(bias, np.float32) if bias is not None else None
+    lib().or_ternary_linear_i8(_p(np.ascontiguousarray(xq, np.uint32)),
+                               _p(np.ascontiguousarray(gamma, np.float32)),
+                               _p(np.ascontiguousarray(w2, np.uint32)), _p(b),
+                               _p(np.ascontiguousarray(beta, np.float32)), int(beta_per_row),
+                               _p(y), seq, out, cols)
+    return y
+
+
+def softmax_rows(a: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    c = np.empty_like(a)
+    lib().or_softmax_rows(_p(a), _p(c), rows, cols)
+    return c
+
+
+def threads() -> int:
+    return lib().or_threads()
+
+
+def set_threads(n: int) -> None:
+    lib().or_set_threads(n)

@@ -1,0 +1,99 @@
+"""The decode hot path on the MI355X: pack-act-rows quantisation and the
+2-bit x int8 ternary linear, bit-exact against the CPU restatement (exact
+int32 accumulators and the same IEEE epilogue), at the BASELINE shapes
+(4096 x 4096 decode GEMV; the 2560/6912 SwiGLU projections at B = 1 and
+16) and at ragged edges (cols not a multiple of 16 or 4, one row, one
+column), for every launch geometry."""
+import numpy as np
+import pytest
+
+import nlg_oracle as orc
+import nlgpu
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    nlgpu.init()
+    yield
+
+
+def make(seed, seq, out, cols, per_row=False):
+    t = nlgpu.trits(seed, (out, cols))
+    w2 = nlgpu.pack_ternary(t)
+    x = nlgpu.normal(seed + 1, seq * cols)
+    bias = nlgpu.normal(seed + 2, out) * np.float32(0.1)
+    beta = (np.abs(nlgpu.normal(seed + 3, out if per_row else 1)) * np.float32(0.05)).astype(np.float32)
+    return t, w2, x, bias, beta
+
+
+SHAPES = [(1, 4096, 4096), (1, 6912, 2560), (1, 2560, 6912), (16, 6912, 2560), (16, 2560, 6912),
+          (3, 37, 300), (1, 100, 1000), (2, 33, 4100), (5, 64, 16), (1, 1, 64), (4, 7, 1), (1, 5, 17),
+          (9, 130, 2048)]
+
+
+@pytest.mark.parametrize("seq,out,cols", SHAPES)
+def test_pack_and_ternary_linear_bit_exact(seq, out, cols):
+    print(f"[gpu] ternary seq={seq} out={out} cols={cols}", flush=True)
+    t, w2, x, bias, beta = make(seq * 7 + cols, seq, out, cols)
+    ng = (cols + 3) // 4
+    dx = nlgpu.to_device(x)
+    dxq = nlgpu.DeviceArray(seq * ng * 4)
+    dg = nlgpu.DeviceArray(seq * 4)
+    nlgpu.pack_act_rows(dx, dxq, dg, seq, cols)
+    xq_ref, g_ref = orc.pack_act_rows(x, seq, cols)
+    nlgpu.sync()
+    assert np.array_equal(dxq.download(np.uint32, seq * ng), xq_ref)
+    assert np.array_equal(dg.download(np.float32, seq).view(np.uint32), g_ref.view(np.uint32))
+    dw, db, dbe = nlgpu.to_device(w2), nlgpu.to_device(bias), nlgpu.to_device(beta)
+    dy = nlgpu.DeviceArray(seq * out * 4)
+    nlgpu.ternary_linear_i8(dxq, dg, dw, db, dbe, dy, seq, out, cols)
+    y = dy.download(np.float32, seq * out)
+    y_ref = orc.ternary_linear_i8(xq_ref, g_ref, w2, bias, beta, seq, out, cols)
+    bad = np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} outputs differ, first {bad[:5]}: {y[bad[:3]]} vs {y_ref[bad[:3]]}"
+
+
+@pytest.mark.parametrize("rpw", [1, 2, 4, 8])
+@pytest.mark.parametrize("wpb", [1, 2, 4])
+def test_every_launch_geometry_gives_the_same_bits(rpw, wpb):
+    seq, out, cols = 2, 1027, 2560
+    t, w2, x, bias, beta = make(99, seq, out, cols, per_row=True)
+    xq, g = orc.pack_act_rows(x, seq, cols)
+    y_ref = orc.ternary_linear_i8(xq, g, w2, None, beta, seq, out, cols, beta_per_row=True)
+    dy = nlgpu.DeviceArray(seq * out * 4)
+    nlgpu.ternary_linear_i8(nlgpu.to_device(xq), nlgpu.to_device(g), nlgpu.to_device(w2), None,
+                            nlgpu.to_device(beta), dy, seq, out, cols, beta_per_row=True,
+                            rows_per_wave=rpw, waves_per_block=wpb)
+    assert np.array_equal(dy.download(np.float32, seq * out).view(np.uint32), y_ref.view(np.uint32))
+
+
+def test_named_ternary_i8_matches_typed_entry():
+    seq, out, cols = 3, 300, 1024
+    t, w2, x, bias, beta = make(5, seq, out, cols)
+    xq, g = orc.pack_act_rows(x, seq, cols)
+    y_ref = orc.ternary_linear_i8(xq, g, w2, bias, beta, seq, out, cols)
+    dy = nlgpu.DeviceArray(seq * out * 4)
+    bufs = [nlgpu.to_device(xq), nlgpu.to_device(w2), nlgpu.to_device(bias), nlgpu.to_device(beta),
+            nlgpu.to_device(g), dy]
+    nlgpu.dispatch("ternary-i8", bufs, [seq, out, cols], (seq * out + 63) // 64)
+    assert np.array_equal(dy.download(np.float32, seq * out).view(np.uint32), y_ref.view(np.uint32))
+
+
+def test_int32_accumulator_extremes():
+    # every weight -2 (code 10) against x = +-127 lanes: the largest partial sums
+    seq, out, cols = 2, 64, 8192
+    t = np.full((out, cols), -2, np.int8)
+    t[1::2, ::3] = 1
+    w2 = nlgpu.pack_ternary(t)
+    x = np.full(seq * cols, 5.0, np.float32)
+    x[cols:] = -5.0  # second token all -127 lanes
+    xq, g = orc.pack_act_rows(x, seq, cols)
+    acc = orc.ternary_acc_i8(xq, w2, seq, out, cols)
+    assert np.abs(acc).max() > 100000
+    y_ref = orc.ternary_linear_i8(xq, g, w2, None, np.array([1.0], np.float32), seq, out, cols)
+    dy = nlgpu.DeviceArray(seq * out * 4)
+    nlgpu.ternary_linear_i8(nlgpu.to_device(xq), nlgpu.to_device(g), nlgpu.to_device(w2), None,
+                            nlgpu.to_device(np.array([1.0], np.float32)), dy, seq, out, cols)
+    assert np.array_equal(dy.download(np.float32, seq * out).view(np.uint32), y_ref.view(np.uint32))
