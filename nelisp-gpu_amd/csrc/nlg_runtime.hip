@@ -78,9 +78,13 @@ extern "C" int nlg_shutdown(void) {
 
 extern "C" int nlg_device_name(char *buf, size_t len) {
   if (nlg_ensure_init()) return NLG_ERR;
-  hipDeviceProp_t prop;
-  NLG_HIP(hipGetDeviceProperties(&prop, g_device));
-  snprintf(buf, len, "%s", prop.name);
+  char name[256] = {0};
+  if (hipDeviceGetName(name, sizeof name, g_device) != hipSuccess || !name[0]) {
+    hipDeviceProp_t prop;
+    NLG_HIP(hipGetDeviceProperties(&prop, g_device));
+    snprintf(name, sizeof name, "%s", prop.name[0] ? prop.name : prop.gcnArchName);
+  }
+  snprintf(buf, len, "%s", name);
   return NLG_OK;
 }
 

@@ -210,8 +210,8 @@ __device__ __forceinline__ void tern_store(const TernArgs &a, uint32_t s, uint32
   a.y[(size_t)s * a.out + o] = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, a.gamma[s]), acc));
 }
 
-// FAST path: cols % 16 == 0 (so rows are whole 16-byte chunks and the
-// activation rows are 16-byte aligned).  R rows per wave, ST tokens per block
+// FAST path: cols % 64 == 0, so every row is a whole number of 16-byte
+// chunks (4 words = 64 weights) and every activation row is 16-byte aligned.  R rows per wave, ST tokens per block
 // (blockIdx.y picks the token tile).
 template <int R, int ST>
 __global__ __launch_bounds__(256) void k_tern_i8_fast(TernArgs a) {
@@ -314,7 +314,7 @@ __global__ __launch_bounds__(256) void k_tern_i8_any(TernArgs a) {
 static int tern_launch(const TernArgs &a, int rows_per_wave, int waves_per_block, hipStream_t st) {
   if (!a.seq || !a.out) return NLG_OK;
   if (a.cols > 131072) return nlg_fail("ternary linear: cols %u > 131072", a.cols);
-  const bool fast = (a.cols % 16 == 0) && (((uintptr_t)a.w2 & 15) == 0) &&
+  const bool fast = (a.cols % 64 == 0) && (((uintptr_t)a.w2 & 15) == 0) &&
                     (((uintptr_t)a.xq & 15) == 0);
   const uint32_t threads = 64u * (uint32_t)waves_per_block;
   const uint64_t rows_per_block = (uint64_t)rows_per_wave * waves_per_block;
