@@ -4,19 +4,25 @@ Workload: the ternary decode GEMV, W[4096 x 4096]
 with trits {-1,0,+1} at p = {.25,.5,.25} packed 2 bits/weight row-major, one
 fp32 per-tensor scale, x[4096] f32 ~ N(0,1) quantised to int8 by per-token
 absmax, int32 accumulation, fp32 rescale, batch 1.  A step is one pass of
-the path: pack-act-rows(x) then the GEMV, on the next of 128 distinct weight
-copies (512 MiB, twice the 256 MB Infinity Cache, so weights stream from HBM).
+the path -- quantise x, then the GEMV -- on the next of 128 distinct weight
+copies (512 MiB, twice the 256 MB Infinity Cache, so weights come from HBM).
+The step is one kernel launch (nlg_ternary_linear: quantisation fused into
+the GEMV).
 
-value = algorithmic bytes of a step (4,227,076 B: packed W, f32 x, beta, f32 y)
-      / measured step time, in GB/s.  The roofline object is for the GEMV
-kernel alone (4,214,792 B per launch: W, int8 x, gamma, beta, y) over its
-average launch duration, measured with HIP events on the stream the kernels
-run on.  cpu_baseline is the CPU restatement (oracle/) of the same step on
-the host cores.
+value    = algorithmic bytes of a step (4,227,076 B: packed W 4 MiB, f32 x,
+           beta, f32 y) / measured step time, GB/s.
+roofline = the same kernel (the only one in the step): those bytes over its
+           average launch duration from HIP events on the stream it runs on.
+Extra fields: the GEMV alone on pre-quantised int8 x (4,214,792 B/launch),
+the same GEMV kernel over all 128 copies stacked into one [524288 x 4096]
+launch (launch cost amortised: the kernel's streaming rate), and the
+measured launch floor (an empty kernel, back to back).
+cpu_baseline: the CPU restatement (oracle/) of the same step on host cores.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep]
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -35,7 +41,29 @@ GEMV_BYTES = OUT * COLS // 4 + COLS + 4 + 4 + OUT * 4          # 4,214,792
 METRIC = "ternary GEMV GB/s (% HBM peak) at 4096²; decode tok/s, 2B ternary model, batch 1"
 
 
-def gpu_bench(steps: int, warmup: int):
+def timed(fn, n, stream):
+    """Average ms per call of fn(i) for i in 0..n-1.  The calls are captured
+    into a HIP graph of COPIES launches (one pass over the rotating weight
+    copies) replayed n/COPIES times between two events, so host-side launch
+    overhead (Python, ctypes, hipLaunchKernel) is not what gets measured."""
+    import nlgpu
+    nlgpu.graph_begin(stream)
+    for i in range(COPIES):
+        fn(i)
+    g = nlgpu.graph_end(stream)
+    reps = max(1, n // COPIES)
+    nlgpu.graph_launch(g, stream)  # warm replay
+    e0, e1 = nlgpu.Event(), nlgpu.Event()
+    e0.record(stream)
+    for _ in range(reps):
+        nlgpu.graph_launch(g, stream)
+    e1.record(stream)
+    ms = e0.elapsed_ms(e1) / (reps * COPIES)
+    nlgpu.graph_destroy(g)
+    return ms
+
+
+def gpu_bench(steps: int, warmup: int, sweep: bool):
     import nlgpu
 
     nlgpu.init()
@@ -43,8 +71,7 @@ def gpu_bench(steps: int, warmup: int):
     t = nlgpu.trits(seed, (OUT, COLS))
     w_one = nlgpu.pack_ternary(t)
     wbytes = w_one.nbytes
-    # 128 distinct copies: each row set is the same trits rotated by copy index
-    # (different bytes per copy, same statistics)
+    # 128 distinct copies: the same trits with rows rotated per copy
     dW = nlgpu.DeviceArray(wbytes * COPIES)
     for c in range(COPIES):
         dW.upload(np.roll(w_one, c, axis=0), offset=c * wbytes)
@@ -54,36 +81,64 @@ def gpu_bench(steps: int, warmup: int):
     dxq = nlgpu.DeviceArray(COLS)
     dg = nlgpu.DeviceArray(4)
     dy = nlgpu.DeviceArray(OUT * 4)
+    dY = nlgpu.DeviceArray(OUT * COPIES * 4)
     L = nlgpu.lib()
     stream = L.nlg_default_stream()
+    res = dict(device=nlgpu.device_name(), x=x, w_one=w_one)
 
     def w_ptr(i):
         return dW.ptr + (i % COPIES) * wbytes
 
-    def step(i):
-        L.nlg_pack_act_rows(dx.ptr, dxq.ptr, dg.ptr, 1, COLS, stream)
-        L.nlg_ternary_linear_i8(dxq.ptr, dg.ptr, w_ptr(i), None, dbeta.ptr, 0, dy.ptr, 1, OUT, COLS, stream)
+    def step(i, rpw=0):
+        rc = L.nlg_ternary_linear_cfg(dx.ptr, w_ptr(i), None, dbeta.ptr, 0, dy.ptr, None, 1, OUT, COLS,
+                                      rpw, None, 0, stream)
+        if rc:
+            raise nlgpu.NlgError(nlgpu.last_error())
 
+    def gemv(i, rpw=4, wpb=4):
+        L.nlg_ternary_linear_i8_cfg(dxq.ptr, dg.ptr, w_ptr(i), None, dbeta.ptr, 0, dy.ptr, 1, OUT, COLS,
+                                    rpw, wpb, stream)
+
+    L.nlg_pack_act_rows(dx.ptr, dxq.ptr, dg.ptr, 1, COLS, stream)
     for i in range(warmup):
         step(i)
     nlgpu.sync()
+    res["step_ms"] = timed(step, steps, stream)
+    nlgpu.sync()
+    for i in range(warmup):
+        gemv(i)
+    res["gemv_ms"] = timed(gemv, steps, stream)
+    nlgpu.sync()
+    # one launch over all copies stacked: [COPIES*OUT x COLS]
+    stacked = lambda i: L.nlg_ternary_linear_i8_cfg(dxq.ptr, dg.ptr, dW.ptr, None, dbeta.ptr, 0, dY.ptr, 1,
+                                                    OUT * COPIES, COLS, 4, 4, stream)
+    stacked(0)
+    nlgpu.sync()
     e0, e1 = nlgpu.Event(), nlgpu.Event()
     e0.record(stream)
-    for i in range(steps):
-        step(i)
+    for i in range(20):
+        stacked(i)
     e1.record(stream)
-    step_ms = e0.elapsed_ms(e1) / steps
-
-    # the GEMV kernel alone: back-to-back launches over the rotating copies
+    res["stacked_ms"] = e0.elapsed_ms(e1) / 20
     nlgpu.sync()
-    g0, g1 = nlgpu.Event(), nlgpu.Event()
-    g0.record(stream)
-    for i in range(steps):
-        L.nlg_ternary_linear_i8(dxq.ptr, dg.ptr, w_ptr(i), None, dbeta.ptr, 0, dy.ptr, 1, OUT, COLS, stream)
-    g1.record(stream)
-    gemv_ms = g0.elapsed_ms(g1) / steps
+    # launch floor: an empty fill of 16 bytes, back to back
+    res["floor_ms"] = timed(lambda i: L.nlg_zero(dg.ptr, 4, stream), steps, stream)
     nlgpu.sync()
-    return dict(step_ms=step_ms, gemv_ms=gemv_ms, device=nlgpu.device_name(), x=x, w_one=w_one)
+    if sweep:
+        sw = {}
+        for rpw in (1, 2, 4):
+            for i in range(warmup):
+                step(i, rpw)
+            sw[f"fused rpw={rpw}"] = round(timed(lambda i: step(i, rpw), steps, stream) * 1e3, 3)
+        for rpw in (1, 2, 4, 8):
+            for wpb in (1, 2, 4):
+                f = lambda i: gemv(i, rpw, wpb)
+                for i in range(warmup):
+                    f(i)
+                sw[f"i8 rpw={rpw} wpb={wpb}"] = round(timed(f, steps, stream) * 1e3, 3)
+        res["sweep_us"] = sw
+    nlgpu.sync()
+    return res
 
 
 def cpu_baseline(x, w_one, seconds: float):
@@ -100,8 +155,8 @@ def cpu_baseline(x, w_one, seconds: float):
         if dt >= seconds:
             break
     return dict(value=round(STEP_BYTES * n / dt / 1e9, 3), unit="GB/s", cores=orc.threads(), kind="port",
-                sample=f"{n} steps of the 4096x4096 config-2 step (pack-act-rows + ternary GEMV, "
-                       f"C restatement, OpenMP over output rows) in {dt:.1f} s")
+                sample=f"{n} steps of the 4096x4096 config-2 step (pack-act-rows + ternary GEMV, C "
+                       f"restatement of the reference kernels, OpenMP over output rows) in {dt:.1f} s")
 
 
 def main():
@@ -110,14 +165,16 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--sweep", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the decode path is not sharded); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
-    r = gpu_bench(args.steps, args.warmup)
+    r = gpu_bench(args.steps, args.warmup, args.sweep)
     value = STEP_BYTES / (r["step_ms"] * 1e-3) / 1e9
-    achieved = GEMV_BYTES / (r["gemv_ms"] * 1e-3) / 1e9
+    gemv_gbs = GEMV_BYTES / (r["gemv_ms"] * 1e-3) / 1e9
+    stacked_gbs = GEMV_BYTES * COPIES / (r["stacked_ms"] * 1e-3) / 1e9
     cpu = cpu_baseline(r["x"], r["w_one"], args.cpu_seconds)
     out = {
         "metric": METRIC,
@@ -135,14 +192,21 @@ def main():
         "config": {"workload": "ternary decode GEMV W[4096x4096] 2-bit, x f32 -> int8 absmax, batch 1, "
                                "128 rotated weight copies (512 MiB)",
                    "out": OUT, "cols": COLS, "batch": 1, "weight_copies": COPIES,
-                   "step": "pack-act-rows + ternary GEMV"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_tern_i8_fast<4,1>", "bytes_per_launch": GEMV_BYTES,
-                     "us_per_launch": round(r["gemv_ms"] * 1e3, 3)},
+                   "step": "one launch: pack-act-rows quantisation fused into the ternary GEMV"},
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_tern_fused", "bytes_per_launch": STEP_BYTES,
+                     "us_per_launch": round(r["step_ms"] * 1e3, 3)},
+        "gemv_prequantised": {"gbs": round(gemv_gbs, 2), "us_per_launch": round(r["gemv_ms"] * 1e3, 3),
+                              "bytes_per_launch": GEMV_BYTES, "kernel": "k_tern_i8_fast"},
+        "gemv_stacked_one_launch": {"gbs": round(stacked_gbs, 2), "frac": round(stacked_gbs / HBM_PEAK_GBS, 4),
+                                    "rows": OUT * COPIES, "ms": round(r["stacked_ms"], 4)},
+        "launch_floor_us": round(r["floor_ms"] * 1e3, 3),
         "cpu_baseline": cpu,
         "device": r["device"],
     }
+    if "sweep_us" in r:
+        out["sweep_us"] = r["sweep_us"]
     print(json.dumps(out), flush=True)
 
 

@@ -151,6 +151,31 @@ int nlg_ternary_linear_i8(const uint32_t *xq, const float *gamma, const uint32_t
                           float *y, uint32_t seq, uint32_t out, uint32_t cols,
                           void *stream);
 
+/* Launch-geometry variant of nlg_ternary_linear_i8 for tuning sweeps:
+ * rows_per_wave in {1,2,4,8}, waves_per_block in 1..4.  Results are
+ * bit-identical for every geometry. */
+int nlg_ternary_linear_i8_cfg(const uint32_t *xq, const float *gamma, const uint32_t *w2,
+                              const float *bias, const float *beta, int beta_per_row, float *y,
+                              uint32_t seq, uint32_t out, uint32_t cols, int rows_per_wave,
+                              int waves_per_block, void *stream);
+
+/* The whole ternary linear from f32 activations: pack-act-rows quantisation
+ * of x then nlg_ternary_linear_i8, bit-identical to running the two.  When
+ * cols % 64 == 0, cols <= 16384 and seq <= 4 it is one launch (each
+ * workgroup quantises the row into LDS while its weight loads are in
+ * flight) and needs no workspace; otherwise it runs pack-act-rows into
+ * `workspace` (nlg_ternary_linear_workspace bytes) and then the GEMV.
+ * gamma_out (may be NULL) receives the per-token scales. */
+int nlg_ternary_linear(const float *x, const uint32_t *w2, const float *bias, const float *beta,
+                       int beta_per_row, float *y, float *gamma_out, uint32_t seq, uint32_t out,
+                       uint32_t cols, void *workspace, size_t workspace_bytes, void *stream);
+size_t nlg_ternary_linear_workspace(uint32_t seq, uint32_t cols);
+/* Tuning variant: rows_per_wave in {1,2,4} for the one-launch form (0 = default). */
+int nlg_ternary_linear_cfg(const float *x, const uint32_t *w2, const float *bias, const float *beta,
+                           int beta_per_row, float *y, float *gamma_out, uint32_t seq, uint32_t out,
+                           uint32_t cols, int rows_per_wave, void *workspace, size_t workspace_bytes,
+                           void *stream);
+
 /* Row softmax, numerically stable (row max subtracted), in place when
  * c == a.  Semantics of `softmax` (kernels.el:28-42). */
 int nlg_softmax_rows(const float *a, float *c, uint32_t rows, uint32_t cols, void *stream);

@@ -41,6 +41,56 @@ __device__ __forceinline__ uint32_t pack_lane(float v, float gamma) {
   return neg ? (256u - ri) % 256u : ri;
 }
 
+// ---- exact quantisation without a division per element ----
+//
+// pack-act-rows' lane magnitude is ri = min(trunc(t'), 127) with
+// t' = RN(RN(|v|/gamma) + 0.5).  With ginv = RN(1/gamma) finite, the estimate
+// t = RN(RN(|v|*ginv) + 0.5) differs from t' by less than 4e-5 whenever
+// t < 128 (the reciprocal, the product and the quotient each err by at most
+// 2^-24 relative on a value below 128.5, plus half an ulp of the final add),
+// so trunc(t) == trunc(t') unless t lies within 2^-13 of an integer; and
+// t >= 128 means t' > 127.99, which the clamp maps to 127 either way.  The
+// few elements that fall inside that band (and NaNs) are recomputed with the
+// reference's IEEE division.  |v|/gamma = |v/gamma| under round-to-nearest,
+// and a nonzero lane implies |v/gamma| >= 0.5, so the sign is v's.
+__device__ __forceinline__ uint32_t lane_est(float v, float ginv, bool &near) {
+  const float t = __fadd_rn(__fmul_rn(fabsf(v), ginv), 0.5f);
+  const float kf = truncf(t), fr = t - kf;
+  const bool big = t >= 128.0f;
+  near = !(big || (fr >= 0x1p-13f && fr <= 1.0f - 0x1p-13f));  // NaN lands here
+  const uint32_t k = big ? 127u : (uint32_t)kf;
+  return v < 0.0f ? (256u - k) & 255u : k;
+}
+// Packed word of four lanes; `near` gets one bit per lane that needs the
+// exact path.
+__device__ __forceinline__ uint32_t word_est(float4 v, float ginv, uint32_t &near) {
+  bool n0, n1, n2, n3;
+  const uint32_t w = lane_est(v.x, ginv, n0) | (lane_est(v.y, ginv, n1) << 8) |
+                     (lane_est(v.z, ginv, n2) << 16) | (lane_est(v.w, ginv, n3) << 24);
+  near = (n0 ? 1u : 0u) | (n1 ? 2u : 0u) | (n2 ? 4u : 0u) | (n3 ? 8u : 0u);
+  return w;
+}
+// Replace the flagged lanes of a word with the reference's own computation.
+__device__ __forceinline__ uint32_t word_fix(uint32_t w, float4 v, float gamma, uint32_t near) {
+  if (near & 1u) w = (w & 0xFFFFFF00u) | pack_lane(v.x, gamma);
+  if (near & 2u) w = (w & 0xFFFF00FFu) | (pack_lane(v.y, gamma) << 8);
+  if (near & 4u) w = (w & 0xFF00FFFFu) | (pack_lane(v.z, gamma) << 16);
+  if (near & 8u) w = (w & 0x00FFFFFFu) | (pack_lane(v.w, gamma) << 24);
+  return w;
+}
+// The packed word pack-act-rows stores for v.  `fast` (1/gamma finite and
+// gamma > 0) is uniform across the block.  The exact fix-up sits behind a
+// wave-uniform vote, so a wave with no flagged lane skips it entirely.
+__device__ __forceinline__ uint32_t quant_word(float4 v, float gamma, float ginv, bool fast) {
+  if (!fast)
+    return pack_lane(v.x, gamma) | (pack_lane(v.y, gamma) << 8) | (pack_lane(v.z, gamma) << 16) |
+           (pack_lane(v.w, gamma) << 24);
+  uint32_t near;
+  uint32_t w = word_est(v, ginv, near);
+  if (__builtin_amdgcn_ballot_w64(near != 0u) != 0ull) w = word_fix(w, v, gamma, near);
+  return w;
+}
+
 // One workgroup per row.  Pass 1: amax (order-free: the DSL max never
 // selects a NaN and starts from 0).  Pass 2: one packed word per thread-step.
 template <bool VEC4>
@@ -70,15 +120,15 @@ __global__ __launch_bounds__(256) void k_pack_act_rows(const float *__restrict__
     }
   }
   amax = nlg_block_max_f32(amax, red);
-  const float g = amax / 127.0f;
+  const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
+  const float ginv = 1.0f / g;
   if (threadIdx.x == 0) gamma[row] = g;
+  const bool fast = g > 0.0f && ginv < INFINITY;
   uint32_t *q = xq + (size_t)row * ng;
   for (uint32_t w = threadIdx.x; w < ng; w += blockDim.x) {
     uint32_t word = 0;
     if (VEC4 && 4 * w + 3 < cols) {
-      float4 v = ((const float4 *)xr)[w];
-      word = pack_lane(v.x, g) | (pack_lane(v.y, g) << 8) | (pack_lane(v.z, g) << 16) |
-             (pack_lane(v.w, g) << 24);
+      word = quant_word(((const float4 *)xr)[w], g, ginv, fast);
     } else {
       for (uint32_t l = 0; l < 4; l++) {
         uint32_t c = 4 * w + l;
@@ -232,6 +282,15 @@ __global__ __launch_bounds__(256) void k_tern_i8_fast(TernArgs a) {
   for (int r = 0; r < R; r++)
 #pragma unroll
     for (int s = 0; s < ST; s++) acc[r][s] = 0;
+  // epilogue operands are loaded now, with the weights, not after the sums
+  const uint32_t orow_u = row0 + (lane < R ? lane : 0);
+  const uint32_t orow = orow_u < a.out ? orow_u : a.out - 1;  // every lane loads a valid row
+  const bool olive = lane < R && orow_u < a.out;
+  const float bo = a.bias ? a.bias[orow] : 0.0f;  // uniform test of a kernel argument
+  const float be = a.beta[a.beta_per_row ? orow : 0];
+  float gm[ST];
+#pragma unroll
+  for (int s = 0; s < ST; s++) gm[s] = (s0 + s < a.seq) ? a.gamma[s0 + s] : 0.0f;
 
   // Lanes leave this loop at different trips and reconverge after it, so the
   // DPP reductions below run with the full wave active.
@@ -267,8 +326,77 @@ __global__ __launch_bounds__(256) void k_tern_i8_fast(TernArgs a) {
 #pragma unroll
     for (int r = 0; r < R; r++) {
       const int tot = nlg_wave_sum_i32(acc[r][s]);
-      if (lane == r && row0 + r < a.out) tern_store(a, tok, row0 + r, tot);
+      // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
+      if (lane == r && olive)
+        a.y[(size_t)tok * a.out + orow] = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, gm[s]), (float)(tot >> 6)));
     }
+  }
+}
+
+// One token (the decode GEMV): cols % 64 == 0 and nchunk <= 64*CPL.  All of a
+// lane's loads -- activation chunks (L2), weight chunks (HBM) and epilogue
+// operands -- are issued as straight-line code before any use; invalid chunks
+// read a clamped real address and are zeroed by selects, because a branch
+// around a load makes the wait-count pass drain every load at the join.
+template <int R, int CPL>
+__global__ __launch_bounds__(256) void k_tern_i8_dec(TernArgs a) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const uint32_t row0 = wave * R;
+  if (row0 >= a.out) return;  // wave-uniform
+  const uint32_t nchunk = a.wng >> 2;
+  const uint32_t tok = blockIdx.y;
+  uint4 xv[CPL][4];
+  const uint4 *xr = (const uint4 *)(a.xq + (size_t)tok * a.ng);
+#pragma unroll
+  for (int i = 0; i < CPL; i++) {
+    const uint32_t c = lane + 64u * i, cc = c < nchunk ? c : nchunk - 1;
+#pragma unroll
+    for (int j = 0; j < 4; j++) xv[i][j] = xr[4 * cc + j];
+  }
+  uint4 wv[R][CPL];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const uint32_t row = row0 + r < a.out ? row0 + r : a.out - 1;
+    const uint4 *wr = (const uint4 *)(a.w2 + (size_t)row * a.wng);
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+      const uint32_t c = lane + 64u * i;
+      wv[r][i] = wr[c < nchunk ? c : nchunk - 1];
+    }
+  }
+  const uint32_t orow_u = row0 + (lane < R ? lane : 0);
+  const uint32_t orow = orow_u < a.out ? orow_u : a.out - 1;
+  const bool olive = lane < R && orow_u < a.out;
+  const float *bsrc = a.bias ? a.bias : a.beta;
+  const float bo_raw = bsrc[a.bias ? orow : 0];
+  const float be = a.beta[a.beta_per_row ? orow : 0];
+  const float gm = a.gamma[tok];
+  const float bo = a.bias ? bo_raw : 0.0f;
+  int acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) acc[r] = 0;
+#pragma unroll
+  for (int i = 0; i < CPL; i++) {
+    const bool valid = lane + 64u * i < nchunk;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      uint32_t y0, y1, y2, y3;
+      xpose4(xv[i][j].x, xv[i][j].y, xv[i][j].z, xv[i][j].w, y0, y1, y2, y3);
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        uint32_t w = j == 0 ? wv[r][i].x : j == 1 ? wv[r][i].y : j == 2 ? wv[r][i].z : wv[r][i].w;
+        w = valid ? w : 0u;
+        acc[r] = wdot(w, y0, y1, y2, y3, acc[r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int tot = nlg_wave_sum_i32(acc[r]);
+    // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
+    if (lane == r && olive)
+      a.y[(size_t)tok * a.out + orow] = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, gm), (float)(tot >> 6)));
   }
 }
 
@@ -322,10 +450,14 @@ static int tern_launch(const TernArgs &a, int rows_per_wave, int waves_per_block
 #define TERN_FAST(RR, SS)                                                                     \
   hipLaunchKernelGGL((k_tern_i8_fast<RR, SS>),                                               \
                      dim3(nlg_blocks(a.out, rows_per_block), (a.seq + SS - 1) / SS), blk, 0, st, a)
-#define TERN_FAST_R(RR)                     \
-  do {                                      \
-    if (a.seq == 1) TERN_FAST(RR, 1);       \
-    else if (a.seq <= 2) TERN_FAST(RR, 2);  \
+#define TERN_DEC(RR, CC) \
+  hipLaunchKernelGGL((k_tern_i8_dec<RR, CC>), dim3(nlg_blocks(a.out, rows_per_block), 1), blk, 0, st, a)
+#define TERN_FAST_R(RR)                                     \
+  do {                                                      \
+    if (a.seq == 1 && a.wng / 4 <= 64) TERN_DEC(RR, 1);     \
+    else if (a.seq == 1 && a.wng / 4 <= 128) TERN_DEC(RR, 2); \
+    else if (a.seq == 1) TERN_FAST(RR, 1);                  \
+    else if (a.seq <= 2) TERN_FAST(RR, 2);                  \
     else if (a.seq <= 4) TERN_FAST(RR, 4);  \
     else TERN_FAST(RR, 8);                  \
   } while (0)
@@ -348,6 +480,7 @@ static int tern_launch(const TernArgs &a, int rows_per_wave, int waves_per_block
   }
 #undef TERN_FAST
 #undef TERN_FAST_R
+#undef TERN_DEC
 #undef TERN_ANY
   NLG_LAUNCHED("ternary linear i8");
   return NLG_OK;
@@ -357,7 +490,8 @@ static void tern_default_geometry(uint32_t out, uint32_t seq, int *rpw, int *wpb
   // Enough waves to give every SIMD of 256 CUs work at decode shapes.
   (void)seq;
   *wpb = 4;
-  *rpw = out >= 4096 ? 4 : (out >= 1024 ? 2 : 1);
+  // about two workgroups per CU measured best at 4096 rows (3.2 us)
+  *rpw = out >= 2048 ? 2 : 1;
 }
 
 extern "C" int nlg_ternary_linear_i8_cfg(const uint32_t *xq, const float *gamma, const uint32_t *w2,
@@ -381,6 +515,204 @@ extern "C" int nlg_ternary_linear_i8(const uint32_t *xq, const float *gamma, con
   tern_default_geometry(out, seq, &rpw, &wpb);
   return nlg_ternary_linear_i8_cfg(xq, gamma, w2, bias, beta, beta_per_row, y, seq, out, cols, rpw,
                                    wpb, stream);
+}
+
+// ---------------------------------------- fused: quantise + GEMV, one launch
+
+// The decode step as one kernel: each workgroup first issues the HBM loads
+// of its weight rows (kept in registers), then -- while those loads are in
+// flight -- reads the token's f32 activation row (L2-resident after the
+// first workgroup), finds amax, and writes pack-act-rows' int8 words into
+// LDS; after one barrier every wave dots its rows against the LDS copy.
+// The rounding (pack_lane) and epilogue (tern_store) are the same code as
+// the two-kernel path, so the result is bit-identical to it.
+// Requires cols % 64 == 0 and cols <= 64*64*CPL.
+struct FusedArgs {
+  const float *x;        // [seq x cols] f32
+  const uint32_t *w2;    // [out x wng]
+  const float *bias;     // [out] or null
+  const float *beta;     // [1] or [out]
+  float *y;              // [seq x out]
+  float *gamma_out;      // [seq] or null
+  uint32_t seq, out, cols, wng;
+  int beta_per_row;
+};
+
+// F4: float4s of the activation row per thread (cols <= 1024*F4).
+template <int R, int CPL, int F4>
+__global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
+  extern __shared__ uint4 s_xq4[];  // cols/16 uint4 = cols int8 lanes
+  __shared__ float red[4];
+  const int lane = threadIdx.x & 63, wvi = threadIdx.x >> 6;
+  const uint32_t tok = blockIdx.y;
+  const uint32_t row0 = (blockIdx.x * 4 + wvi) * R;
+  const uint32_t nchunk = a.wng >> 2;
+  // 1. every global load is issued up front, activation first: vmcnt retires
+  //    in issue order, so waiting for x must not also wait for the weights'
+  //    HBM fetch, which stays in flight through the quantisation below.  The
+  //    loads are straight-line (clamped addresses, validity applied with
+  //    selects afterwards): a branch around a load makes the wait-count pass
+  //    drain every outstanding load at the join.
+  const float4 *x4 = (const float4 *)(a.x + (size_t)tok * a.cols);
+  const uint32_t nf4 = a.cols >> 2;
+  float4 xv4[F4];
+#pragma unroll
+  for (int k = 0; k < F4; k++) {
+    const uint32_t f = threadIdx.x + 256u * k;
+    xv4[k] = x4[f < nf4 ? f : nf4 - 1];
+  }
+  uint4 wv[R][CPL];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const uint32_t row = row0 + r < a.out ? row0 + r : a.out - 1;
+    const uint4 *wr = (const uint4 *)(a.w2 + (size_t)row * a.wng);
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+      const uint32_t c = lane + 64 * i;
+      wv[r][i] = wr[c < nchunk ? c : nchunk - 1];
+    }
+  }
+  const uint32_t orow_u = row0 + (lane < R ? lane : 0);
+  const uint32_t orow = orow_u < a.out ? orow_u : a.out - 1;  // every lane loads a valid row
+  const bool olive = lane < R && orow_u < a.out;
+  const float *bsrc = a.bias ? a.bias : a.beta;  // a real address either way
+  const float bo_raw = bsrc[a.bias ? orow : 0];
+  const float be = a.beta[a.beta_per_row ? orow : 0];
+  const float bo = a.bias ? bo_raw : 0.0f;
+#pragma unroll
+  for (int k = 0; k < F4; k++)
+    if (threadIdx.x + 256u * k >= nf4) xv4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int i = 0; i < CPL; i++)
+      if (lane + 64u * i >= nchunk) wv[r][i] = make_uint4(0, 0, 0, 0);
+  // 2. amax of the token's row (every thread takes part: barriers follow)
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < F4; k++) {
+    float t;
+    t = dsl_abs(xv4[k].x); amax = t > amax ? t : amax;
+    t = dsl_abs(xv4[k].y); amax = t > amax ? t : amax;
+    t = dsl_abs(xv4[k].z); amax = t > amax ? t : amax;
+    t = dsl_abs(xv4[k].w); amax = t > amax ? t : amax;
+  }
+  amax = nlg_block_max_f32(amax, red);
+  const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;  // uniform: a scalar
+  const float ginv = 1.0f / g;
+  if (a.gamma_out && blockIdx.x == 0 && threadIdx.x == 0) a.gamma_out[tok] = g;
+  // 3. quantise into LDS, one packed word per float4 (exact; see lane_est)
+  const bool fast = g > 0.0f && ginv < INFINITY;
+  uint32_t *s_xq = (uint32_t *)s_xq4;
+#pragma unroll
+  for (int k = 0; k < F4; k++) {
+    const uint32_t f = threadIdx.x + 256u * k;
+    const uint32_t wd = quant_word(xv4[k], g, ginv, fast);
+    if (f < nf4) s_xq[f] = wd;
+  }
+  __syncthreads();
+  if (row0 >= a.out) return;  // wave-uniform, after the last barrier
+  // 4. dots against the LDS activation
+  int acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) acc[r] = 0;
+#pragma unroll
+  for (int i = 0; i < CPL; i++) {
+    const uint32_t c = lane + 64 * i;
+    if (c < nchunk) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint4 xv = s_xq4[4 * c + j];
+        uint32_t y0, y1, y2, y3;
+        xpose4(xv.x, xv.y, xv.z, xv.w, y0, y1, y2, y3);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          const uint32_t w = j == 0 ? wv[r][i].x : j == 1 ? wv[r][i].y : j == 2 ? wv[r][i].z : wv[r][i].w;
+          acc[r] = wdot(w, y0, y1, y2, y3, acc[r]);
+        }
+      }
+    }
+  }
+  // 5. reduce and write (tern_store's epilogue, with gamma from registers)
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int tot = nlg_wave_sum_i32(acc[r]);
+    if (lane == r && olive)
+      a.y[(size_t)tok * a.out + orow] = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, g), (float)(tot >> 6)));
+  }
+}
+
+static int fused_launch(const FusedArgs &a, int rpw, hipStream_t st) {
+  const uint32_t nchunk = a.wng / 4;
+  const size_t lds = (size_t)a.cols;  // one byte per column
+  dim3 grid(nlg_blocks(a.out, 4u * rpw), a.seq), blk(256);
+  // float4s per thread: cols/1024 rounded up to 2, 4, 8 or 16
+#define FZ(RR, CC)                                                                         \
+  do {                                                                                     \
+    if (a.cols <= 2048) hipLaunchKernelGGL((k_tern_fused<RR, CC, 2>), grid, blk, lds, st, a); \
+    else if (a.cols <= 4096) hipLaunchKernelGGL((k_tern_fused<RR, CC, 4>), grid, blk, lds, st, a); \
+    else if (a.cols <= 8192) hipLaunchKernelGGL((k_tern_fused<RR, CC, 8>), grid, blk, lds, st, a); \
+    else hipLaunchKernelGGL((k_tern_fused<RR, CC, 16>), grid, blk, lds, st, a);            \
+  } while (0)
+#define FZR(RR)                          \
+  do {                                   \
+    if (nchunk <= 64) FZ(RR, 1);         \
+    else if (nchunk <= 128) FZ(RR, 2);   \
+    else FZ(RR, 4);                      \
+  } while (0)
+  switch (rpw) {
+    case 1: FZR(1); break;
+    case 2: FZR(2); break;
+    default: FZR(4); break;
+  }
+#undef FZR
+#undef FZ
+  NLG_LAUNCHED("ternary linear (fused quantisation)");
+  return NLG_OK;
+}
+
+extern "C" int nlg_ternary_linear_cfg(const float *x, const uint32_t *w2, const float *bias,
+                                      const float *beta, int beta_per_row, float *y, float *gamma_out,
+                                      uint32_t seq, uint32_t out, uint32_t cols, int rows_per_wave,
+                                      void *workspace, size_t workspace_bytes, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!seq || !out) return NLG_OK;
+  hipStream_t st = nlg_stream(stream);
+  const bool fusable = (cols % 64 == 0) && cols <= 16384 && (((uintptr_t)x & 15) == 0) &&
+                       (((uintptr_t)w2 & 15) == 0) && seq <= 4;
+  if (fusable) {
+    FusedArgs a{x, w2, bias, beta, y, gamma_out, seq, out, cols, cols / 16, beta_per_row};
+    int rpw = rows_per_wave;
+    // Each workgroup quantises the whole row, so fewer, fatter workgroups
+    // waste less; about one per CU measured best at 4096 rows (4.3 us).
+    if (rpw != 1 && rpw != 2 && rpw != 4) rpw = out >= 4096 ? 4 : (out >= 2048 ? 2 : 1);
+    return fused_launch(a, rpw, st);
+  }
+  // two launches: pack-act-rows into the workspace, then the GEMV
+  const size_t ng = (cols + 3) / 4;
+  const size_t need = (seq * ng * 4 + 255) / 256 * 256 + (size_t)seq * 4;
+  if (!workspace || workspace_bytes < need)
+    return nlg_fail("ternary linear: this shape needs a %zu-byte workspace", need);
+  uint32_t *xq = (uint32_t *)workspace;
+  float *gm = gamma_out ? gamma_out : (float *)((char *)workspace + (seq * ng * 4 + 255) / 256 * 256);
+  if (launch_pack_act(x, xq, gm, seq, cols, (uint32_t)ng, st)) return NLG_ERR;
+  TernArgs ta{xq, gm, w2, bias, beta, y, seq, out, cols, (uint32_t)ng, (cols + 15) / 16, beta_per_row};
+  int rpw, wpb;
+  tern_default_geometry(out, seq, &rpw, &wpb);
+  return tern_launch(ta, rpw, wpb, st);
+}
+
+extern "C" size_t nlg_ternary_linear_workspace(uint32_t seq, uint32_t cols) {
+  const size_t ng = (cols + 3) / 4;
+  return (seq * ng * 4 + 255) / 256 * 256 + (size_t)seq * 4;
+}
+
+extern "C" int nlg_ternary_linear(const float *x, const uint32_t *w2, const float *bias,
+                                  const float *beta, int beta_per_row, float *y, float *gamma_out,
+                                  uint32_t seq, uint32_t out, uint32_t cols, void *workspace,
+                                  size_t workspace_bytes, void *stream) {
+  return nlg_ternary_linear_cfg(x, w2, bias, beta, beta_per_row, y, gamma_out, seq, out, cols, 0,
+                                workspace, workspace_bytes, stream);
 }
 
 // "ternary-i8" by name (an extension with no reference counterpart: the

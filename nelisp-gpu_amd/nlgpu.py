@@ -81,6 +81,9 @@ def lib() -> C.CDLL:
         "nlg_ternary_linear_i8": (i32, [vp, vp, vp, vp, vp, i32, vp, u32, u32, u32, vp]),
         "nlg_ternary_linear_i8_cfg": (i32, [vp, vp, vp, vp, vp, i32, vp, u32, u32, u32, i32, i32, vp]),
         "nlg_softmax_rows": (i32, [vp, vp, u32, u32, vp]),
+        "nlg_ternary_linear": (i32, [vp, vp, vp, vp, i32, vp, vp, u32, u32, u32, vp, sz, vp]),
+        "nlg_ternary_linear_cfg": (i32, [vp, vp, vp, vp, i32, vp, vp, u32, u32, u32, i32, vp, sz, vp]),
+        "nlg_ternary_linear_workspace": (sz, [u32, u32]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -220,6 +223,25 @@ def ternary_linear_i8(xq, gamma, w2, bias, beta, y, seq, out, cols, beta_per_row
         rc = L.nlg_ternary_linear_i8(xq.ptr, gamma.ptr, w2.ptr, bp, beta.ptr, int(beta_per_row),
                                      y.ptr, seq, out, cols, stream)
     _check(rc, "ternary_linear_i8")
+
+
+def ternary_linear(x, w2, bias, beta, y, seq, out, cols, beta_per_row=False, gamma_out=None,
+                   workspace=None, rows_per_wave: int = 0, stream=None) -> None:
+    """pack-act-rows + ternary GEMV from f32 activations (one launch when fusable)."""
+    L = lib()
+    args = (x.ptr, w2.ptr, bias.ptr if bias is not None else None, beta.ptr, int(beta_per_row), y.ptr,
+            gamma_out.ptr if gamma_out is not None else None, seq, out, cols)
+    ws = workspace.ptr if workspace is not None else None
+    wsb = workspace.nbytes if workspace is not None else 0
+    if rows_per_wave:
+        rc = L.nlg_ternary_linear_cfg(*args, rows_per_wave, ws, wsb, stream)
+    else:
+        rc = L.nlg_ternary_linear(*args, ws, wsb, stream)
+    _check(rc, "ternary_linear")
+
+
+def ternary_linear_workspace(seq: int, cols: int) -> int:
+    return lib().nlg_ternary_linear_workspace(seq, cols)
 
 
 def softmax_rows(a: DeviceArray, c: DeviceArray, rows: int, cols: int, stream=None) -> None:

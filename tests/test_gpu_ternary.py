@@ -97,3 +97,37 @@ def test_int32_accumulator_extremes():
     nlgpu.ternary_linear_i8(nlgpu.to_device(xq), nlgpu.to_device(g), nlgpu.to_device(w2), None,
                             nlgpu.to_device(np.array([1.0], np.float32)), dy, seq, out, cols)
     assert np.array_equal(dy.download(np.float32, seq * out).view(np.uint32), y_ref.view(np.uint32))
+
+
+FUSED = [(1, 4096, 4096), (1, 6912, 2560), (1, 2560, 6912), (2, 3840, 2560), (4, 100, 1024), (3, 5, 64),
+         (1, 128256, 2560)]
+
+
+@pytest.mark.parametrize("seq,out,cols", FUSED)
+@pytest.mark.parametrize("rpw", [0, 1, 2, 4])
+def test_fused_linear_bit_exact(seq, out, cols, rpw):
+    if rpw and out > 20000:
+        pytest.skip("geometry sweep on the small shapes only")
+    print(f"[gpu] fused ternary seq={seq} out={out} cols={cols} rpw={rpw}", flush=True)
+    t, w2, x, bias, beta = make(seq * 3 + out, seq, out, cols, per_row=(out % 2 == 0))
+    xq, g = orc.pack_act_rows(x, seq, cols)
+    y_ref = orc.ternary_linear_i8(xq, g, w2, bias, beta, seq, out, cols, beta_per_row=(out % 2 == 0))
+    dy, dg = nlgpu.DeviceArray(seq * out * 4), nlgpu.DeviceArray(seq * 4)
+    nlgpu.ternary_linear(nlgpu.to_device(x), nlgpu.to_device(w2), nlgpu.to_device(bias), nlgpu.to_device(beta),
+                         dy, seq, out, cols, beta_per_row=(out % 2 == 0), gamma_out=dg, rows_per_wave=rpw)
+    assert np.array_equal(dg.download(np.float32, seq).view(np.uint32), g.view(np.uint32))
+    assert np.array_equal(dy.download(np.float32, seq * out).view(np.uint32), y_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("seq,out,cols", [(16, 300, 2560), (2, 50, 1000), (5, 64, 4096)])
+def test_linear_two_launch_path_with_workspace(seq, out, cols):
+    t, w2, x, bias, beta = make(77 + seq, seq, out, cols)
+    xq, g = orc.pack_act_rows(x, seq, cols)
+    y_ref = orc.ternary_linear_i8(xq, g, w2, bias, beta, seq, out, cols)
+    dy = nlgpu.DeviceArray(seq * out * 4)
+    dx, dw, db, dbe = (nlgpu.to_device(a) for a in (x, w2, bias, beta))
+    with pytest.raises(nlgpu.NlgError):
+        nlgpu.ternary_linear(dx, dw, db, dbe, dy, seq, out, cols)  # needs a workspace
+    ws = nlgpu.DeviceArray(nlgpu.ternary_linear_workspace(seq, cols))
+    nlgpu.ternary_linear(dx, dw, db, dbe, dy, seq, out, cols, workspace=ws)
+    assert np.array_equal(dy.download(np.float32, seq * out).view(np.uint32), y_ref.view(np.uint32))
