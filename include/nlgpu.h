@@ -180,6 +180,109 @@ int nlg_ternary_linear_cfg(const float *x, const uint32_t *w2, const float *bias
  * c == a.  Semantics of `softmax` (kernels.el:28-42). */
 int nlg_softmax_rows(const float *a, float *c, uint32_t rows, uint32_t cols, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Decoder-layer fusions.  The reference runs a decode layer as a chain of
+ * named kernels over resident buffers (rmsnorm-istd, rmsnorm-fwd,
+ * pack-act-rows, the linear, decode-rope, cache-append, decode-attn,
+ * silu-mul, add2); each entry point below is one launch doing a run of that
+ * chain, with the same per-element arithmetic.  All require
+ * cols % 64 == 0, cols <= 16384 and 16-byte aligned x, gain and weights.
+ * The RMSNorm is rmsnorm-istd + rmsnorm-fwd (kernels.el:1249-1265) with eps
+ * a parameter: S = 1/sqrt(sum(x*x)/cols + eps), xn = (x*S)*gain; its sum is
+ * a tree, so S may differ from the serial loop's in the last bit.
+ * ---------------------------------------------------------------------- */
+
+/* y = linear(rmsnorm(x)) (rmsnorm-istd, rmsnorm-fwd, pack-act-rows,
+ * bitlinear-dp4a-1f on 2-bit weights). */
+int nlg_rms_ternary_linear(const float *x, const float *gain, float eps, const uint32_t *w2,
+                           const float *bias, const float *beta, int beta_per_row, float *y,
+                           uint32_t seq, uint32_t out, uint32_t cols, void *stream);
+
+/* y = res + linear(x) (pack-act-rows, the linear, add2 kernels.el:812-821);
+ * res may equal y (the residual stream updated in place). */
+int nlg_ternary_linear_residual(const float *x, const uint32_t *w2, const float *bias,
+                                const float *beta, int beta_per_row, const float *res, float *y,
+                                uint32_t seq, uint32_t out, uint32_t cols, void *stream);
+
+/* SwiGLU: w2gu holds 2*dff rows, row 2j = gate row j, row 2j+1 = up row j;
+ * g, u = linear(rmsnorm(x)); h[j] = (g * (1/(1 + exp(0 - g)))) * u
+ * (silu-mul, kernels.el:186-193).  beta indexes the interleaved rows. */
+int nlg_rms_ternary_swiglu(const float *x, const float *gain, float eps, const uint32_t *w2gu,
+                           const float *beta, int beta_per_row, float *h, uint32_t seq,
+                           uint32_t dff, uint32_t cols, void *stream);
+
+/* Attention input projection at decode: rows of w2qkv are q (heads*head_dim)
+ * | k (kvheads*head_dim) | v.  q and k are rotated at position pos[0]
+ * (decode-rope / decode-rope-b, kernels.el:291-306, :340-355: pairs (2m,
+ * 2m+1) of each head, C0 = a0*cos - a1*sin, C1 = a0*sin + a1*cos with
+ * tables [max_seq x head_dim/2]); q goes to `q` [seq x heads*head_dim]; k
+ * and v are rounded to fp16 and stored at position pos[0] of the caches
+ * (cache-append-b, kernels.el:356-365), laid out [seq][kvheads][max_seq]
+ * [head_dim].  A pos[0] outside [0, max_seq) stores nothing to the caches. */
+int nlg_rms_ternary_qkv_rope(const float *x, const float *gain, float eps, const uint32_t *w2qkv,
+                             const float *beta, int beta_per_row, float *q, uint16_t *kcache,
+                             uint16_t *vcache, const float *rope_cos, const float *rope_sin,
+                             const int32_t *pos, uint32_t seq, uint32_t heads, uint32_t kvheads,
+                             uint32_t head_dim, uint32_t max_seq, uint32_t cols, void *stream);
+
+/* LM head + greedy choice: logits = linear(rmsnorm(x)) and argmax[s] = the
+ * lowest index of the largest logit (NaN never chosen; -1 if none). */
+int nlg_rms_ternary_argmax(const float *x, const float *gain, float eps, const uint32_t *w2,
+                           const float *beta, int beta_per_row, float *logits, int32_t *argmax,
+                           uint32_t seq, uint32_t vocab, uint32_t cols, void *workspace,
+                           size_t workspace_bytes, void *stream);
+size_t nlg_rms_ternary_argmax_workspace(uint32_t seq, uint32_t vocab);
+
+/* Single-query GQA attention over fp16 caches [batch][kvheads][max_seq]
+ * [head_dim] for positions 0..pos[0]: decode-attn-b's arithmetic
+ * (kernels.el:366-390: s = (q.k)/sqrt(head_dim), e = exp(s - max),
+ * out = sum(e*v)/sum(e)) with K, V read as fp16.  head_dim 64 or 128,
+ * heads/kvheads in {1,2,4,8}.  The workspace
+ * (nlg_decode_attn_f16_workspace bytes) must be zero-filled before its
+ * first use (nlg_malloc memory is); calls leave it ready for the next. */
+int nlg_decode_attn_f16(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                        const int32_t *pos, float *out, uint32_t batch, uint32_t heads,
+                        uint32_t kvheads, uint32_t head_dim, uint32_t max_seq, void *workspace,
+                        size_t workspace_bytes, void *stream);
+size_t nlg_decode_attn_f16_workspace(uint32_t batch, uint32_t heads, uint32_t kvheads,
+                                     uint32_t head_dim, uint32_t max_seq);
+
+/* ------------------------------------------------------------------------
+ * A random-initialised ternary decoder stack (pre-norm, SwiGLU, GQA, RoPE,
+ * fp16 KV cache, ternary LM head, greedy decode) built from the fusions
+ * above.  The reference composes its models in Lisp over vkserver (the
+ * nl-llm-* callers, not part of the reference tree); this is the same
+ * composition run as one captured graph per token.
+ * ---------------------------------------------------------------------- */
+typedef struct nlg_stack nlg_stack;
+typedef struct {
+  uint32_t layers, d_model, heads, kv_heads, head_dim, d_ff, vocab, max_seq, batch;
+  float rms_eps, rope_theta;
+  uint64_t seed;
+} nlg_stack_config;
+
+/* Allocate and generate every weight on the device from cfg->seed. */
+int nlg_stack_create(const nlg_stack_config *cfg, nlg_stack **out);
+void nlg_stack_destroy(nlg_stack *s);
+/* Begin `batch` sequences with prompts [batch x n_prompt] (host int32). */
+int nlg_stack_start(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt);
+/* Run `steps` token steps: the token at the current position goes through
+ * every layer, its K/V are cached, and the next token is the prompt's while
+ * the prompt lasts, else the greedy choice.  use_graph != 0 replays one
+ * captured graph per step. */
+int nlg_stack_step(nlg_stack *s, uint32_t steps, int use_graph);
+/* Current position (tokens consumed per sequence). */
+int nlg_stack_position(nlg_stack *s, uint32_t *pos);
+/* Token history [batch x max_seq] (prompt, then generated; -1 unwritten) and
+ * greedy choices [batch x max_seq] (argmax after position p). */
+int nlg_stack_tokens(nlg_stack *s, int32_t *tokens, int32_t *greedy);
+/* Logits of the last step, [batch x vocab] (host). */
+int nlg_stack_logits(nlg_stack *s, float *logits);
+/* Device pointer and size of a named tensor ("wqkv", "bqkv", "wo", "bo",
+ * "wgu", "bgu", "wd", "bd", "gattn", "gffn", "kc", "vc" with a layer;
+ * "wlm", "blm", "gfinal", "emb", "rope_cos", "rope_sin", "x" with layer -1). */
+int nlg_stack_tensor(nlg_stack *s, const char *name, int layer, void **ptr, size_t *bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -136,6 +136,47 @@ __device__ __forceinline__ float nlg_block_max_f32(float v, float *scratch) {
   return t;
 }
 
+// ------------------------------------------------- fused quantise + GEMV
+// One launch: optional RMSNorm of the activation row, pack-act-rows'
+// quantisation into LDS, the 2-bit x int8 GEMV, and an epilogue.
+enum { NLG_PRO_NONE = 0, NLG_PRO_RMS = 1 };
+enum {
+  NLG_EPI_STORE = 0,   // y = bias + (beta*gamma)*acc
+  NLG_EPI_RESID = 1,   // y = res + that
+  NLG_EPI_SWIGLU = 2,  // rows 2j, 2j+1 = gate j, up j; y[j] = silu(gate)*up
+  NLG_EPI_QKV = 3,     // rows = q | k | v; RoPE on q, k; k, v appended to fp16 caches
+  NLG_EPI_ARGMAX = 4,  // y = logits, plus one (max, index) per wave
+};
+struct FusedArgs {
+  const float *x;        // [seq x cols] f32 activation rows
+  const float *gain;     // PRO_RMS: [cols]
+  float eps;             // PRO_RMS
+  const uint32_t *w2;    // [out x wng] 2-bit rows
+  const float *bias;     // [out] or null
+  const float *beta;     // [1] or [out]
+  int beta_per_row;
+  uint32_t seq, out, cols, wng;
+  float *y;              // output rows, ystride floats apart
+  uint32_t ystride;
+  const float *res;      // EPI_RESID, rstride floats apart (may equal y)
+  uint32_t rstride;
+  float *gamma_out;      // [seq] or null
+  // EPI_QKV: q -> y; k, v -> caches [seq][kvheads][max_seq][hd] (fp16 bits)
+  uint32_t nq, nkv, hd, kvheads, max_seq;
+  const float *co, *si;  // RoPE tables [max_seq x hd/2]
+  const int32_t *pos;    // device position (one for every row of the batch)
+  uint16_t *kc, *vc;
+  // EPI_ARGMAX: per wave (max, index), [seq x ceil(out/R)]
+  float *pval;
+  int32_t *pidx;
+  uint32_t nparts;
+};
+// Launch the fused kernel; rows_per_wave 0 picks a default.  Requires
+// cols % 64 == 0, cols <= 16384 and 16-byte aligned x and w2.
+int nlg_fused_launch(const FusedArgs &a, int pro, int epi, int rows_per_wave, hipStream_t st);
+// The rows-per-wave the launcher uses for `out` rows in mode `epi`.
+int nlg_fused_rows_per_wave(uint32_t out, int epi);
+
 // ---------------------------------------------------------------- launchers
 // One per kernel name (Appendix A of the survey, lisp/nelisp-gpu-kernels.el).
 #define NLG_DECL(fn) int fn(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st)

@@ -1,0 +1,640 @@
+// nlg_layer.hip -- the decoder layer's fused kernels.
+//
+// k_tern_fused: one launch per ternary linear of a decode step.  Each
+// workgroup (4 waves, R output rows per wave) issues its weight loads first,
+// then -- while they are in flight -- optionally RMS-normalises the token's
+// activation row, quantises it exactly as pack-act-rows does into LDS, dots
+// its rows against it, and finishes with one of these epilogues:
+//
+//   STORE   Y = BIAS + (BETA*GAMMA)*acc            bitlinear-dp4a-1f (kernels.el:619-634)
+//   RESID   X = X + that                           add2 (kernels.el:812-821)
+//   SWIGLU  rows 2j/2j+1 are gate/up row j:        silu-mul (kernels.el:186-193)
+//           H[j] = (g * 1/(1+exp(0-g))) * u
+//   QKV     rows are q | k | v: RoPE on q and k    decode-rope(-b) (kernels.el:291-306, :340-355)
+//           at the device position, k and v        cache-append(-b) (kernels.el:307-314, :356-365)
+//           appended to fp16 caches
+//   ARGMAX  logits, plus (max, first index) per wave for greedy sampling
+//
+// The RMSNorm prologue is rmsnorm-istd + rmsnorm-fwd (kernels.el:1249-1265)
+// with the epsilon a parameter: S = 1/sqrt(sum(x*x)/N + eps), C = (X*S)*G.
+// Its sum is a tree, not the reference's serial loop, so S can differ from
+// the reference in the last bit; everything after it is the reference's
+// arithmetic.
+//
+// k_attn_f16: single-query GQA attention over fp16 KV caches, split over
+// 64-position chunks (decode-attn(-b), kernels.el:315-338, :366-390: scale
+// 1/sqrt(hd), max seeded at -1e30, C = sum(e*V)/sum(e)).  Each workgroup
+// handles one (sequence, kv head, chunk) for all the query heads of that kv
+// head, so K and V are read from HBM once; the last workgroup of a (sequence,
+// kv head) to finish merges the chunks (a completion counter, no waiting).
+#include <math.h>
+
+#include "nlg_quant.h"
+
+// ------------------------------------------------------------ fused GEMV
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+  return __builtin_bit_cast(uint16_t, (_Float16)v);  // round to nearest even
+}
+// fp16 element e (0..7) of eight packed in a uint4, as f32 (exact)
+__device__ __forceinline__ float f16x8_at(const uint4 &u, int e) {
+  const uint32_t w = e < 2 ? u.x : e < 4 ? u.y : e < 6 ? u.z : u.w;
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu)));
+}
+
+// F4: float4s of the activation row per thread (cols <= 1024*F4).
+template <int R, int CPL, int F4, int PRO, int EPI>
+__global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
+  extern __shared__ uint4 s_xq4[];  // cols/16 uint4 = cols int8 lanes
+  __shared__ float red[4];
+  const int lane = threadIdx.x & 63, wvi = threadIdx.x >> 6;
+  const uint32_t tok = blockIdx.y;
+  const uint32_t wave = blockIdx.x * 4 + wvi;
+  const uint32_t row0 = wave * R;
+  const uint32_t nchunk = a.wng >> 2;
+  // 1. every global load is issued up front, activation first: vmcnt retires
+  //    in issue order, so waiting for x must not also wait for the weights'
+  //    HBM fetch, which stays in flight through the quantisation below.  The
+  //    loads are straight-line (clamped addresses, validity applied with
+  //    selects afterwards): a branch around a load makes the wait-count pass
+  //    drain every outstanding load at the join.
+  const float4 *x4 = (const float4 *)(a.x + (size_t)tok * a.cols);
+  const uint32_t nf4 = a.cols >> 2;
+  float4 xv4[F4], gv4[F4];
+#pragma unroll
+  for (int k = 0; k < F4; k++) {
+    const uint32_t f = threadIdx.x + 256u * k;
+    xv4[k] = x4[f < nf4 ? f : nf4 - 1];
+  }
+  if (PRO == NLG_PRO_RMS) {
+    const float4 *g4 = (const float4 *)a.gain;
+#pragma unroll
+    for (int k = 0; k < F4; k++) {
+      const uint32_t f = threadIdx.x + 256u * k;
+      gv4[k] = g4[f < nf4 ? f : nf4 - 1];
+    }
+  }
+  uint4 wv[R][CPL];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const uint32_t row = row0 + r < a.out ? row0 + r : a.out - 1;
+    const uint4 *wr = (const uint4 *)(a.w2 + (size_t)row * a.wng);
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+      const uint32_t c = lane + 64 * i;
+      wv[r][i] = wr[c < nchunk ? c : nchunk - 1];
+    }
+  }
+  const uint32_t orow_u = row0 + (lane < R ? lane : 0);
+  const uint32_t orow = orow_u < a.out ? orow_u : a.out - 1;  // every lane loads a valid row
+  const bool olive = lane < R && orow_u < a.out;
+  const float *bsrc = a.bias ? a.bias : a.beta;  // a real address either way
+  const float bo_raw = bsrc[a.bias ? orow : 0];
+  const float be = a.beta[a.beta_per_row ? orow : 0];
+  const float bo = a.bias ? bo_raw : 0.0f;
+  float rv = 0.0f;
+  if (EPI == NLG_EPI_RESID) rv = a.res[(size_t)tok * a.rstride + orow];
+  // QKV: this lane's row is q, k or v; RoPE pair m of head dimension dd
+  float cc = 0.0f, ss = 0.0f;
+  uint32_t dd = 0, p = 0;
+  bool pos_ok = false;
+  if (EPI == NLG_EPI_QKV) {
+    const int32_t pr = a.pos[0];
+    pos_ok = pr >= 0 && (uint32_t)pr < a.max_seq;
+    p = pos_ok ? (uint32_t)pr : 0u;
+    const uint32_t sec = orow < a.nq ? orow : (orow < a.nq + a.nkv ? orow - a.nq : orow - a.nq - a.nkv);
+    dd = sec % a.hd;
+    const uint32_t half = a.hd >> 1, ci = p * half + (dd >> 1);
+    cc = a.co[ci];
+    ss = a.si[ci];  // SG[0] = +1: SI*SG is SI exactly
+  }
+#pragma unroll
+  for (int k = 0; k < F4; k++)
+    if (threadIdx.x + 256u * k >= nf4) xv4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int i = 0; i < CPL; i++)
+      if (lane + 64u * i >= nchunk) wv[r][i] = make_uint4(0, 0, 0, 0);
+  // 2. RMSNorm: S = 1/sqrt(sum(x*x)/N + eps); C = (X*S)*G
+  if (PRO == NLG_PRO_RMS) {
+    float sq = 0.0f;
+#pragma unroll
+    for (int k = 0; k < F4; k++) {
+      sq = sq + xv4[k].x * xv4[k].x;
+      sq = sq + xv4[k].y * xv4[k].y;
+      sq = sq + xv4[k].z * xv4[k].z;
+      sq = sq + xv4[k].w * xv4[k].w;
+    }
+    sq = nlg_block_sum_f32(sq, red);
+    sq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq)));
+    const float istd = 1.0f / sqrtf(sq / (float)a.cols + a.eps);
+#pragma unroll
+    for (int k = 0; k < F4; k++) {
+      xv4[k].x = (xv4[k].x * istd) * gv4[k].x;
+      xv4[k].y = (xv4[k].y * istd) * gv4[k].y;
+      xv4[k].z = (xv4[k].z * istd) * gv4[k].z;
+      xv4[k].w = (xv4[k].w * istd) * gv4[k].w;
+    }
+  }
+  // 3. amax of the token's row (every thread takes part: barriers follow)
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < F4; k++) {
+    float t;
+    t = dsl_abs(xv4[k].x); amax = t > amax ? t : amax;
+    t = dsl_abs(xv4[k].y); amax = t > amax ? t : amax;
+    t = dsl_abs(xv4[k].z); amax = t > amax ? t : amax;
+    t = dsl_abs(xv4[k].w); amax = t > amax ? t : amax;
+  }
+  amax = nlg_block_max_f32(amax, red);
+  const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
+  const float ginv = 1.0f / g;
+  if (a.gamma_out && blockIdx.x == 0 && threadIdx.x == 0) a.gamma_out[tok] = g;
+  // 4. quantise into LDS, one packed word per float4 (exact; see lane_est)
+  const bool fast = g > 0.0f && ginv < INFINITY;
+  uint32_t *s_xq = (uint32_t *)s_xq4;
+#pragma unroll
+  for (int k = 0; k < F4; k++) {
+    const uint32_t f = threadIdx.x + 256u * k;
+    const uint32_t wd = quant_word(xv4[k], g, ginv, fast);
+    if (f < nf4) s_xq[f] = wd;
+  }
+  __syncthreads();
+  if (row0 >= a.out) return;  // wave-uniform, after the last barrier
+  // 5. dots against the LDS activation
+  int acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) acc[r] = 0;
+#pragma unroll
+  for (int i = 0; i < CPL; i++) {
+    const uint32_t c = lane + 64 * i;
+    if (c < nchunk) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint4 xv = s_xq4[4 * c + j];
+        uint32_t y0, y1, y2, y3;
+        xpose4(xv.x, xv.y, xv.z, xv.w, y0, y1, y2, y3);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          const uint32_t w = j == 0 ? wv[r][i].x : j == 1 ? wv[r][i].y : j == 2 ? wv[r][i].z : wv[r][i].w;
+          acc[r] = wdot(w, y0, y1, y2, y3, acc[r]);
+        }
+      }
+    }
+  }
+  // 6. reduce; lane r takes row r's exact accumulator
+  int tl = 0;
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int tot = nlg_wave_sum_i32(acc[r]);
+    tl = lane == r ? tot : tl;
+  }
+  // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
+  const float val = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, g), (float)(tl >> 6)));
+  if (EPI == NLG_EPI_STORE || EPI == NLG_EPI_ARGMAX) {
+    if (olive) a.y[(size_t)tok * a.ystride + orow] = val;
+  }
+  if (EPI == NLG_EPI_RESID) {
+    if (olive) a.y[(size_t)tok * a.ystride + orow] = __fadd_rn(rv, val);
+  }
+  if (EPI == NLG_EPI_SWIGLU || EPI == NLG_EPI_QKV) {
+    // the other row of the pair (lane ^ 1)
+    const float pv = __int_as_float(nlg_dpp<0xB1>(__float_as_int(val)));
+    if (EPI == NLG_EPI_SWIGLU) {
+      if (olive && !(lane & 1)) {
+        const float sg = 1.0f / (1.0f + expf(0.0f - val));
+        a.y[(size_t)tok * a.ystride + (orow >> 1)] = (val * sg) * pv;
+      }
+    } else if (olive) {
+      // decode-rope: C[i0] = a0*cc - a1*ss; C[i1] = a0*ss + a1*cc
+      const bool odd = lane & 1;
+      const float a0 = odd ? pv : val, a1 = odd ? val : pv;
+      const float rot = odd ? __fadd_rn(__fmul_rn(a0, ss), __fmul_rn(a1, cc))
+                            : __fsub_rn(__fmul_rn(a0, cc), __fmul_rn(a1, ss));
+      if (orow < a.nq) {
+        a.y[(size_t)tok * a.ystride + orow] = rot;
+      } else if (pos_ok) {
+        const bool isk = orow < a.nq + a.nkv;
+        const uint32_t sec = isk ? orow - a.nq : orow - a.nq - a.nkv;
+        const uint32_t kh = sec / a.hd;
+        const size_t at = (((size_t)tok * a.kvheads + kh) * a.max_seq + p) * a.hd + dd;
+        if (isk) a.kc[at] = f32_to_f16_bits(rot);
+        else a.vc[at] = f32_to_f16_bits(val);
+      }
+    }
+  }
+  if (EPI == NLG_EPI_ARGMAX) {
+    // first maximum of the wave's rows (NaN never wins)
+    float bv = -INFINITY;
+    int32_t bi = -1;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(val), r));
+      if (row0 + r < a.out && (bi < 0 ? v == v : v > bv)) {
+        bv = v;
+        bi = (int32_t)(row0 + r);
+      }
+    }
+    if (lane == 0) {
+      a.pval[(size_t)tok * a.nparts + wave] = bv;
+      a.pidx[(size_t)tok * a.nparts + wave] = bi;
+    }
+  }
+}
+
+int nlg_fused_rows_per_wave(uint32_t out, int epi) {
+  if (epi == NLG_EPI_ARGMAX) return out >= 32768 ? 8 : 4;
+  if (epi == NLG_EPI_SWIGLU || epi == NLG_EPI_QKV) return out >= 2048 ? 4 : 2;
+  // Each workgroup quantises the whole row, so fewer, fatter workgroups
+  // waste less; about one per CU measured best at 4096 rows (4.3 us).
+  return out >= 4096 ? 4 : (out >= 2048 ? 2 : 1);
+}
+
+template <int PRO, int EPI, int R>
+static void fused_go(const FusedArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+  const uint32_t nchunk = a.wng / 4;
+  const dim3 blk(256);
+#define FZ(CC)                                                                                  \
+  do {                                                                                          \
+    if (a.cols <= 2048) hipLaunchKernelGGL((k_tern_fused<R, CC, 2, PRO, EPI>), grid, blk, lds, st, a); \
+    else if (a.cols <= 4096) hipLaunchKernelGGL((k_tern_fused<R, CC, 4, PRO, EPI>), grid, blk, lds, st, a); \
+    else if (a.cols <= 8192) hipLaunchKernelGGL((k_tern_fused<R, CC, 8, PRO, EPI>), grid, blk, lds, st, a); \
+    else hipLaunchKernelGGL((k_tern_fused<R, CC, 16, PRO, EPI>), grid, blk, lds, st, a);       \
+  } while (0)
+  if (nchunk <= 64) FZ(1);
+  else if (nchunk <= 128) FZ(2);
+  else FZ(4);
+#undef FZ
+}
+
+int nlg_fused_launch(const FusedArgs &a0, int pro, int epi, int rpw, hipStream_t st) {
+  FusedArgs a = a0;
+  if (!a.seq || !a.out) return NLG_OK;
+  if (a.cols % 64 || a.cols > 16384 || !a.cols)
+    return nlg_fail("fused ternary linear: cols must be a multiple of 64 in [64, 16384] (got %u)", a.cols);
+  if (((uintptr_t)a.x & 15) || ((uintptr_t)a.w2 & 15) || (pro == NLG_PRO_RMS && ((uintptr_t)a.gain & 15)))
+    return nlg_fail("fused ternary linear: x, w2 and gain must be 16-byte aligned");
+  if (a.seq > 65535) return nlg_fail("fused ternary linear: seq %u > 65535", a.seq);
+  a.wng = a.cols / 16;
+  if (rpw <= 0) rpw = nlg_fused_rows_per_wave(a.out, epi);
+  if ((epi == NLG_EPI_SWIGLU || epi == NLG_EPI_QKV) && (rpw < 2 || a.out % 2))
+    return nlg_fail("fused ternary linear: paired epilogues need an even row count");
+  const size_t lds = (size_t)a.cols;  // one byte per column
+  const dim3 grid(nlg_blocks(a.out, 4u * rpw), a.seq);
+  // one (max, index) per wave that has rows
+  if (epi == NLG_EPI_ARGMAX) a.nparts = (a.out + rpw - 1) / rpw;
+#define PE(P, E)                                          \
+  do {                                                    \
+    switch (rpw) {                                        \
+      case 1: fused_go<P, E, 1>(a, grid, lds, st); break; \
+      case 2: fused_go<P, E, 2>(a, grid, lds, st); break; \
+      case 8: fused_go<P, E, 8>(a, grid, lds, st); break; \
+      default: fused_go<P, E, 4>(a, grid, lds, st); break; \
+    }                                                     \
+  } while (0)
+  if (rpw != 1 && rpw != 2 && rpw != 4 && rpw != 8) return nlg_fail("rows_per_wave must be 1, 2, 4 or 8");
+  if (pro == NLG_PRO_NONE && epi == NLG_EPI_STORE) PE(NLG_PRO_NONE, NLG_EPI_STORE);
+  else if (pro == NLG_PRO_RMS && epi == NLG_EPI_STORE) PE(NLG_PRO_RMS, NLG_EPI_STORE);
+  else if (pro == NLG_PRO_NONE && epi == NLG_EPI_RESID) PE(NLG_PRO_NONE, NLG_EPI_RESID);
+  else if (pro == NLG_PRO_RMS && epi == NLG_EPI_SWIGLU) PE(NLG_PRO_RMS, NLG_EPI_SWIGLU);
+  else if (pro == NLG_PRO_RMS && epi == NLG_EPI_QKV) PE(NLG_PRO_RMS, NLG_EPI_QKV);
+  else if (pro == NLG_PRO_RMS && epi == NLG_EPI_ARGMAX) PE(NLG_PRO_RMS, NLG_EPI_ARGMAX);
+  else return nlg_fail("fused ternary linear: unsupported prologue/epilogue %d/%d", pro, epi);
+#undef PE
+  NLG_LAUNCHED("fused ternary linear");
+  return NLG_OK;
+}
+
+// ------------------------------------------------------ public entry points
+
+extern "C" int nlg_rms_ternary_linear(const float *x, const float *gain, float eps, const uint32_t *w2,
+                                      const float *bias, const float *beta, int beta_per_row, float *y,
+                                      uint32_t seq, uint32_t out, uint32_t cols, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  FusedArgs a{};
+  a.x = x; a.gain = gain; a.eps = eps; a.w2 = w2; a.bias = bias; a.beta = beta;
+  a.beta_per_row = beta_per_row; a.seq = seq; a.out = out; a.cols = cols;
+  a.y = y; a.ystride = out;
+  return nlg_fused_launch(a, NLG_PRO_RMS, NLG_EPI_STORE, 0, nlg_stream(stream));
+}
+
+extern "C" int nlg_ternary_linear_residual(const float *x, const uint32_t *w2, const float *bias,
+                                           const float *beta, int beta_per_row, const float *res,
+                                           float *y, uint32_t seq, uint32_t out, uint32_t cols,
+                                           void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!res) return nlg_fail("ternary linear residual: res is null");
+  FusedArgs a{};
+  a.x = x; a.w2 = w2; a.bias = bias; a.beta = beta; a.beta_per_row = beta_per_row;
+  a.seq = seq; a.out = out; a.cols = cols; a.y = y; a.ystride = out; a.res = res; a.rstride = out;
+  return nlg_fused_launch(a, NLG_PRO_NONE, NLG_EPI_RESID, 0, nlg_stream(stream));
+}
+
+extern "C" int nlg_rms_ternary_swiglu(const float *x, const float *gain, float eps, const uint32_t *w2gu,
+                                      const float *beta, int beta_per_row, float *h, uint32_t seq,
+                                      uint32_t dff, uint32_t cols, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  FusedArgs a{};
+  a.x = x; a.gain = gain; a.eps = eps; a.w2 = w2gu; a.beta = beta; a.beta_per_row = beta_per_row;
+  a.seq = seq; a.out = 2 * dff; a.cols = cols; a.y = h; a.ystride = dff;
+  return nlg_fused_launch(a, NLG_PRO_RMS, NLG_EPI_SWIGLU, 0, nlg_stream(stream));
+}
+
+extern "C" int nlg_rms_ternary_qkv_rope(const float *x, const float *gain, float eps, const uint32_t *w2qkv,
+                                        const float *beta, int beta_per_row, float *q, uint16_t *kcache,
+                                        uint16_t *vcache, const float *rope_cos, const float *rope_sin,
+                                        const int32_t *pos, uint32_t seq, uint32_t heads,
+                                        uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
+                                        uint32_t cols, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!heads || !kvheads || !head_dim || head_dim % 2 || !max_seq)
+    return nlg_fail("qkv: heads, kvheads, max_seq must be nonzero and head_dim even");
+  FusedArgs a{};
+  a.x = x; a.gain = gain; a.eps = eps; a.w2 = w2qkv; a.beta = beta; a.beta_per_row = beta_per_row;
+  a.seq = seq; a.nq = heads * head_dim; a.nkv = kvheads * head_dim; a.out = a.nq + 2 * a.nkv;
+  a.cols = cols; a.y = q; a.ystride = a.nq; a.hd = head_dim; a.kvheads = kvheads; a.max_seq = max_seq;
+  a.co = rope_cos; a.si = rope_sin; a.pos = pos; a.kc = kcache; a.vc = vcache;
+  if (a.nq % 4 || a.nkv % 4) return nlg_fail("qkv: heads*head_dim and kvheads*head_dim must be multiples of 4");
+  return nlg_fused_launch(a, NLG_PRO_RMS, NLG_EPI_QKV, 0, nlg_stream(stream));
+}
+
+// ------------------------------------------------------------ sampling
+
+// Greedy choice over the LM head's per-wave (max, index) pairs: the largest
+// logit, the lowest index among equals; -1 marks a wave with no candidate.
+__device__ __forceinline__ bool cand_better(float v, int32_t i, float bv, int32_t bi) {
+  if (i < 0) return false;
+  if (bi < 0) return true;
+  return v > bv || (v == bv && i < bi);
+}
+
+__device__ void block_argmax(float &v, int32_t &i, float *sv, int32_t *si) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(v, off);
+    const int32_t oi = __shfl_xor(i, off);
+    if (cand_better(ov, oi, v, i)) { v = ov; i = oi; }
+  }
+  const int nw = blockDim.x >> 6, w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) { sv[w] = v; si[w] = i; }
+  __syncthreads();
+  v = sv[0]; i = si[0];
+  for (int k = 1; k < nw; k++)
+    if (cand_better(sv[k], si[k], v, i)) { v = sv[k]; i = si[k]; }
+}
+
+__global__ __launch_bounds__(1024) void k_argmax_parts(const float *pval, const int32_t *pidx,
+                                                       uint32_t nparts, int32_t *out) {
+  __shared__ float sv[16];
+  __shared__ int32_t si[16];
+  const uint32_t t = blockIdx.x;
+  float v = -INFINITY;
+  int32_t i = -1;
+  for (uint32_t j = threadIdx.x; j < nparts; j += blockDim.x) {
+    const float ov = pval[(size_t)t * nparts + j];
+    const int32_t oi = pidx[(size_t)t * nparts + j];
+    if (cand_better(ov, oi, v, i)) { v = ov; i = oi; }
+  }
+  block_argmax(v, i, sv, si);
+  if (threadIdx.x == 0) out[t] = i;
+}
+
+extern "C" size_t nlg_rms_ternary_argmax_workspace(uint32_t seq, uint32_t vocab) {
+  const int rpw = nlg_fused_rows_per_wave(vocab, NLG_EPI_ARGMAX);
+  const size_t nparts = (vocab + rpw - 1) / rpw;
+  return seq * nparts * 8;
+}
+
+extern "C" int nlg_rms_ternary_argmax(const float *x, const float *gain, float eps, const uint32_t *w2,
+                                      const float *beta, int beta_per_row, float *logits,
+                                      int32_t *argmax, uint32_t seq, uint32_t vocab, uint32_t cols,
+                                      void *workspace, size_t workspace_bytes, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!seq || !vocab) return NLG_OK;
+  const size_t need = nlg_rms_ternary_argmax_workspace(seq, vocab);
+  if (!workspace || workspace_bytes < need)
+    return nlg_fail("rms ternary argmax: needs a %zu-byte workspace", need);
+  hipStream_t st = nlg_stream(stream);
+  const int rpw = nlg_fused_rows_per_wave(vocab, NLG_EPI_ARGMAX);
+  const uint32_t nparts = (vocab + rpw - 1) / rpw;
+  FusedArgs a{};
+  a.x = x; a.gain = gain; a.eps = eps; a.w2 = w2; a.beta = beta; a.beta_per_row = beta_per_row;
+  a.seq = seq; a.out = vocab; a.cols = cols; a.y = logits; a.ystride = vocab;
+  a.pval = (float *)workspace;
+  a.pidx = (int32_t *)((char *)workspace + (size_t)seq * nparts * 4);
+  if (nlg_fused_launch(a, NLG_PRO_RMS, NLG_EPI_ARGMAX, rpw, st)) return NLG_ERR;
+  hipLaunchKernelGGL(k_argmax_parts, dim3(seq), dim3(1024), 0, st, a.pval, a.pidx, nparts, argmax);
+  NLG_LAUNCHED("argmax");
+  return NLG_OK;
+}
+
+// -------------------------------------------------- fp16 decode attention
+
+struct AttnArgs {
+  const float *q;           // [B x heads*hd]
+  const uint16_t *kc, *vc;  // [B][kvheads][max_seq][hd] fp16 bits
+  const int32_t *pos;       // attend positions 0..pos[0]
+  float *out;               // [B x heads*hd]
+  float *part;              // [B][kvheads][nchunk][G][2 + hd]
+  int32_t *cnt;             // [B][kvheads], zero between launches
+  uint32_t heads, kvheads, max_seq, nchunk;
+  float coef;               // 1/sqrt(hd)
+};
+
+// Sum over aligned groups of L lanes (L = 8 or 16); every lane gets its
+// group's sum.
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+  v = v + __int_as_float(nlg_dpp<0xB1>(__float_as_int(v)));   // quad_perm [1,0,3,2]
+  v = v + __int_as_float(nlg_dpp<0x4E>(__float_as_int(v)));   // quad_perm [2,3,0,1]
+  v = v + __int_as_float(nlg_dpp<0x141>(__float_as_int(v)));  // row_half_mirror
+  if (L == 16) v = v + __int_as_float(nlg_dpp<0x140>(__float_as_int(v)));  // row_mirror
+  return v;
+}
+
+// HD = head dim (64 or 128), G = query heads per kv head.  Lanes hold 8
+// dimensions of one position: LPP = HD/8 lanes per position, PPI = 64/LPP
+// positions per wave instruction, NI = 16/PPI instructions for the wave's 16
+// positions of the workgroup's 64.
+template <int HD, int G>
+__global__ __launch_bounds__(256) void k_attn_f16(AttnArgs a) {
+  constexpr int LPP = HD / 8, PPI = 64 / LPP, NI = 16 / PPI, PSTR = 2 + HD;
+  __shared__ float s_m[4][G], s_z[4][G];
+  __shared__ float s_ctx[4][G][HD];
+  __shared__ int s_last;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint32_t c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int32_t pr = a.pos[0];
+  const uint32_t len = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
+  const uint32_t nvalid = (len + 63) / 64;
+  const size_t slot = (size_t)b * a.kvheads + kvh;
+  if (c < nvalid) {
+    const int d0 = 8 * (lane % LPP), grp = lane / LPP;
+    const float *qb = a.q + (size_t)b * a.heads * HD + (size_t)kvh * G * HD + d0;
+    const uint16_t *kb = a.kc + slot * a.max_seq * HD + d0;
+    const uint16_t *vb = a.vc + slot * a.max_seq * HD + d0;
+    uint4 kr[NI], vr[NI];
+    uint32_t pp[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      pp[i] = c * 64 + w * 16 + i * PPI + grp;
+      const uint32_t pc = pp[i] < len ? pp[i] : len - 1;
+      kr[i] = *(const uint4 *)(kb + (size_t)pc * HD);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const uint32_t pc = pp[i] < len ? pp[i] : len - 1;
+      vr[i] = *(const uint4 *)(vb + (size_t)pc * HD);
+    }
+    float q[G][8];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      const float4 q0 = *(const float4 *)(qb + h * HD), q1 = *(const float4 *)(qb + h * HD + 4);
+      q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
+      q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
+    }
+    float s[NI][G];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+#pragma unroll
+      for (int h = 0; h < G; h++) {
+        float d = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) d = fmaf(q[h][j], f16x8_at(kr[i], j), d);
+        d = group_sum<LPP>(d);
+        s[i][h] = pp[i] < len ? d * a.coef : -INFINITY;
+      }
+    }
+    float m[G], z[G], ctx[G][8];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      float mm = -1.0e30f;
+#pragma unroll
+      for (int i = 0; i < NI; i++) mm = s[i][h] > mm ? s[i][h] : mm;
+      for (int off = LPP; off < 64; off <<= 1) {
+        const float o = __shfl_xor(mm, off);
+        mm = o > mm ? o : mm;
+      }
+      m[h] = mm;
+      z[h] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; j++) ctx[h][j] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+#pragma unroll
+      for (int h = 0; h < G; h++) {
+        const float e = expf(s[i][h] - m[h]);
+        z[h] = z[h] + e;
+#pragma unroll
+        for (int j = 0; j < 8; j++) ctx[h][j] = fmaf(e, f16x8_at(vr[i], j), ctx[h][j]);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      for (int off = LPP; off < 64; off <<= 1) {
+        z[h] = z[h] + __shfl_xor(z[h], off);
+#pragma unroll
+        for (int j = 0; j < 8; j++) ctx[h][j] = ctx[h][j] + __shfl_xor(ctx[h][j], off);
+      }
+      if (grp == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) s_ctx[w][h][d0 + j] = ctx[h][j];
+      }
+      if (lane == 0) {
+        s_m[w][h] = m[h];
+        s_z[w][h] = z[h];
+      }
+    }
+  }
+  __syncthreads();
+  if (c < nvalid) {
+    float *part = a.part + (slot * a.nchunk + c) * (size_t)(G * PSTR);
+    for (int idx = threadIdx.x; idx < G * HD; idx += 256) {
+      const int h = idx / HD, d = idx % HD;
+      float mm = s_m[0][h];
+      for (int k = 1; k < 4; k++) mm = s_m[k][h] > mm ? s_m[k][h] : mm;
+      float zz = 0.0f, cx = 0.0f;
+      for (int k = 0; k < 4; k++) {
+        const float sc = expf(s_m[k][h] - mm);
+        zz = fmaf(s_z[k][h], sc, zz);
+        cx = fmaf(s_ctx[k][h][d], sc, cx);
+      }
+      part[h * PSTR + 2 + d] = cx;
+      if (d == 0) {
+        part[h * PSTR] = mm;
+        part[h * PSTR + 1] = zz;
+      }
+    }
+  }
+  // completion: the last workgroup of this (sequence, kv head) merges chunks
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = atomicAdd(&a.cnt[slot], 1) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  const float *pb = a.part + slot * a.nchunk * (size_t)(G * PSTR);
+  for (int idx = threadIdx.x; idx < G * HD; idx += 256) {
+    const int h = idx / HD, d = idx % HD;
+    float mm = -1.0e30f;
+    for (uint32_t k = 0; k < nvalid; k++) {
+      const float mk = pb[(size_t)k * G * PSTR + h * PSTR];
+      mm = mk > mm ? mk : mm;
+    }
+    float zz = 0.0f, cx = 0.0f;
+    for (uint32_t k = 0; k < nvalid; k++) {
+      const float *ck = pb + (size_t)k * G * PSTR + h * PSTR;
+      const float sc = expf(ck[0] - mm);
+      zz = fmaf(ck[1], sc, zz);
+      cx = fmaf(ck[2 + d], sc, cx);
+    }
+    a.out[(size_t)b * a.heads * HD + ((size_t)kvh * G + h) * HD + d] = cx / zz;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&a.cnt[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+extern "C" size_t nlg_decode_attn_f16_workspace(uint32_t batch, uint32_t heads, uint32_t kvheads,
+                                                uint32_t head_dim, uint32_t max_seq) {
+  if (!kvheads) return 0;
+  const size_t nchunk = (max_seq + 63) / 64, G = heads / kvheads;
+  const size_t part = (size_t)batch * kvheads * nchunk * G * (2 + head_dim) * 4;
+  return (part + 255) / 256 * 256 + (size_t)batch * kvheads * 4;
+}
+
+extern "C" int nlg_decode_attn_f16(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                                   const int32_t *pos, float *out, uint32_t batch, uint32_t heads,
+                                   uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
+                                   void *workspace, size_t workspace_bytes, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!batch) return NLG_OK;
+  if (!kvheads || !heads || heads % kvheads) return nlg_fail("decode attn: heads must be a multiple of kvheads");
+  const uint32_t G = heads / kvheads;
+  if (head_dim != 64 && head_dim != 128) return nlg_fail("decode attn: head_dim must be 64 or 128");
+  if (G != 1 && G != 2 && G != 4 && G != 8) return nlg_fail("decode attn: heads/kvheads must be 1, 2, 4 or 8");
+  if (!max_seq || batch > 65535 || kvheads > 65535) return nlg_fail("decode attn: bad max_seq/batch/kvheads");
+  if (((uintptr_t)q & 15) || ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15))
+    return nlg_fail("decode attn: q and caches must be 16-byte aligned");
+  const size_t need = nlg_decode_attn_f16_workspace(batch, heads, kvheads, head_dim, max_seq);
+  if (!workspace || workspace_bytes < need) return nlg_fail("decode attn: needs a %zu-byte workspace", need);
+  AttnArgs a;
+  a.q = q; a.kc = kcache; a.vc = vcache; a.pos = pos; a.out = out;
+  a.nchunk = (max_seq + 63) / 64;
+  a.part = (float *)workspace;
+  const size_t part = (size_t)batch * kvheads * a.nchunk * G * (2 + head_dim) * 4;
+  a.cnt = (int32_t *)((char *)workspace + (part + 255) / 256 * 256);
+  a.heads = heads; a.kvheads = kvheads; a.max_seq = max_seq;
+  a.coef = 1.0f / sqrtf((float)head_dim);  // (/ 1.0 (sqrt (float hd)))
+  const dim3 grid(a.nchunk, kvheads, batch), blk(256);
+  hipStream_t st = nlg_stream(stream);
+#define AT(HD, GG) hipLaunchKernelGGL((k_attn_f16<HD, GG>), grid, blk, 0, st, a)
+  if (head_dim == 128) {
+    if (G == 1) AT(128, 1); else if (G == 2) AT(128, 2); else if (G == 4) AT(128, 4); else AT(128, 8);
+  } else {
+    if (G == 1) AT(64, 1); else if (G == 2) AT(64, 2); else if (G == 4) AT(64, 4); else AT(64, 8);
+  }
+#undef AT
+  NLG_LAUNCHED("decode attention (fp16 KV)");
+  return NLG_OK;
+}

@@ -19,77 +19,9 @@
 // 16 columns, done once per wave and reused for every row).  The int32 sum
 // is therefore 64x the exact accumulator and `>> 6` recovers it exactly;
 // the fp32 epilogue is bitlinear-dp4a-1f's, evaluated without contraction.
-#include "nlg_internal.h"
+#include "nlg_quant.h"
 
 // ------------------------------------------------------------ quantisation
-
-// |v| as the DSL computes it: (when (< v 0.0) (set av (- 0.0 v))).
-__device__ __forceinline__ float dsl_abs(float v) { return v < 0.0f ? 0.0f - v : v; }
-
-// One lane of pack-act-rows (kernels.el:912-926): returns the stored byte.
-__device__ __forceinline__ uint32_t pack_lane(float v, float gamma) {
-  float q = 0.0f;
-  if (gamma > 0.0f) q = v / gamma;
-  uint32_t neg = 0;
-  float aq = q;
-  if (q < 0.0f) {
-    neg = 1;
-    aq = 0.0f - q;
-  }
-  uint32_t ri = nlg_f2u(aq + 0.5f);
-  if (ri > 127u) ri = 127u;
-  return neg ? (256u - ri) % 256u : ri;
-}
-
-// ---- exact quantisation without a division per element ----
-//
-// pack-act-rows' lane magnitude is ri = min(trunc(t'), 127) with
-// t' = RN(RN(|v|/gamma) + 0.5).  With ginv = RN(1/gamma) finite, the estimate
-// t = RN(RN(|v|*ginv) + 0.5) differs from t' by less than 4e-5 whenever
-// t < 128 (the reciprocal, the product and the quotient each err by at most
-// 2^-24 relative on a value below 128.5, plus half an ulp of the final add),
-// so trunc(t) == trunc(t') unless t lies within 2^-13 of an integer; and
-// t >= 128 means t' > 127.99, which the clamp maps to 127 either way.  The
-// few elements that fall inside that band (and NaNs) are recomputed with the
-// reference's IEEE division.  |v|/gamma = |v/gamma| under round-to-nearest,
-// and a nonzero lane implies |v/gamma| >= 0.5, so the sign is v's.
-__device__ __forceinline__ uint32_t lane_est(float v, float ginv, bool &near) {
-  const float t = __fadd_rn(__fmul_rn(fabsf(v), ginv), 0.5f);
-  const float kf = truncf(t), fr = t - kf;
-  const bool big = t >= 128.0f;
-  near = !(big || (fr >= 0x1p-13f && fr <= 1.0f - 0x1p-13f));  // NaN lands here
-  const uint32_t k = big ? 127u : (uint32_t)kf;
-  return v < 0.0f ? (256u - k) & 255u : k;
-}
-// Packed word of four lanes; `near` gets one bit per lane that needs the
-// exact path.
-__device__ __forceinline__ uint32_t word_est(float4 v, float ginv, uint32_t &near) {
-  bool n0, n1, n2, n3;
-  const uint32_t w = lane_est(v.x, ginv, n0) | (lane_est(v.y, ginv, n1) << 8) |
-                     (lane_est(v.z, ginv, n2) << 16) | (lane_est(v.w, ginv, n3) << 24);
-  near = (n0 ? 1u : 0u) | (n1 ? 2u : 0u) | (n2 ? 4u : 0u) | (n3 ? 8u : 0u);
-  return w;
-}
-// Replace the flagged lanes of a word with the reference's own computation.
-__device__ __forceinline__ uint32_t word_fix(uint32_t w, float4 v, float gamma, uint32_t near) {
-  if (near & 1u) w = (w & 0xFFFFFF00u) | pack_lane(v.x, gamma);
-  if (near & 2u) w = (w & 0xFFFF00FFu) | (pack_lane(v.y, gamma) << 8);
-  if (near & 4u) w = (w & 0xFF00FFFFu) | (pack_lane(v.z, gamma) << 16);
-  if (near & 8u) w = (w & 0x00FFFFFFu) | (pack_lane(v.w, gamma) << 24);
-  return w;
-}
-// The packed word pack-act-rows stores for v.  `fast` (1/gamma finite and
-// gamma > 0) is uniform across the block.  The exact fix-up sits behind a
-// wave-uniform vote, so a wave with no flagged lane skips it entirely.
-__device__ __forceinline__ uint32_t quant_word(float4 v, float gamma, float ginv, bool fast) {
-  if (!fast)
-    return pack_lane(v.x, gamma) | (pack_lane(v.y, gamma) << 8) | (pack_lane(v.z, gamma) << 16) |
-           (pack_lane(v.w, gamma) << 24);
-  uint32_t near;
-  uint32_t w = word_est(v, ginv, near);
-  if (__builtin_amdgcn_ballot_w64(near != 0u) != 0ull) w = word_fix(w, v, gamma, near);
-  return w;
-}
 
 // One workgroup per row.  Pass 1: amax (order-free: the DSL max never
 // selects a NaN and starts from 0).  Pass 2: one packed word per thread-step.
@@ -216,30 +148,6 @@ int L_quant_act(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStre
 
 // ------------------------------------------------------ 2-bit x int8 GEMV
 
-// 4x4 byte transpose: X[k] holds columns 4k..4k+3 of a 16-column group;
-// Y[s] byte k = X[k] byte s = column 4k+s, the order the masked weight
-// bytes of field group s come in.
-__device__ __forceinline__ void xpose4(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
-                                       uint32_t &y0, uint32_t &y1, uint32_t &y2, uint32_t &y3) {
-  const uint32_t a = __builtin_amdgcn_perm(x1, x0, 0x05010400u);  // x0.b0 x1.b0 x0.b1 x1.b1
-  const uint32_t b = __builtin_amdgcn_perm(x1, x0, 0x07030602u);  // x0.b2 x1.b2 x0.b3 x1.b3
-  const uint32_t c = __builtin_amdgcn_perm(x3, x2, 0x05010400u);  // x2.b0 x3.b0 x2.b1 x3.b1
-  const uint32_t d = __builtin_amdgcn_perm(x3, x2, 0x07030602u);  // x2.b2 x3.b2 x2.b3 x3.b3
-  y0 = __builtin_amdgcn_perm(c, a, 0x05040100u);
-  y1 = __builtin_amdgcn_perm(c, a, 0x07060302u);
-  y2 = __builtin_amdgcn_perm(d, b, 0x05040100u);
-  y3 = __builtin_amdgcn_perm(d, b, 0x07060302u);
-}
-
-// 64 x (sum over the 16 fields of w of decode(field) * x[column]).
-__device__ __forceinline__ int wdot(uint32_t w, uint32_t y0, uint32_t y1, uint32_t y2, uint32_t y3,
-                                    int acc) {
-  acc = __builtin_amdgcn_sdot4((int)((w << 6) & 0xC0C0C0C0u), (int)y0, acc, false);
-  acc = __builtin_amdgcn_sdot4((int)((w << 4) & 0xC0C0C0C0u), (int)y1, acc, false);
-  acc = __builtin_amdgcn_sdot4((int)((w << 2) & 0xC0C0C0C0u), (int)y2, acc, false);
-  acc = __builtin_amdgcn_sdot4((int)(w & 0xC0C0C0C0u), (int)y3, acc, false);
-  return acc;
-}
 
 struct TernArgs {
   const uint32_t *xq;    // [seq x ng]
@@ -518,158 +426,7 @@ extern "C" int nlg_ternary_linear_i8(const uint32_t *xq, const float *gamma, con
 }
 
 // ---------------------------------------- fused: quantise + GEMV, one launch
-
-// The decode step as one kernel: each workgroup first issues the HBM loads
-// of its weight rows (kept in registers), then -- while those loads are in
-// flight -- reads the token's f32 activation row (L2-resident after the
-// first workgroup), finds amax, and writes pack-act-rows' int8 words into
-// LDS; after one barrier every wave dots its rows against the LDS copy.
-// The rounding (pack_lane) and epilogue (tern_store) are the same code as
-// the two-kernel path, so the result is bit-identical to it.
-// Requires cols % 64 == 0 and cols <= 64*64*CPL.
-struct FusedArgs {
-  const float *x;        // [seq x cols] f32
-  const uint32_t *w2;    // [out x wng]
-  const float *bias;     // [out] or null
-  const float *beta;     // [1] or [out]
-  float *y;              // [seq x out]
-  float *gamma_out;      // [seq] or null
-  uint32_t seq, out, cols, wng;
-  int beta_per_row;
-};
-
-// F4: float4s of the activation row per thread (cols <= 1024*F4).
-template <int R, int CPL, int F4>
-__global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
-  extern __shared__ uint4 s_xq4[];  // cols/16 uint4 = cols int8 lanes
-  __shared__ float red[4];
-  const int lane = threadIdx.x & 63, wvi = threadIdx.x >> 6;
-  const uint32_t tok = blockIdx.y;
-  const uint32_t row0 = (blockIdx.x * 4 + wvi) * R;
-  const uint32_t nchunk = a.wng >> 2;
-  // 1. every global load is issued up front, activation first: vmcnt retires
-  //    in issue order, so waiting for x must not also wait for the weights'
-  //    HBM fetch, which stays in flight through the quantisation below.  The
-  //    loads are straight-line (clamped addresses, validity applied with
-  //    selects afterwards): a branch around a load makes the wait-count pass
-  //    drain every outstanding load at the join.
-  const float4 *x4 = (const float4 *)(a.x + (size_t)tok * a.cols);
-  const uint32_t nf4 = a.cols >> 2;
-  float4 xv4[F4];
-#pragma unroll
-  for (int k = 0; k < F4; k++) {
-    const uint32_t f = threadIdx.x + 256u * k;
-    xv4[k] = x4[f < nf4 ? f : nf4 - 1];
-  }
-  uint4 wv[R][CPL];
-#pragma unroll
-  for (int r = 0; r < R; r++) {
-    const uint32_t row = row0 + r < a.out ? row0 + r : a.out - 1;
-    const uint4 *wr = (const uint4 *)(a.w2 + (size_t)row * a.wng);
-#pragma unroll
-    for (int i = 0; i < CPL; i++) {
-      const uint32_t c = lane + 64 * i;
-      wv[r][i] = wr[c < nchunk ? c : nchunk - 1];
-    }
-  }
-  const uint32_t orow_u = row0 + (lane < R ? lane : 0);
-  const uint32_t orow = orow_u < a.out ? orow_u : a.out - 1;  // every lane loads a valid row
-  const bool olive = lane < R && orow_u < a.out;
-  const float *bsrc = a.bias ? a.bias : a.beta;  // a real address either way
-  const float bo_raw = bsrc[a.bias ? orow : 0];
-  const float be = a.beta[a.beta_per_row ? orow : 0];
-  const float bo = a.bias ? bo_raw : 0.0f;
-#pragma unroll
-  for (int k = 0; k < F4; k++)
-    if (threadIdx.x + 256u * k >= nf4) xv4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-  for (int r = 0; r < R; r++)
-#pragma unroll
-    for (int i = 0; i < CPL; i++)
-      if (lane + 64u * i >= nchunk) wv[r][i] = make_uint4(0, 0, 0, 0);
-  // 2. amax of the token's row (every thread takes part: barriers follow)
-  float amax = 0.0f;
-#pragma unroll
-  for (int k = 0; k < F4; k++) {
-    float t;
-    t = dsl_abs(xv4[k].x); amax = t > amax ? t : amax;
-    t = dsl_abs(xv4[k].y); amax = t > amax ? t : amax;
-    t = dsl_abs(xv4[k].z); amax = t > amax ? t : amax;
-    t = dsl_abs(xv4[k].w); amax = t > amax ? t : amax;
-  }
-  amax = nlg_block_max_f32(amax, red);
-  const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;  // uniform: a scalar
-  const float ginv = 1.0f / g;
-  if (a.gamma_out && blockIdx.x == 0 && threadIdx.x == 0) a.gamma_out[tok] = g;
-  // 3. quantise into LDS, one packed word per float4 (exact; see lane_est)
-  const bool fast = g > 0.0f && ginv < INFINITY;
-  uint32_t *s_xq = (uint32_t *)s_xq4;
-#pragma unroll
-  for (int k = 0; k < F4; k++) {
-    const uint32_t f = threadIdx.x + 256u * k;
-    const uint32_t wd = quant_word(xv4[k], g, ginv, fast);
-    if (f < nf4) s_xq[f] = wd;
-  }
-  __syncthreads();
-  if (row0 >= a.out) return;  // wave-uniform, after the last barrier
-  // 4. dots against the LDS activation
-  int acc[R];
-#pragma unroll
-  for (int r = 0; r < R; r++) acc[r] = 0;
-#pragma unroll
-  for (int i = 0; i < CPL; i++) {
-    const uint32_t c = lane + 64 * i;
-    if (c < nchunk) {
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const uint4 xv = s_xq4[4 * c + j];
-        uint32_t y0, y1, y2, y3;
-        xpose4(xv.x, xv.y, xv.z, xv.w, y0, y1, y2, y3);
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-          const uint32_t w = j == 0 ? wv[r][i].x : j == 1 ? wv[r][i].y : j == 2 ? wv[r][i].z : wv[r][i].w;
-          acc[r] = wdot(w, y0, y1, y2, y3, acc[r]);
-        }
-      }
-    }
-  }
-  // 5. reduce and write (tern_store's epilogue, with gamma from registers)
-#pragma unroll
-  for (int r = 0; r < R; r++) {
-    const int tot = nlg_wave_sum_i32(acc[r]);
-    if (lane == r && olive)
-      a.y[(size_t)tok * a.out + orow] = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, g), (float)(tot >> 6)));
-  }
-}
-
-static int fused_launch(const FusedArgs &a, int rpw, hipStream_t st) {
-  const uint32_t nchunk = a.wng / 4;
-  const size_t lds = (size_t)a.cols;  // one byte per column
-  dim3 grid(nlg_blocks(a.out, 4u * rpw), a.seq), blk(256);
-  // float4s per thread: cols/1024 rounded up to 2, 4, 8 or 16
-#define FZ(RR, CC)                                                                         \
-  do {                                                                                     \
-    if (a.cols <= 2048) hipLaunchKernelGGL((k_tern_fused<RR, CC, 2>), grid, blk, lds, st, a); \
-    else if (a.cols <= 4096) hipLaunchKernelGGL((k_tern_fused<RR, CC, 4>), grid, blk, lds, st, a); \
-    else if (a.cols <= 8192) hipLaunchKernelGGL((k_tern_fused<RR, CC, 8>), grid, blk, lds, st, a); \
-    else hipLaunchKernelGGL((k_tern_fused<RR, CC, 16>), grid, blk, lds, st, a);            \
-  } while (0)
-#define FZR(RR)                          \
-  do {                                   \
-    if (nchunk <= 64) FZ(RR, 1);         \
-    else if (nchunk <= 128) FZ(RR, 2);   \
-    else FZ(RR, 4);                      \
-  } while (0)
-  switch (rpw) {
-    case 1: FZR(1); break;
-    case 2: FZR(2); break;
-    default: FZR(4); break;
-  }
-#undef FZR
-#undef FZ
-  NLG_LAUNCHED("ternary linear (fused quantisation)");
-  return NLG_OK;
-}
+// (k_tern_fused in nlg_layer.hip; this entry point is its plain form)
 
 extern "C" int nlg_ternary_linear_cfg(const float *x, const uint32_t *w2, const float *bias,
                                       const float *beta, int beta_per_row, float *y, float *gamma_out,
@@ -681,12 +438,12 @@ extern "C" int nlg_ternary_linear_cfg(const float *x, const uint32_t *w2, const 
   const bool fusable = (cols % 64 == 0) && cols <= 16384 && (((uintptr_t)x & 15) == 0) &&
                        (((uintptr_t)w2 & 15) == 0) && seq <= 4;
   if (fusable) {
-    FusedArgs a{x, w2, bias, beta, y, gamma_out, seq, out, cols, cols / 16, beta_per_row};
+    FusedArgs a{};
+    a.x = x; a.w2 = w2; a.bias = bias; a.beta = beta; a.beta_per_row = beta_per_row;
+    a.y = y; a.ystride = out; a.gamma_out = gamma_out; a.seq = seq; a.out = out; a.cols = cols;
     int rpw = rows_per_wave;
-    // Each workgroup quantises the whole row, so fewer, fatter workgroups
-    // waste less; about one per CU measured best at 4096 rows (4.3 us).
-    if (rpw != 1 && rpw != 2 && rpw != 4) rpw = out >= 4096 ? 4 : (out >= 2048 ? 2 : 1);
-    return fused_launch(a, rpw, st);
+    if (rpw != 1 && rpw != 2 && rpw != 4) rpw = 0;  // the launcher's default
+    return nlg_fused_launch(a, NLG_PRO_NONE, NLG_EPI_STORE, rpw, st);
   }
   // two launches: pack-act-rows into the workspace, then the GEMV
   const size_t ng = (cols + 3) / 4;

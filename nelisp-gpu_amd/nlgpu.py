@@ -33,6 +33,12 @@ class Buffer(C.Structure):
     _fields_ = [("ptr", C.c_void_p), ("nfloats", C.c_uint32)]
 
 
+class StackConfig(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("layers", "d_model", "heads", "kv_heads", "head_dim",
+                                          "d_ff", "vocab", "max_seq", "batch")] + \
+               [("rms_eps", C.c_float), ("rope_theta", C.c_float), ("seed", C.c_uint64)]
+
+
 _lib = None
 
 
@@ -84,6 +90,24 @@ def lib() -> C.CDLL:
         "nlg_ternary_linear": (i32, [vp, vp, vp, vp, i32, vp, vp, u32, u32, u32, vp, sz, vp]),
         "nlg_ternary_linear_cfg": (i32, [vp, vp, vp, vp, i32, vp, vp, u32, u32, u32, i32, vp, sz, vp]),
         "nlg_ternary_linear_workspace": (sz, [u32, u32]),
+        "nlg_rms_ternary_linear": (i32, [vp, vp, C.c_float, vp, vp, vp, i32, vp, u32, u32, u32, vp]),
+        "nlg_ternary_linear_residual": (i32, [vp, vp, vp, vp, i32, vp, vp, u32, u32, u32, vp]),
+        "nlg_rms_ternary_swiglu": (i32, [vp, vp, C.c_float, vp, vp, i32, vp, u32, u32, u32, vp]),
+        "nlg_rms_ternary_qkv_rope": (i32, [vp, vp, C.c_float, vp, vp, i32, vp, vp, vp, vp, vp, vp,
+                                           u32, u32, u32, u32, u32, u32, vp]),
+        "nlg_rms_ternary_argmax": (i32, [vp, vp, C.c_float, vp, vp, i32, vp, vp, u32, u32, u32, vp,
+                                         sz, vp]),
+        "nlg_rms_ternary_argmax_workspace": (sz, [u32, u32]),
+        "nlg_decode_attn_f16": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, sz, vp]),
+        "nlg_decode_attn_f16_workspace": (sz, [u32, u32, u32, u32, u32]),
+        "nlg_stack_create": (i32, [C.POINTER(StackConfig), C.POINTER(vp)]),
+        "nlg_stack_destroy": (None, [vp]),
+        "nlg_stack_start": (i32, [vp, vp, u32]),
+        "nlg_stack_step": (i32, [vp, u32, i32]),
+        "nlg_stack_position": (i32, [vp, C.POINTER(u32)]),
+        "nlg_stack_tokens": (i32, [vp, vp, vp]),
+        "nlg_stack_logits": (i32, [vp, vp]),
+        "nlg_stack_tensor": (i32, [vp, C.c_char_p, i32, C.POINTER(vp), C.POINTER(sz)]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -248,6 +272,116 @@ def softmax_rows(a: DeviceArray, c: DeviceArray, rows: int, cols: int, stream=No
     _check(lib().nlg_softmax_rows(a.ptr, c.ptr, rows, cols, stream), "softmax_rows")
 
 
+def _ptr(a):
+    return a.ptr if a is not None else None
+
+
+def rms_ternary_linear(x, gain, eps, w2, bias, beta, y, seq, out, cols, beta_per_row=False,
+                       stream=None) -> None:
+    _check(lib().nlg_rms_ternary_linear(x.ptr, gain.ptr, eps, w2.ptr, _ptr(bias), beta.ptr,
+                                        int(beta_per_row), y.ptr, seq, out, cols, stream),
+           "rms_ternary_linear")
+
+
+def ternary_linear_residual(x, w2, bias, beta, res, y, seq, out, cols, beta_per_row=False,
+                            stream=None) -> None:
+    _check(lib().nlg_ternary_linear_residual(x.ptr, w2.ptr, _ptr(bias), beta.ptr, int(beta_per_row),
+                                             res.ptr, y.ptr, seq, out, cols, stream),
+           "ternary_linear_residual")
+
+
+def rms_ternary_swiglu(x, gain, eps, w2gu, beta, h, seq, dff, cols, beta_per_row=True,
+                       stream=None) -> None:
+    _check(lib().nlg_rms_ternary_swiglu(x.ptr, gain.ptr, eps, w2gu.ptr, beta.ptr, int(beta_per_row),
+                                        h.ptr, seq, dff, cols, stream), "rms_ternary_swiglu")
+
+
+def rms_ternary_qkv_rope(x, gain, eps, w2, beta, q, kc, vc, co, si, pos, seq, heads, kvheads,
+                         head_dim, max_seq, cols, beta_per_row=True, stream=None) -> None:
+    _check(lib().nlg_rms_ternary_qkv_rope(x.ptr, gain.ptr, eps, w2.ptr, beta.ptr, int(beta_per_row),
+                                          q.ptr, kc.ptr, vc.ptr, co.ptr, si.ptr, pos.ptr, seq, heads,
+                                          kvheads, head_dim, max_seq, cols, stream),
+           "rms_ternary_qkv_rope")
+
+
+def rms_ternary_argmax(x, gain, eps, w2, beta, logits, argmax, seq, vocab, cols, workspace,
+                       beta_per_row=False, stream=None) -> None:
+    _check(lib().nlg_rms_ternary_argmax(x.ptr, gain.ptr, eps, w2.ptr, beta.ptr, int(beta_per_row),
+                                        logits.ptr, argmax.ptr, seq, vocab, cols, workspace.ptr,
+                                        workspace.nbytes, stream), "rms_ternary_argmax")
+
+
+def rms_ternary_argmax_workspace(seq: int, vocab: int) -> int:
+    return lib().nlg_rms_ternary_argmax_workspace(seq, vocab)
+
+
+def decode_attn_f16(q, kc, vc, pos, out, batch, heads, kvheads, head_dim, max_seq, workspace,
+                    stream=None) -> None:
+    _check(lib().nlg_decode_attn_f16(q.ptr, kc.ptr, vc.ptr, pos.ptr, out.ptr, batch, heads, kvheads,
+                                     head_dim, max_seq, workspace.ptr, workspace.nbytes, stream),
+           "decode_attn_f16")
+
+
+def decode_attn_f16_workspace(batch, heads, kvheads, head_dim, max_seq) -> int:
+    return lib().nlg_decode_attn_f16_workspace(batch, heads, kvheads, head_dim, max_seq)
+
+
+class Stack:
+    """The random-initialised ternary decoder stack (nlg_stack_* in nlgpu.h)."""
+
+    def __init__(self, layers, d_model, heads, kv_heads, head_dim, d_ff, vocab, max_seq, batch,
+                 rms_eps=1e-5, rope_theta=500000.0, seed=20260921 + 5):
+        self.cfg = StackConfig(layers, d_model, heads, kv_heads, head_dim, d_ff, vocab, max_seq,
+                               batch, rms_eps, rope_theta, seed)
+        h = C.c_void_p()
+        _check(lib().nlg_stack_create(C.byref(self.cfg), C.byref(h)), "stack_create")
+        self.h = h.value
+
+    def start(self, prompts: np.ndarray) -> None:
+        p = np.ascontiguousarray(prompts, np.int32)
+        assert p.ndim == 2 and p.shape[0] == self.cfg.batch
+        _check(lib().nlg_stack_start(self.h, p.ctypes.data, p.shape[1]), "stack_start")
+
+    def step(self, steps: int = 1, graph: bool = True) -> None:
+        _check(lib().nlg_stack_step(self.h, steps, int(graph)), "stack_step")
+
+    def position(self) -> int:
+        p = C.c_uint32(0)
+        _check(lib().nlg_stack_position(self.h, C.byref(p)), "stack_position")
+        return p.value
+
+    def tokens(self):
+        n = self.cfg.batch * self.cfg.max_seq
+        t, g = np.empty(n, np.int32), np.empty(n, np.int32)
+        _check(lib().nlg_stack_tokens(self.h, t.ctypes.data, g.ctypes.data), "stack_tokens")
+        return t.reshape(self.cfg.batch, -1), g.reshape(self.cfg.batch, -1)
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.cfg.batch * self.cfg.vocab, np.float32)
+        _check(lib().nlg_stack_logits(self.h, out.ctypes.data), "stack_logits")
+        return out.reshape(self.cfg.batch, -1)
+
+    def tensor(self, name: str, layer: int = -1, dtype=np.float32) -> np.ndarray:
+        p, n = C.c_void_p(), C.c_size_t(0)
+        _check(lib().nlg_stack_tensor(self.h, name.encode(), layer, C.byref(p), C.byref(n)),
+               f"stack_tensor {name}")
+        dt = np.dtype(dtype)
+        out = np.empty(n.value // dt.itemsize, dt)
+        _check(lib().nlg_download(out.ctypes.data, p.value, out.nbytes), "download")
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().nlg_stack_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 # ------------------------------------------------------------- events, graphs
 
 class Event:
@@ -353,3 +487,22 @@ def trits(seed: int, shape) -> np.ndarray:
     u = uniform(seed, n)
     t = np.where(u < 0.25, -1, np.where(u < 0.75, 0, 1)).astype(np.int8)
     return t.reshape(shape)
+
+
+def normal_pairs(seed: int, n: int) -> np.ndarray:
+    """float32 N(0,1) as the device generator draws it: elements 2p and 2p+1
+    share u1 = 1 - u(2p), u2 = u(2p+1) and take r cos(2 pi u2), r sin(2 pi u2)."""
+    m = (n + 1) // 2
+    u = uniform(seed, 2 * m)
+    r = np.sqrt(-2.0 * np.log(1.0 - u[0::2]))
+    t = 6.283185307179586 * u[1::2]
+    z = np.empty(2 * m)
+    z[0::2], z[1::2] = r * np.cos(t), r * np.sin(t)
+    return z[:n].astype(np.float32)
+
+
+def stack_tensor_seed(seed: int, layer: int, tensor: int) -> int:
+    """Seed of one tensor of the decoder stack: per layer, tensors 0..8 are
+    q, k, v, o, gate, up, down, attention gain, FFN gain; after the last
+    layer, 0..2 are the LM head, the final gain and the embedding."""
+    return (seed + 1000003 * (layer + 1) + tensor) & _M64

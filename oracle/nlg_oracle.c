@@ -749,6 +749,74 @@ void or_ternary_linear_i8(const uint32_t *xq, const float *gamma, const uint32_t
   }
 }
 
+/* ---- decoder-stack pieces ---------------------------------------------- */
+
+/* rmsnorm-istd then rmsnorm-fwd (kernels.el:1249-1265) with the epsilon a
+ * parameter (the DSL kernel hard-codes 1e-6): S = 1/sqrt(ss/N + eps) with ss
+ * the serial sum of x*x, C = (X*S)*G. */
+void or_rmsnorm_rows(const float *x, const float *gain, float eps, float *y, uint32_t rows,
+                     uint32_t cols) {
+  for (uint32_t r = 0; r < rows; r++) {
+    const float *xr = x + (size_t)r * cols;
+    float ss = 0.0f;
+    for (uint32_t k = 0; k < cols; k++) ss = ss + xr[k] * xr[k];
+    float s = 1.0f / sqrtf(ss / (float)cols + eps);
+    for (uint32_t j = 0; j < cols; j++) y[(size_t)r * cols + j] = (xr[j] * s) * gain[j];
+  }
+}
+
+static float f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31u, m = h & 1023u, u;
+  if (e == 31u) {
+    u = sign | 0x7f800000u | (m << 13);
+  } else if (e == 0u) {
+    if (!m) {
+      u = sign;
+    } else { /* subnormal: m * 2^-24 exactly */
+      float f = (float)m * 5.9604644775390625e-8f;
+      memcpy(&u, &f, 4);
+      u |= sign;
+    }
+  } else {
+    u = sign | ((e + 112u) << 23) | (m << 13);
+  }
+  return bits2f(u);
+}
+
+/* decode-attn-b (kernels.el:366-390) with K and V read from fp16 caches
+ * laid out [B][kvheads][max_seq][hd]: per output element (b, h, t), serial
+ * q.k dot, s = acc*coef, mx seeded at -1e30, e = exp(s - mx), z = sum e,
+ * ctx = sum e*v, C = ctx/z, over positions 0..pos. */
+void or_decode_attn_f16(const float *q, const uint16_t *kc, const uint16_t *vc, uint32_t pos,
+                        float *out, uint32_t B, uint32_t heads, uint32_t kvheads, uint32_t hd,
+                        uint32_t max_seq) {
+  const uint32_t dim = heads * hd, grp = heads / kvheads, len = pos + 1u;
+  const float coef = 1.0f / sqrtf((float)hd);
+#pragma omp parallel for schedule(static)
+  for (int64_t idx = 0; idx < (int64_t)B * dim; idx++) {
+    uint32_t bb = (uint32_t)(idx / dim), c = (uint32_t)(idx % dim);
+    uint32_t h = c / hd, t = c % hd, kvh = h / grp;
+    const float *qh = q + (size_t)bb * dim + (size_t)h * hd;
+    size_t cb = ((size_t)bb * kvheads + kvh) * max_seq * hd;
+    float mx = NEG_BIG;
+    for (uint32_t j = 0; j < len; j++) {
+      float acc = 0.0f;
+      for (uint32_t tt = 0; tt < hd; tt++) acc = acc + qh[tt] * f16_to_f32(kc[cb + (size_t)j * hd + tt]);
+      float s = acc * coef;
+      if (s > mx) mx = s;
+    }
+    float z = 0.0f, ctx = 0.0f;
+    for (uint32_t j = 0; j < len; j++) {
+      float acc = 0.0f;
+      for (uint32_t tt = 0; tt < hd; tt++) acc = acc + qh[tt] * f16_to_f32(kc[cb + (size_t)j * hd + tt]);
+      float e = expf(acc * coef - mx);
+      z = z + e;
+      ctx = ctx + e * f16_to_f32(vc[cb + (size_t)j * hd + t]);
+    }
+    out[idx] = ctx / z;
+  }
+}
+
 int or_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

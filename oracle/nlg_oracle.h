@@ -49,6 +49,14 @@ void or_pack_act_rows(const float *x, uint32_t *xq, float *gamma, uint32_t seq, 
 /* softmax over rows (kernels.el:28-42); c may equal a. */
 void or_softmax_rows(const float *a, float *c, uint32_t rows, uint32_t cols);
 
+/* rmsnorm-istd + rmsnorm-fwd (kernels.el:1249-1265) with eps a parameter. */
+void or_rmsnorm_rows(const float *x, const float *gain, float eps, float *y, uint32_t rows,
+                     uint32_t cols);
+/* decode-attn-b (kernels.el:366-390) over fp16 caches [B][kvheads][max_seq][hd]. */
+void or_decode_attn_f16(const float *q, const uint16_t *kc, const uint16_t *vc, uint32_t pos,
+                        float *out, uint32_t B, uint32_t heads, uint32_t kvheads, uint32_t hd,
+                        uint32_t max_seq);
+
 /* Number of OpenMP threads the parallel loops use (1 when built without
  * OpenMP); set_threads(0) keeps the runtime default. */
 int or_threads(void);

@@ -43,6 +43,10 @@ def lib() -> C.CDLL:
         L.or_pack_act_rows.argtypes = [vp, vp, vp, u32, u32]
         L.or_softmax_rows.restype = None
         L.or_softmax_rows.argtypes = [vp, vp, u32, u32]
+        L.or_rmsnorm_rows.restype = None
+        L.or_rmsnorm_rows.argtypes = [vp, vp, C.c_float, vp, u32, u32]
+        L.or_decode_attn_f16.restype = None
+        L.or_decode_attn_f16.argtypes = [vp, vp, vp, u32, vp, u32, u32, u32, u32, u32]
         L.or_threads.restype = i32
         L.or_set_threads.argtypes = [i32]
         _lib = L
@@ -114,6 +118,23 @@ def softmax_rows(a: np.ndarray, rows: int, cols: int) -> np.ndarray:
     c = np.empty_like(a)
     lib().or_softmax_rows(_p(a), _p(c), rows, cols)
     return c
+
+
+def rmsnorm_rows(x: np.ndarray, gain: np.ndarray, eps: float, rows: int, cols: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows * cols, np.float32)
+    lib().or_rmsnorm_rows(_p(x), _p(np.ascontiguousarray(gain, np.float32)), float(eps), _p(y), rows, cols)
+    return y
+
+
+def decode_attn_f16(q, kc, vc, pos, B, heads, kvheads, hd, max_seq) -> np.ndarray:
+    """kc, vc: uint16 fp16 bit patterns [B][kvheads][max_seq][hd]."""
+    out = np.empty(B * heads * hd, np.float32)
+    lib().or_decode_attn_f16(_p(np.ascontiguousarray(q, np.float32)),
+                             _p(np.ascontiguousarray(kc, np.uint16)),
+                             _p(np.ascontiguousarray(vc, np.uint16)), int(pos), _p(out), B, heads,
+                             kvheads, hd, max_seq)
+    return out
 
 
 def threads() -> int:

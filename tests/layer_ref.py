@@ -1,0 +1,92 @@
+"""CPU compositions of the reference kernels that the decoder-layer fusions
+replace, built from the oracle's restatements (test infrastructure only).
+
+Each helper chains the oracle's statements of the named DSL kernels in the
+order a reference caller would dispatch them:
+  linear      pack-act-rows (kernels.el:884-932) + bitlinear-dp4a-1f on the
+              2-bit weights unpacked to int8 lanes (kernels.el:619-634)
+  rms         rmsnorm-istd + rmsnorm-fwd (kernels.el:1249-1265), eps a parameter
+  rope_b      decode-rope-b (kernels.el:340-355)
+  silu_mul    silu-mul (kernels.el:186-193)
+  attention   decode-attn-b (kernels.el:366-390) over fp16 caches
+and RefStack runs the decoder stack's token step from those pieces.
+"""
+import numpy as np
+
+import nlg_oracle as orc
+
+f32 = np.float32
+
+
+def linear(x, w2, beta, seq, out, cols, bias=None, per_row=False):
+    xq, g = orc.pack_act_rows(np.ascontiguousarray(x, f32), seq, cols)
+    return orc.ternary_linear_i8(xq, g, w2, bias, beta, seq, out, cols, beta_per_row=per_row)
+
+
+def rms(x, gain, eps, rows, cols):
+    return orc.rmsnorm_rows(x, gain, eps, rows, cols)
+
+
+def silu_mul(a, b):
+    a = np.ascontiguousarray(a, f32).copy()
+    b = np.ascontiguousarray(b, f32).copy()
+    c = np.zeros(a.size, f32)
+    orc.dispatch("silu-mul", [a, b, c], [a.size], (a.size + 63) // 64)
+    return c
+
+
+def rope_b(x, co, si, pos, B, cols, heads):
+    x = np.ascontiguousarray(x, f32).copy()
+    c = np.zeros(B * cols, f32)
+    npairs = B * cols // 2
+    orc.dispatch("decode-rope-b", [x, np.ascontiguousarray(co, f32), np.ascontiguousarray(si, f32),
+                                   np.array([1.0], f32), np.array([float(pos)], f32), c],
+                 [B, cols, heads], (npairs + 63) // 64)
+    return c
+
+
+class RefStack:
+    """The decoder stack's step (nelisp-gpu_amd/csrc/nlg_stack.hip) composed
+    from the reference kernels, with weights downloaded from a device stack."""
+
+    def __init__(self, stack):
+        c = stack.cfg
+        self.c = c
+        self.nq, self.nkv = c.heads * c.head_dim, c.kv_heads * c.head_dim
+        g = stack.tensor
+        self.L = []
+        for l in range(c.layers):
+            self.L.append({
+                "wqkv": g("wqkv", l, np.uint32), "bqkv": g("bqkv", l), "wo": g("wo", l, np.uint32),
+                "bo": g("bo", l), "wgu": g("wgu", l, np.uint32), "bgu": g("bgu", l),
+                "wd": g("wd", l, np.uint32), "bd": g("bd", l), "gattn": g("gattn", l),
+                "gffn": g("gffn", l),
+            })
+        self.wlm, self.blm, self.gfinal = g("wlm", -1, np.uint32), g("blm"), g("gfinal")
+        self.emb = g("emb").reshape(c.vocab, c.d_model)
+        self.co, self.si = g("rope_cos"), g("rope_sin")
+        shape = (c.batch, c.kv_heads, c.max_seq, c.head_dim)
+        self.kc = [np.zeros(shape, np.float16) for _ in range(c.layers)]
+        self.vc = [np.zeros(shape, np.float16) for _ in range(c.layers)]
+
+    def step(self, tokens, pos):
+        c, B, d, f = self.c, self.c.batch, self.c.d_model, self.c.d_ff
+        nq, nkv, hd = self.nq, self.nkv, c.head_dim
+        x = self.emb[np.asarray(tokens)].astype(f32).ravel()
+        for l, w in enumerate(self.L):
+            xn = rms(x, w["gattn"], c.rms_eps, B, d)
+            qkv = linear(xn, w["wqkv"], w["bqkv"], B, nq + 2 * nkv, d, per_row=True).reshape(B, -1)
+            q = rope_b(qkv[:, :nq].ravel(), self.co, self.si, pos, B, nq, c.heads)
+            k = rope_b(qkv[:, nq:nq + nkv].ravel(), self.co, self.si, pos, B, nkv, c.kv_heads)
+            v = qkv[:, nq + nkv:]
+            self.kc[l][:, :, pos, :] = k.reshape(B, c.kv_heads, hd).astype(np.float16)
+            self.vc[l][:, :, pos, :] = v.reshape(B, c.kv_heads, hd).astype(np.float16)
+            att = orc.decode_attn_f16(q, self.kc[l].view(np.uint16), self.vc[l].view(np.uint16), pos,
+                                      B, c.heads, c.kv_heads, hd, c.max_seq)
+            x = (x + linear(att, w["wo"], w["bo"], B, d, nq)).astype(f32)
+            xn = rms(x, w["gffn"], c.rms_eps, B, d)
+            gu = linear(xn, w["wgu"], w["bgu"], B, 2 * f, d, per_row=True).reshape(B, 2 * f)
+            h = silu_mul(gu[:, 0::2].ravel(), gu[:, 1::2].ravel())
+            x = (x + linear(h, w["wd"], w["bd"], B, d, f)).astype(f32)
+        xn = rms(x, self.gfinal, c.rms_eps, B, d)
+        return linear(xn, self.wlm, self.blm, B, c.vocab, d).reshape(B, c.vocab)
