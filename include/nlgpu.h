@@ -237,9 +237,9 @@ size_t nlg_rms_ternary_argmax_workspace(uint32_t seq, uint32_t vocab);
  * [head_dim] for positions 0..pos[0]: decode-attn-b's arithmetic
  * (kernels.el:366-390: s = (q.k)/sqrt(head_dim), e = exp(s - max),
  * out = sum(e*v)/sum(e)) with K, V read as fp16.  head_dim 64 or 128,
- * heads/kvheads in {1,2,4,8}.  The workspace
- * (nlg_decode_attn_f16_workspace bytes) must be zero-filled before its
- * first use (nlg_malloc memory is); calls leave it ready for the next. */
+ * heads/kvheads in {1,2,4,8}.  Two launches: chunks of positions scored
+ * in parallel into `workspace` (nlg_decode_attn_f16_workspace bytes), then
+ * merged. */
 int nlg_decode_attn_f16(const float *q, const uint16_t *kcache, const uint16_t *vcache,
                         const int32_t *pos, float *out, uint32_t batch, uint32_t heads,
                         uint32_t kvheads, uint32_t head_dim, uint32_t max_seq, void *workspace,

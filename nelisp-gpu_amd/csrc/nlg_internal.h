@@ -115,9 +115,12 @@ __device__ __forceinline__ float nlg_wave_max_f32(float v) {
 
 // Block-wide (blockDim.x multiple of 64, <= 1024) sum / max through LDS.
 // `scratch` needs blockDim.x/64 floats.  Every thread gets the result.
+// NW > 0 states the block's wave count at compile time (no read of the
+// launch's block size).
+template <int NW = 0>
 __device__ __forceinline__ float nlg_block_sum_f32(float v, float *scratch) {
   v = nlg_wave_sum_f32(v);
-  const int nw = blockDim.x >> 6, w = threadIdx.x >> 6;
+  const int nw = NW > 0 ? NW : (int)(blockDim.x >> 6), w = threadIdx.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) scratch[w] = v;
   __syncthreads();
@@ -125,9 +128,10 @@ __device__ __forceinline__ float nlg_block_sum_f32(float v, float *scratch) {
   for (int i = 0; i < nw; i++) t = t + scratch[i];
   return t;
 }
+template <int NW = 0>
 __device__ __forceinline__ float nlg_block_max_f32(float v, float *scratch) {
   v = nlg_wave_max_f32(v);
-  const int nw = blockDim.x >> 6, w = threadIdx.x >> 6;
+  const int nw = NW > 0 ? NW : (int)(blockDim.x >> 6), w = threadIdx.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) scratch[w] = v;
   __syncthreads();

@@ -21,12 +21,12 @@
 // the reference in the last bit; everything after it is the reference's
 // arithmetic.
 //
-// k_attn_f16: single-query GQA attention over fp16 KV caches, split over
-// 64-position chunks (decode-attn(-b), kernels.el:315-338, :366-390: scale
-// 1/sqrt(hd), max seeded at -1e30, C = sum(e*V)/sum(e)).  Each workgroup
-// handles one (sequence, kv head, chunk) for all the query heads of that kv
-// head, so K and V are read from HBM once; the last workgroup of a (sequence,
-// kv head) to finish merges the chunks (a completion counter, no waiting).
+// k_attn_part + k_attn_merge: single-query GQA attention over fp16 KV
+// caches (decode-attn(-b), kernels.el:315-338, :366-390: scale 1/sqrt(hd),
+// max seeded at -1e30, C = sum(e*V)/sum(e)), split over chunks of positions.
+// Each workgroup of the first pass handles one (chunk, kv head, sequence)
+// for all the query heads of that kv head, so K and V are read from HBM once;
+// a second launch merges the chunks (max-rescaled sums).
 #include <math.h>
 
 #include "nlg_quant.h"
@@ -47,6 +47,12 @@ template <int R, int CPL, int F4, int PRO, int EPI>
 __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   extern __shared__ uint4 s_xq4[];  // cols/16 uint4 = cols int8 lanes
   __shared__ float red[4];
+  // Every argument the kernel uses is pinned into SGPRs here, so they all
+  // arrive with the first kernarg fetch instead of in later round trips.
+  float *const y_out = a.y;
+  float *const gamma_out = a.gamma_out;
+  const uint32_t ystride = a.ystride;
+  asm volatile("" ::"s"(y_out), "s"(gamma_out), "s"(ystride));
   const int lane = threadIdx.x & 63, wvi = threadIdx.x >> 6;
   const uint32_t tok = blockIdx.y;
   const uint32_t wave = blockIdx.x * 4 + wvi;
@@ -126,7 +132,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
       sq = sq + xv4[k].z * xv4[k].z;
       sq = sq + xv4[k].w * xv4[k].w;
     }
-    sq = nlg_block_sum_f32(sq, red);
+    sq = nlg_block_sum_f32<4>(sq, red);
     sq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq)));
     const float istd = 1.0f / sqrtf(sq / (float)a.cols + a.eps);
 #pragma unroll
@@ -147,10 +153,10 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
     t = dsl_abs(xv4[k].z); amax = t > amax ? t : amax;
     t = dsl_abs(xv4[k].w); amax = t > amax ? t : amax;
   }
-  amax = nlg_block_max_f32(amax, red);
+  amax = nlg_block_max_f32<4>(amax, red);
   const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
   const float ginv = 1.0f / g;
-  if (a.gamma_out && blockIdx.x == 0 && threadIdx.x == 0) a.gamma_out[tok] = g;
+  if (gamma_out && blockIdx.x == 0 && threadIdx.x == 0) gamma_out[tok] = g;
   // 4. quantise into LDS, one packed word per float4 (exact; see lane_est)
   const bool fast = g > 0.0f && ginv < INFINITY;
   uint32_t *s_xq = (uint32_t *)s_xq4;
@@ -193,10 +199,10 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
   const float val = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, g), (float)(tl >> 6)));
   if (EPI == NLG_EPI_STORE || EPI == NLG_EPI_ARGMAX) {
-    if (olive) a.y[(size_t)tok * a.ystride + orow] = val;
+    if (olive) y_out[(size_t)tok * ystride + orow] = val;
   }
   if (EPI == NLG_EPI_RESID) {
-    if (olive) a.y[(size_t)tok * a.ystride + orow] = __fadd_rn(rv, val);
+    if (olive) y_out[(size_t)tok * ystride + orow] = __fadd_rn(rv, val);
   }
   if (EPI == NLG_EPI_SWIGLU || EPI == NLG_EPI_QKV) {
     // the other row of the pair (lane ^ 1)
@@ -204,7 +210,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
     if (EPI == NLG_EPI_SWIGLU) {
       if (olive && !(lane & 1)) {
         const float sg = 1.0f / (1.0f + expf(0.0f - val));
-        a.y[(size_t)tok * a.ystride + (orow >> 1)] = (val * sg) * pv;
+        y_out[(size_t)tok * ystride + (orow >> 1)] = (val * sg) * pv;
       }
     } else if (olive) {
       // decode-rope: C[i0] = a0*cc - a1*ss; C[i1] = a0*ss + a1*cc
@@ -213,7 +219,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
       const float rot = odd ? __fadd_rn(__fmul_rn(a0, ss), __fmul_rn(a1, cc))
                             : __fsub_rn(__fmul_rn(a0, cc), __fmul_rn(a1, ss));
       if (orow < a.nq) {
-        a.y[(size_t)tok * a.ystride + orow] = rot;
+        y_out[(size_t)tok * ystride + orow] = rot;
       } else if (pos_ok) {
         const bool isk = orow < a.nq + a.nkv;
         const uint32_t sec = isk ? orow - a.nq : orow - a.nq - a.nkv;
@@ -243,12 +249,14 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   }
 }
 
+// Each workgroup quantises the whole activation row, so fewer, fatter
+// workgroups waste less -- down to about one workgroup per CU.  Measured
+// at the decode shapes (graph-timed, weights streamed from HBM): 4 rows per
+// wave for 2560..4096 outputs, 8 for the 13824-row gate|up and the LM head.
 int nlg_fused_rows_per_wave(uint32_t out, int epi) {
   if (epi == NLG_EPI_ARGMAX) return out >= 32768 ? 8 : 4;
-  if (epi == NLG_EPI_SWIGLU || epi == NLG_EPI_QKV) return out >= 2048 ? 4 : 2;
-  // Each workgroup quantises the whole row, so fewer, fatter workgroups
-  // waste less; about one per CU measured best at 4096 rows (4.3 us).
-  return out >= 4096 ? 4 : (out >= 2048 ? 2 : 1);
+  if (epi == NLG_EPI_SWIGLU || epi == NLG_EPI_QKV) return out >= 8192 ? 8 : (out >= 2048 ? 4 : 2);
+  return out >= 8192 ? 8 : (out >= 2048 ? 4 : (out >= 1024 ? 2 : 1));
 }
 
 template <int PRO, int EPI, int R>
@@ -435,9 +443,8 @@ struct AttnArgs {
   const float *q;           // [B x heads*hd]
   const uint16_t *kc, *vc;  // [B][kvheads][max_seq][hd] fp16 bits
   const int32_t *pos;       // attend positions 0..pos[0]
-  float *out;               // [B x heads*hd]
-  float *part;              // [B][kvheads][nchunk][G][2 + hd]
-  int32_t *cnt;             // [B][kvheads], zero between launches
+  float *pctx;              // [B][nchunk][heads*hd]: sum of e*V over the chunk
+  float *pmz;               // [B][nchunk][heads][2]: chunk max, sum of e
   uint32_t heads, kvheads, max_seq, nchunk;
   float coef;               // 1/sqrt(hd)
 };
@@ -453,154 +460,191 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// HD = head dim (64 or 128), G = query heads per kv head.  Lanes hold 8
-// dimensions of one position: LPP = HD/8 lanes per position, PPI = 64/LPP
-// positions per wave instruction, NI = 16/PPI instructions for the wave's 16
-// positions of the workgroup's 64.
-template <int HD, int G>
-__global__ __launch_bounds__(256) void k_attn_f16(AttnArgs a) {
-  constexpr int LPP = HD / 8, PPI = 64 / LPP, NI = 16 / PPI, PSTR = 2 + HD;
-  __shared__ float s_m[4][G], s_z[4][G];
-  __shared__ float s_ctx[4][G][HD];
-  __shared__ int s_last;
+// Positions per workgroup for head dim HD: 8 waves x ATTN_NI instructions x
+// (64 / (HD/8)) positions per instruction.
+#define ATTN_NI 4
+#define ATTN_WAVES 8
+static inline uint32_t attn_chunk(uint32_t hd) { return ATTN_WAVES * ATTN_NI * (64u / (hd / 8u)); }
+
+// Pass 1: one workgroup per (chunk, kv head, sequence) scores its chunk's
+// positions for every query head of that kv head (K and V read once) and
+// stores the chunk's max m, sum z = sum(exp(s - m)) and sum(exp(s - m) * V).
+// Lanes hold 8 dimensions of one position: LPP = HD/8 lanes per position,
+// PPI = 64/LPP positions per wave instruction.  Every K and V load of the
+// workgroup is issued before the first score is computed.
+template <int HD, int G, int NI>
+__global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
+  constexpr int LPP = HD / 8, PPI = 64 / LPP, PW = NI * PPI, NW = ATTN_WAVES, CS = NW * PW;
+  __shared__ float s_m[NW][G], s_z[NW][G];
+  __shared__ float s_ctx[NW][G][HD];
+  asm volatile("" ::"s"(a.q), "s"(a.kc), "s"(a.vc), "s"(a.pos), "s"(a.pctx), "s"(a.pmz), "s"(a.heads),
+               "s"(a.kvheads), "s"(a.max_seq), "s"(a.nchunk), "s"(a.coef));
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const uint32_t c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const size_t cb = (size_t)b * a.nchunk + c;
+  float *pctx = a.pctx + cb * a.heads * HD + (size_t)kvh * G * HD;
+  float *pmz = a.pmz + (cb * a.heads + (size_t)kvh * G) * 2;
+  const uint32_t p0 = c * CS;
+  // K, V and q are fetched before the position arrives (addresses clamped
+  // to the cache, not to the position), so the position's fetch is not a
+  // round trip ahead of theirs; positions past it are masked afterwards.
+  const int d0 = 8 * (lane % LPP), grp = lane / LPP;
+  const size_t slot = (size_t)b * a.kvheads + kvh;
+  const uint16_t *kb = a.kc + slot * a.max_seq * HD + d0;
+  const uint16_t *vb = a.vc + slot * a.max_seq * HD + d0;
+  uint4 kr[NI], vr[NI];
+  uint32_t pp[NI];
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    pp[i] = p0 + w * PW + i * PPI + grp;
+    const uint32_t pc = pp[i] < a.max_seq ? pp[i] : a.max_seq - 1;
+    kr[i] = *(const uint4 *)(kb + (size_t)pc * HD);
+    vr[i] = *(const uint4 *)(vb + (size_t)pc * HD);
+  }
+  const float *qb = a.q + (size_t)b * a.heads * HD + (size_t)kvh * G * HD + d0;
+  float q[G][8];
+#pragma unroll
+  for (int h = 0; h < G; h++) {
+    const float4 q0 = *(const float4 *)(qb + h * HD), q1 = *(const float4 *)(qb + h * HD + 4);
+    q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
+    q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
+  }
   const int32_t pr = a.pos[0];
   const uint32_t len = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
-  const uint32_t nvalid = (len + 63) / 64;
-  const size_t slot = (size_t)b * a.kvheads + kvh;
-  if (c < nvalid) {
-    const int d0 = 8 * (lane % LPP), grp = lane / LPP;
-    const float *qb = a.q + (size_t)b * a.heads * HD + (size_t)kvh * G * HD + d0;
-    const uint16_t *kb = a.kc + slot * a.max_seq * HD + d0;
-    const uint16_t *vb = a.vc + slot * a.max_seq * HD + d0;
-    uint4 kr[NI], vr[NI];
-    uint32_t pp[NI];
-#pragma unroll
-    for (int i = 0; i < NI; i++) {
-      pp[i] = c * 64 + w * 16 + i * PPI + grp;
-      const uint32_t pc = pp[i] < len ? pp[i] : len - 1;
-      kr[i] = *(const uint4 *)(kb + (size_t)pc * HD);
+  if (p0 >= len) {  // block-uniform: a chunk past the position adds nothing
+    for (int i = threadIdx.x; i < G * HD; i += NW * 64) pctx[i] = 0.0f;
+    if (threadIdx.x < G) {
+      pmz[2 * threadIdx.x] = -1.0e30f;
+      pmz[2 * threadIdx.x + 1] = 0.0f;
     }
+    return;
+  }
+  float s[NI][G];
 #pragma unroll
-    for (int i = 0; i < NI; i++) {
-      const uint32_t pc = pp[i] < len ? pp[i] : len - 1;
-      vr[i] = *(const uint4 *)(vb + (size_t)pc * HD);
-    }
-    float q[G][8];
+  for (int i = 0; i < NI; i++) {
 #pragma unroll
     for (int h = 0; h < G; h++) {
-      const float4 q0 = *(const float4 *)(qb + h * HD), q1 = *(const float4 *)(qb + h * HD + 4);
-      q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
-      q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
-    }
-    float s[NI][G];
+      float d = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NI; i++) {
-#pragma unroll
-      for (int h = 0; h < G; h++) {
-        float d = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) d = fmaf(q[h][j], f16x8_at(kr[i], j), d);
-        d = group_sum<LPP>(d);
-        s[i][h] = pp[i] < len ? d * a.coef : -INFINITY;
-      }
-    }
-    float m[G], z[G], ctx[G][8];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-      float mm = -1.0e30f;
-#pragma unroll
-      for (int i = 0; i < NI; i++) mm = s[i][h] > mm ? s[i][h] : mm;
-      for (int off = LPP; off < 64; off <<= 1) {
-        const float o = __shfl_xor(mm, off);
-        mm = o > mm ? o : mm;
-      }
-      m[h] = mm;
-      z[h] = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; j++) ctx[h][j] = 0.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < NI; i++) {
-#pragma unroll
-      for (int h = 0; h < G; h++) {
-        const float e = expf(s[i][h] - m[h]);
-        z[h] = z[h] + e;
-#pragma unroll
-        for (int j = 0; j < 8; j++) ctx[h][j] = fmaf(e, f16x8_at(vr[i], j), ctx[h][j]);
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-      for (int off = LPP; off < 64; off <<= 1) {
-        z[h] = z[h] + __shfl_xor(z[h], off);
-#pragma unroll
-        for (int j = 0; j < 8; j++) ctx[h][j] = ctx[h][j] + __shfl_xor(ctx[h][j], off);
-      }
-      if (grp == 0) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) s_ctx[w][h][d0 + j] = ctx[h][j];
-      }
-      if (lane == 0) {
-        s_m[w][h] = m[h];
-        s_z[w][h] = z[h];
-      }
+      for (int j = 0; j < 8; j++) d = fmaf(q[h][j], f16x8_at(kr[i], j), d);
+      d = group_sum<LPP>(d);
+      s[i][h] = pp[i] < len ? d * a.coef : -INFINITY;
     }
   }
-  __syncthreads();
-  if (c < nvalid) {
-    float *part = a.part + (slot * a.nchunk + c) * (size_t)(G * PSTR);
-    for (int idx = threadIdx.x; idx < G * HD; idx += 256) {
-      const int h = idx / HD, d = idx % HD;
-      float mm = s_m[0][h];
-      for (int k = 1; k < 4; k++) mm = s_m[k][h] > mm ? s_m[k][h] : mm;
-      float zz = 0.0f, cx = 0.0f;
-      for (int k = 0; k < 4; k++) {
-        const float sc = expf(s_m[k][h] - mm);
-        zz = fmaf(s_z[k][h], sc, zz);
-        cx = fmaf(s_ctx[k][h][d], sc, cx);
-      }
-      part[h * PSTR + 2 + d] = cx;
-      if (d == 0) {
-        part[h * PSTR] = mm;
-        part[h * PSTR + 1] = zz;
-      }
-    }
-  }
-  // completion: the last workgroup of this (sequence, kv head) merges chunks
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(&a.cnt[slot], 1) == (int)gridDim.x - 1;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const float *pb = a.part + slot * a.nchunk * (size_t)(G * PSTR);
-  for (int idx = threadIdx.x; idx < G * HD; idx += 256) {
-    const int h = idx / HD, d = idx % HD;
+  float m[G], z[G], ctx[G][8];
+#pragma unroll
+  for (int h = 0; h < G; h++) {
     float mm = -1.0e30f;
-    for (uint32_t k = 0; k < nvalid; k++) {
-      const float mk = pb[(size_t)k * G * PSTR + h * PSTR];
-      mm = mk > mm ? mk : mm;
+#pragma unroll
+    for (int i = 0; i < NI; i++) mm = s[i][h] > mm ? s[i][h] : mm;
+    for (int off = LPP; off < 64; off <<= 1) {
+      const float o = __shfl_xor(mm, off);
+      mm = o > mm ? o : mm;
     }
-    float zz = 0.0f, cx = 0.0f;
-    for (uint32_t k = 0; k < nvalid; k++) {
-      const float *ck = pb + (size_t)k * G * PSTR + h * PSTR;
-      const float sc = expf(ck[0] - mm);
-      zz = fmaf(ck[1], sc, zz);
-      cx = fmaf(ck[2 + d], sc, cx);
-    }
-    a.out[(size_t)b * a.heads * HD + ((size_t)kvh * G + h) * HD + d] = cx / zz;
+    m[h] = mm;
+    z[h] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) ctx[h][j] = 0.0f;
   }
-  if (threadIdx.x == 0) __hip_atomic_store(&a.cnt[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      const float e = expf(s[i][h] - m[h]);
+      z[h] = z[h] + e;
+#pragma unroll
+      for (int j = 0; j < 8; j++) ctx[h][j] = fmaf(e, f16x8_at(vr[i], j), ctx[h][j]);
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < G; h++) {
+    for (int off = LPP; off < 64; off <<= 1) {
+      z[h] = z[h] + __shfl_xor(z[h], off);
+#pragma unroll
+      for (int j = 0; j < 8; j++) ctx[h][j] = ctx[h][j] + __shfl_xor(ctx[h][j], off);
+    }
+    if (grp == 0) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) s_ctx[w][h][d0 + j] = ctx[h][j];
+    }
+    if (lane == 0) {
+      s_m[w][h] = m[h];
+      s_z[w][h] = z[h];
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * HD; idx += NW * 64) {
+    const int h = idx / HD, d = idx % HD;
+    float mm = s_m[0][h];
+#pragma unroll
+    for (int k = 1; k < NW; k++) mm = s_m[k][h] > mm ? s_m[k][h] : mm;
+    float zz = 0.0f, cx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NW; k++) {
+      const float sc = expf(s_m[k][h] - mm);
+      zz = fmaf(s_z[k][h], sc, zz);
+      cx = fmaf(s_ctx[k][h][d], sc, cx);
+    }
+    pctx[idx] = cx;
+    if (d == 0) {
+      pmz[2 * h] = mm;
+      pmz[2 * h + 1] = zz;
+    }
+  }
+}
+
+// Pass 2: out = sum_c pctx_c * exp(m_c - M) / sum_c z_c * exp(m_c - M),
+// M = max_c m_c, one thread per output element.
+__global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ pctx,
+                                                    const float *__restrict__ pmz, float *__restrict__ out,
+                                                    uint32_t batch, uint32_t heads, uint32_t hd,
+                                                    uint32_t nchunk) {
+  const uint32_t nh = heads * hd;
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (uint64_t)batch * nh) return;
+  const uint32_t b = (uint32_t)(i / nh), e = (uint32_t)(i % nh), h = e / hd;
+  const float *mz = pmz + ((size_t)b * nchunk * heads + h) * 2;
+  const float *cx = pctx + (size_t)b * nchunk * nh + e;
+  // chunks in groups of 8 whose loads are all issued together (addresses
+  // clamped to the last chunk, weights of the extra ones zero)
+  float mm = -1.0e30f;
+  for (uint32_t c0 = 0; c0 < nchunk; c0 += 8) {
+    float2 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t c = c0 + k < nchunk ? c0 + k : nchunk - 1;
+      v[k] = *(const float2 *)(mz + (size_t)c * heads * 2);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) mm = v[k].x > mm ? v[k].x : mm;
+  }
+  float zz = 0.0f, acc = 0.0f;
+  for (uint32_t c0 = 0; c0 < nchunk; c0 += 8) {
+    float2 v[8];
+    float x[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t c = c0 + k < nchunk ? c0 + k : nchunk - 1;
+      v[k] = *(const float2 *)(mz + (size_t)c * heads * 2);
+      x[k] = cx[(size_t)c * nh];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const float sc = c0 + k < nchunk ? expf(v[k].x - mm) : 0.0f;
+      zz = fmaf(v[k].y, sc, zz);
+      acc = fmaf(x[k], sc, acc);
+    }
+  }
+  out[i] = acc / zz;
 }
 
 extern "C" size_t nlg_decode_attn_f16_workspace(uint32_t batch, uint32_t heads, uint32_t kvheads,
                                                 uint32_t head_dim, uint32_t max_seq) {
-  if (!kvheads) return 0;
-  const size_t nchunk = (max_seq + 63) / 64, G = heads / kvheads;
-  const size_t part = (size_t)batch * kvheads * nchunk * G * (2 + head_dim) * 4;
-  return (part + 255) / 256 * 256 + (size_t)batch * kvheads * 4;
+  if (!kvheads || (head_dim != 64 && head_dim != 128)) return 0;
+  (void)kvheads;
+  const size_t nchunk = (max_seq + attn_chunk(head_dim) - 1) / attn_chunk(head_dim);
+  const size_t ctx = (size_t)batch * nchunk * heads * head_dim * 4;
+  return (ctx + 255) / 256 * 256 + (size_t)batch * nchunk * heads * 2 * 4;
 }
 
 extern "C" int nlg_decode_attn_f16(const float *q, const uint16_t *kcache, const uint16_t *vcache,
@@ -619,16 +663,16 @@ extern "C" int nlg_decode_attn_f16(const float *q, const uint16_t *kcache, const
   const size_t need = nlg_decode_attn_f16_workspace(batch, heads, kvheads, head_dim, max_seq);
   if (!workspace || workspace_bytes < need) return nlg_fail("decode attn: needs a %zu-byte workspace", need);
   AttnArgs a;
-  a.q = q; a.kc = kcache; a.vc = vcache; a.pos = pos; a.out = out;
-  a.nchunk = (max_seq + 63) / 64;
-  a.part = (float *)workspace;
-  const size_t part = (size_t)batch * kvheads * a.nchunk * G * (2 + head_dim) * 4;
-  a.cnt = (int32_t *)((char *)workspace + (part + 255) / 256 * 256);
+  a.q = q; a.kc = kcache; a.vc = vcache; a.pos = pos;
+  a.nchunk = (max_seq + attn_chunk(head_dim) - 1) / attn_chunk(head_dim);
+  const size_t ctx = (size_t)batch * a.nchunk * heads * head_dim * 4;
+  a.pctx = (float *)workspace;
+  a.pmz = (float *)((char *)workspace + (ctx + 255) / 256 * 256);
   a.heads = heads; a.kvheads = kvheads; a.max_seq = max_seq;
   a.coef = 1.0f / sqrtf((float)head_dim);  // (/ 1.0 (sqrt (float hd)))
-  const dim3 grid(a.nchunk, kvheads, batch), blk(256);
+  const dim3 grid(a.nchunk, kvheads, batch), blk(ATTN_WAVES * 64);
   hipStream_t st = nlg_stream(stream);
-#define AT(HD, GG) hipLaunchKernelGGL((k_attn_f16<HD, GG>), grid, blk, 0, st, a)
+#define AT(HD, GG) hipLaunchKernelGGL((k_attn_part<HD, GG, ATTN_NI>), grid, blk, 0, st, a)
   if (head_dim == 128) {
     if (G == 1) AT(128, 1); else if (G == 2) AT(128, 2); else if (G == 4) AT(128, 4); else AT(128, 8);
   } else {
@@ -636,5 +680,9 @@ extern "C" int nlg_decode_attn_f16(const float *q, const uint16_t *kcache, const
   }
 #undef AT
   NLG_LAUNCHED("decode attention (fp16 KV)");
+  const uint64_t n = (uint64_t)batch * heads * head_dim;
+  hipLaunchKernelGGL(k_attn_merge, dim3(nlg_blocks(n, 256)), dim3(256), 0, st, a.pctx, a.pmz, out, batch,
+                     heads, head_dim, a.nchunk);
+  NLG_LAUNCHED("decode attention merge");
   return NLG_OK;
 }

@@ -158,7 +158,16 @@ struct TernArgs {
   float *y;              // [seq x out]
   uint32_t seq, out, cols, ng, wng;
   int beta_per_row;
+  uint32_t wpb;          // waves per block (set by the launcher)
 };
+
+// Pin every argument into SGPRs at the top of a kernel: each kernel-argument
+// fetch the compiler defers to first use is another memory round trip on the
+// kernel's critical path.
+#define TERN_PIN_ARGS(a)                                                                   \
+  asm volatile("" ::"s"((a).xq), "s"((a).gamma), "s"((a).w2), "s"((a).bias), "s"((a).beta), \
+               "s"((a).y), "s"((a).seq), "s"((a).out), "s"((a).cols), "s"((a).ng),          \
+               "s"((a).wng), "s"((a).beta_per_row), "s"((a).wpb))
 
 __device__ __forceinline__ void tern_store(const TernArgs &a, uint32_t s, uint32_t o, int acc64) {
   const float acc = (float)(acc64 >> 6);  // exact: acc64 is a multiple of 64
@@ -174,7 +183,8 @@ __device__ __forceinline__ void tern_store(const TernArgs &a, uint32_t s, uint32
 template <int R, int ST>
 __global__ __launch_bounds__(256) void k_tern_i8_fast(TernArgs a) {
   const int lane = threadIdx.x & 63;
-  const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  TERN_PIN_ARGS(a);
+  const uint32_t wave = blockIdx.x * a.wpb + (threadIdx.x >> 6);
   const uint32_t row0 = wave * R;
   if (row0 >= a.out) return;  // wave-uniform
   const uint32_t s0 = blockIdx.y * ST;
@@ -249,7 +259,8 @@ __global__ __launch_bounds__(256) void k_tern_i8_fast(TernArgs a) {
 template <int R, int CPL>
 __global__ __launch_bounds__(256) void k_tern_i8_dec(TernArgs a) {
   const int lane = threadIdx.x & 63;
-  const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  TERN_PIN_ARGS(a);
+  const uint32_t wave = blockIdx.x * a.wpb + (threadIdx.x >> 6);
   const uint32_t row0 = wave * R;
   if (row0 >= a.out) return;  // wave-uniform
   const uint32_t nchunk = a.wng >> 2;
@@ -314,7 +325,8 @@ __global__ __launch_bounds__(256) void k_tern_i8_dec(TernArgs a) {
 template <int R>
 __global__ __launch_bounds__(256) void k_tern_i8_any(TernArgs a) {
   const int lane = threadIdx.x & 63;
-  const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  TERN_PIN_ARGS(a);
+  const uint32_t wave = blockIdx.x * a.wpb + (threadIdx.x >> 6);
   const uint32_t row0 = wave * R;
   if (row0 >= a.out) return;
   const uint32_t tok = blockIdx.y;
@@ -347,7 +359,9 @@ __global__ __launch_bounds__(256) void k_tern_i8_any(TernArgs a) {
 }
 
 // Launch geometry.  rows_per_wave in {1,2,4,8}, waves_per_block in {1,2,4}.
-static int tern_launch(const TernArgs &a, int rows_per_wave, int waves_per_block, hipStream_t st) {
+static int tern_launch(const TernArgs &a0, int rows_per_wave, int waves_per_block, hipStream_t st) {
+  TernArgs a = a0;
+  a.wpb = (uint32_t)waves_per_block;
   if (!a.seq || !a.out) return NLG_OK;
   if (a.cols > 131072) return nlg_fail("ternary linear: cols %u > 131072", a.cols);
   const bool fast = (a.cols % 64 == 0) && (((uintptr_t)a.w2 & 15) == 0) &&
