@@ -18,6 +18,10 @@ the same GEMV kernel over all 128 copies stacked into one [524288 x 4096]
 launch (launch cost amortised: the kernel's streaming rate), and the
 measured launch floor (an empty kernel, back to back).
 cpu_baseline: the CPU restatement (oracle/) of the same step on host cores.
+decode: config 5, the 30-layer ternary decoder stack at batch 1 and 32 --
+tokens/s over 256 greedy steps after a 512-token prompt, the step's
+algorithmic bytes (every weight, the LM head, K/V of the cached positions)
+over its time, and each kernel of a step timed alone at the last position.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep]
 """
@@ -141,6 +145,118 @@ def gpu_bench(steps: int, warmup: int, sweep: bool):
     return res
 
 
+# ---------------------------------------------------------------- config 5
+
+STACK = dict(layers=30, d_model=2560, heads=20, kv_heads=5, head_dim=128, d_ff=6912, vocab=128256)
+PROMPT, DECODE = 512, 256
+
+
+class _Ptr:
+    """A device pointer from the stack, shaped like nlgpu.DeviceArray."""
+
+    def __init__(self, ptr, nbytes):
+        self.ptr, self.nbytes = ptr, nbytes
+
+
+def _tensor(s, name, layer=-1):
+    import ctypes as C
+    import nlgpu
+    p, n = C.c_void_p(), C.c_size_t(0)
+    if nlgpu.lib().nlg_stack_tensor(s.h, name.encode(), layer, C.byref(p), C.byref(n)):
+        raise nlgpu.NlgError(nlgpu.last_error())
+    return _Ptr(p.value, n.value)
+
+
+def _per_launch_us(fn, n, stream):
+    """us per launch of fn(i), i = 0..n-1, captured in one graph."""
+    import nlgpu
+    nlgpu.graph_begin(stream)
+    for i in range(n):
+        fn(i)
+    g = nlgpu.graph_end(stream)
+    nlgpu.graph_launch(g, stream)
+    e0, e1 = nlgpu.Event(), nlgpu.Event()
+    e0.record(stream)
+    for _ in range(3):
+        nlgpu.graph_launch(g, stream)
+    e1.record(stream)
+    us = e0.elapsed_ms(e1) * 1e3 / (3 * n)
+    nlgpu.graph_destroy(g)
+    return us
+
+
+def decode_bench(batch: int, stream):
+    """Config 5: prefill 512 random ids (teacher-forced token steps), then 256
+    greedy steps, one captured graph per step; then each kernel of a step
+    timed on its own over the 30 layers' weights."""
+    import nlgpu
+    c = STACK
+    max_seq = PROMPT + DECODE
+    s = nlgpu.Stack(**c, max_seq=max_seq, batch=batch, seed=20260921 + 5)
+    ids = (nlgpu.uniform(20260921 + 55, batch * PROMPT) * c["vocab"]).astype(np.int32).reshape(batch, PROMPT)
+    s.start(ids)
+    e0, e1, e2 = nlgpu.Event(), nlgpu.Event(), nlgpu.Event()
+    s.step(1)  # capture
+    e0.record(stream)
+    s.step(PROMPT - 1)
+    e1.record(stream)
+    s.step(DECODE)
+    e2.record(stream)
+    prefill_ms, decode_ms = e0.elapsed_ms(e1), e1.elapsed_ms(e2)
+    toks, _ = s.tokens()
+    assert (toks[:, :max_seq] >= 0).all()
+    # per-kernel, at the last position (768 cached), rotating over the layers
+    L, d, f = c["layers"], c["d_model"], c["d_ff"]
+    nq, nkv = c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"]
+    T = lambda n, l=-1: _tensor(s, n, l)
+    x, co, si = T("x"), T("rope_cos"), T("rope_sin")
+    pos = nlgpu.to_device(np.array([max_seq - 1], np.int32))
+    q = nlgpu.DeviceArray(batch * nq * 4)
+    h = nlgpu.DeviceArray(batch * f * 4)
+    ws = nlgpu.DeviceArray(nlgpu.decode_attn_f16_workspace(batch, c["heads"], c["kv_heads"], c["head_dim"], max_seq))
+    ly = [{k: T(k, l) for k in ("wqkv", "bqkv", "wo", "bo", "wgu", "bgu", "wd", "bd", "gattn", "gffn", "kc", "vc")}
+          for l in range(L)]
+    eps = 1e-5
+    n = 4 * L
+    kv_bytes = batch * max_seq * nkv * 2 * 2  # K and V, fp16, every cached position
+    kern = {
+        "qkv_rope_append": (lambda i: nlgpu.rms_ternary_qkv_rope(
+            x, ly[i % L]["gattn"], eps, ly[i % L]["wqkv"], ly[i % L]["bqkv"], q, ly[i % L]["kc"], ly[i % L]["vc"],
+            co, si, pos, batch, c["heads"], c["kv_heads"], c["head_dim"], max_seq, d, stream=stream),
+            (nq + 2 * nkv) * d // 4 + batch * (d * 4 + nq * 4 + 2 * nkv * 2)),
+        "attention_chunks": (lambda i: nlgpu.decode_attn_f16_chunks(
+            q, ly[i % L]["kc"], ly[i % L]["vc"], pos, batch, c["heads"], c["kv_heads"], c["head_dim"], max_seq, ws,
+            stream=stream), kv_bytes + batch * nq * 4),
+        "attn_merge_o_proj_residual": (lambda i: nlgpu.attn_ternary_linear_residual(
+            ws, batch, c["heads"], c["kv_heads"], c["head_dim"], max_seq, ly[i % L]["wo"], None, ly[i % L]["bo"],
+            x, x, d, stream=stream), d * nq // 4 + batch * d * 8),
+        "rms_gate_up_swiglu": (lambda i: nlgpu.rms_ternary_swiglu(
+            x, ly[i % L]["gffn"], eps, ly[i % L]["wgu"], ly[i % L]["bgu"], h, batch, f, d, stream=stream),
+            2 * f * d // 4 + batch * (d * 4 + f * 4)),
+        "down_proj_residual": (lambda i: nlgpu.ternary_linear_residual(
+            h, ly[i % L]["wd"], None, ly[i % L]["bd"], x, x, batch, d, f, stream=stream),
+            d * f // 4 + batch * (f * 4 + d * 8)),
+    }
+    per = {}
+    for name, (fn, nbytes) in kern.items():
+        us = _per_launch_us(fn, n, stream)
+        per[name] = {"us": round(us, 3), "bytes": int(nbytes), "gbs": round(nbytes / us / 1e3, 1),
+                     "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+    lm_bytes = c["vocab"] * d // 4 + batch * (d * 4 + c["vocab"] * 4)
+    ms_tok = decode_ms / DECODE
+    layer_bytes = (nq + 2 * nkv) * d // 4 + d * nq // 4 + 2 * f * d // 4 + d * f // 4
+    # per step: every weight once, the LM head, and K/V of the cached positions
+    mean_len = PROMPT + (DECODE + 1) / 2.0
+    step_bytes = L * layer_bytes + c["vocab"] * d // 4 + L * batch * mean_len * nkv * 2 * 2
+    s.close()
+    return {"batch": batch, "tok_s": round(batch * DECODE / (decode_ms * 1e-3), 1),
+            "ms_per_step": round(ms_tok, 4), "prefill_ms": round(prefill_ms, 2),
+            "prefill": "512 prompt tokens as teacher-forced single-token steps (same graph)",
+            "step_bytes": int(step_bytes), "step_gbs": round(step_bytes / (ms_tok * 1e-3) / 1e9, 1),
+            "step_frac": round(step_bytes / (ms_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "launches_per_step": L * 5 + 2, "lm_head_bytes": int(lm_bytes), "per_kernel": per}
+
+
 def cpu_baseline(x, w_one, seconds: float):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import nlg_oracle as orc
@@ -166,12 +282,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--sweep", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decoder stack")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the decode path is not sharded); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     r = gpu_bench(args.steps, args.warmup, args.sweep)
+    decode = {}
+    if not args.no_decode:
+        import nlgpu
+        stream = nlgpu.lib().nlg_default_stream()
+        for b in (1, 32):
+            decode[f"batch{b}"] = decode_bench(b, stream)
     value = STEP_BYTES / (r["step_ms"] * 1e-3) / 1e9
     gemv_gbs = GEMV_BYTES / (r["gemv_ms"] * 1e-3) / 1e9
     stacked_gbs = GEMV_BYTES * COPIES / (r["stacked_ms"] * 1e-3) / 1e9
@@ -205,6 +328,10 @@ def main():
         "cpu_baseline": cpu,
         "device": r["device"],
     }
+    if decode:
+        out["decode"] = dict(decode, model="30-layer ternary decoder, d 2560, 20/5 heads x 128, d_ff 6912, "
+                                           "vocab 128256 (ternary LM head), fp16 KV, random-init seeded weights, "
+                                           "prompt 512 random ids then 256 greedy tokens")
     if "sweep_us" in r:
         out["sweep_us"] = r["sweep_us"]
     print(json.dumps(out), flush=True)

@@ -247,6 +247,26 @@ int nlg_decode_attn_f16(const float *q, const uint16_t *kcache, const uint16_t *
 size_t nlg_decode_attn_f16_workspace(uint32_t batch, uint32_t heads, uint32_t kvheads,
                                      uint32_t head_dim, uint32_t max_seq);
 
+/* The first of those launches alone: per chunk of positions and head, the
+ * chunk's max score, sum of exp and exp-weighted sum of V, left in
+ * `workspace` for nlg_attn_ternary_linear_residual. */
+int nlg_decode_attn_f16_chunks(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                               const int32_t *pos, uint32_t batch, uint32_t heads, uint32_t kvheads,
+                               uint32_t head_dim, uint32_t max_seq, void *workspace,
+                               size_t workspace_bytes, void *stream);
+
+/* The attention output projection with the chunk merge folded into it:
+ * y = res + linear(attention), where attention is what nlg_decode_attn_f16
+ * would return from the partials in `workspace` (bit-identical to running
+ * that merge and then nlg_ternary_linear_residual).  One launch; needs
+ * max_seq short enough for at most 4 chunks: max_seq <= 1024 at head_dim
+ * 128, <= 2048 at 64 (longer caches: NLG_ERR, use the two calls above). */
+int nlg_attn_ternary_linear_residual(const void *workspace, size_t workspace_bytes, uint32_t batch,
+                                     uint32_t heads, uint32_t kvheads, uint32_t head_dim,
+                                     uint32_t max_seq, const uint32_t *w2, const float *bias,
+                                     const float *beta, int beta_per_row, const float *res, float *y,
+                                     uint32_t out, void *stream);
+
 /* ------------------------------------------------------------------------
  * A random-initialised ternary decoder stack (pre-norm, SwiGLU, GQA, RoPE,
  * fp16 KV cache, ternary LM head, greedy decode) built from the fusions

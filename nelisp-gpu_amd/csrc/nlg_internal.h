@@ -143,7 +143,15 @@ __device__ __forceinline__ float nlg_block_max_f32(float v, float *scratch) {
 // ------------------------------------------------- fused quantise + GEMV
 // One launch: optional RMSNorm of the activation row, pack-act-rows'
 // quantisation into LDS, the 2-bit x int8 GEMV, and an epilogue.
-enum { NLG_PRO_NONE = 0, NLG_PRO_RMS = 1 };
+enum {
+  NLG_PRO_NONE = 0,  // x as given
+  NLG_PRO_RMS = 1,   // x = rmsnorm(x) * gain
+  NLG_PRO_ATTN = 2,  // x = decode attention merged from its chunk partials
+};
+// Most attention chunks the PRO_ATTN prologue merges, and how many chunks
+// the decode attention splits max_seq positions into.
+#define NLG_ATTN_MAX_CHUNKS 4
+uint32_t nlg_attn_chunk_count(uint32_t head_dim, uint32_t max_seq);
 enum {
   NLG_EPI_STORE = 0,   // y = bias + (beta*gamma)*acc
   NLG_EPI_RESID = 1,   // y = res + that
@@ -170,6 +178,10 @@ struct FusedArgs {
   const float *co, *si;  // RoPE tables [max_seq x hd/2]
   const int32_t *pos;    // device position (one for every row of the batch)
   uint16_t *kc, *vc;
+  // PRO_ATTN: x is [seq][attn_nc][cols] chunk contexts (a.x), with
+  // (max, sum) per chunk and head in attn_mz [seq][attn_nc][cols/hd][2]
+  const float *attn_mz;
+  uint32_t attn_nc;
   // EPI_ARGMAX: per wave (max, index), [seq x ceil(out/R)]
   float *pval;
   int32_t *pidx;

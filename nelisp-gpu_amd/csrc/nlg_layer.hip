@@ -64,13 +64,34 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   //    loads are straight-line (clamped addresses, validity applied with
   //    selects afterwards): a branch around a load makes the wait-count pass
   //    drain every outstanding load at the join.
-  const float4 *x4 = (const float4 *)(a.x + (size_t)tok * a.cols);
   const uint32_t nf4 = a.cols >> 2;
   float4 xv4[F4], gv4[F4];
+  // PRO_ATTN: the chunk contexts and (max, sum) pairs of every element
+  constexpr int NCA = PRO == NLG_PRO_ATTN ? NLG_ATTN_MAX_CHUNKS : 1;
+  float4 cx4[F4][NCA];
+  float2 mz2[F4][NCA];
+  if (PRO == NLG_PRO_ATTN) {
+    const float4 *c4 = (const float4 *)a.x;
+    const uint32_t heads = a.cols / a.hd;
 #pragma unroll
-  for (int k = 0; k < F4; k++) {
-    const uint32_t f = threadIdx.x + 256u * k;
-    xv4[k] = x4[f < nf4 ? f : nf4 - 1];
+    for (int k = 0; k < F4; k++) {
+      const uint32_t f = threadIdx.x + 256u * k, fc = f < nf4 ? f : nf4 - 1;
+      const uint32_t h = (4 * fc) / a.hd;
+#pragma unroll
+      for (int c = 0; c < NCA; c++) {
+        const uint32_t cc = (uint32_t)c < a.attn_nc ? (uint32_t)c : a.attn_nc - 1;
+        const size_t tc = (size_t)tok * a.attn_nc + cc;
+        cx4[k][c] = c4[tc * nf4 + fc];
+        mz2[k][c] = *(const float2 *)(a.attn_mz + (tc * heads + h) * 2);
+      }
+    }
+  } else {
+    const float4 *x4 = (const float4 *)(a.x + (size_t)tok * a.cols);
+#pragma unroll
+    for (int k = 0; k < F4; k++) {
+      const uint32_t f = threadIdx.x + 256u * k;
+      xv4[k] = x4[f < nf4 ? f : nf4 - 1];
+    }
   }
   if (PRO == NLG_PRO_RMS) {
     const float4 *g4 = (const float4 *)a.gain;
@@ -122,6 +143,29 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
 #pragma unroll
     for (int i = 0; i < CPL; i++)
       if (lane + 64u * i >= nchunk) wv[r][i] = make_uint4(0, 0, 0, 0);
+  // 2a. attention merge: x = sum_c ctx_c*exp(m_c - M) / sum_c z_c*exp(m_c - M)
+  //     in k_attn_merge's exact operation order, so the two agree bit for bit
+  if (PRO == NLG_PRO_ATTN) {
+#pragma unroll
+    for (int k = 0; k < F4; k++) {
+      float mm = -1.0e30f;
+#pragma unroll
+      for (int c = 0; c < NCA; c++) mm = mz2[k][c].x > mm ? mz2[k][c].x : mm;
+      float zz = 0.0f;
+      float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+      for (int c = 0; c < NCA; c++) {
+        const float sc = (uint32_t)c < a.attn_nc ? expf(mz2[k][c].x - mm) : 0.0f;
+        zz = fmaf(mz2[k][c].y, sc, zz);
+        acc.x = fmaf(cx4[k][c].x, sc, acc.x);
+        acc.y = fmaf(cx4[k][c].y, sc, acc.y);
+        acc.z = fmaf(cx4[k][c].z, sc, acc.z);
+        acc.w = fmaf(cx4[k][c].w, sc, acc.w);
+      }
+      xv4[k] = make_float4(acc.x / zz, acc.y / zz, acc.z / zz, acc.w / zz);
+      if (threadIdx.x + 256u * k >= nf4) xv4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  }
   // 2. RMSNorm: S = 1/sqrt(sum(x*x)/N + eps); C = (X*S)*G
   if (PRO == NLG_PRO_RMS) {
     float sq = 0.0f;
@@ -266,6 +310,7 @@ static void fused_go(const FusedArgs &a, dim3 grid, size_t lds, hipStream_t st) 
 #define FZ(CC)                                                                                  \
   do {                                                                                          \
     if (a.cols <= 2048) hipLaunchKernelGGL((k_tern_fused<R, CC, 2, PRO, EPI>), grid, blk, lds, st, a); \
+    else if (a.cols <= 3072) hipLaunchKernelGGL((k_tern_fused<R, CC, 3, PRO, EPI>), grid, blk, lds, st, a); \
     else if (a.cols <= 4096) hipLaunchKernelGGL((k_tern_fused<R, CC, 4, PRO, EPI>), grid, blk, lds, st, a); \
     else if (a.cols <= 8192) hipLaunchKernelGGL((k_tern_fused<R, CC, 8, PRO, EPI>), grid, blk, lds, st, a); \
     else hipLaunchKernelGGL((k_tern_fused<R, CC, 16, PRO, EPI>), grid, blk, lds, st, a);       \
@@ -308,6 +353,11 @@ int nlg_fused_launch(const FusedArgs &a0, int pro, int epi, int rpw, hipStream_t
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_SWIGLU) PE(NLG_PRO_RMS, NLG_EPI_SWIGLU);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_QKV) PE(NLG_PRO_RMS, NLG_EPI_QKV);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_ARGMAX) PE(NLG_PRO_RMS, NLG_EPI_ARGMAX);
+  else if (pro == NLG_PRO_ATTN && epi == NLG_EPI_RESID) {
+    if (!a.hd || a.hd % 4 || a.cols % a.hd || !a.attn_nc || a.attn_nc > NLG_ATTN_MAX_CHUNKS || !a.attn_mz)
+      return nlg_fail("fused ternary linear: bad attention partials (hd %u, chunks %u)", a.hd, a.attn_nc);
+    PE(NLG_PRO_ATTN, NLG_EPI_RESID);
+  }
   else return nlg_fail("fused ternary linear: unsupported prologue/epilogue %d/%d", pro, epi);
 #undef PE
   NLG_LAUNCHED("fused ternary linear");
@@ -460,11 +510,19 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// Positions per workgroup for head dim HD: 8 waves x ATTN_NI instructions x
-// (64 / (HD/8)) positions per instruction.
-#define ATTN_NI 4
+// Positions per workgroup for head dim HD: 8 waves x NI instructions x
+// (64 / (HD/8)) positions per instruction; NI = 8 when 4 would need more
+// chunks than the O-projection's prologue merges.
 #define ATTN_WAVES 8
-static inline uint32_t attn_chunk(uint32_t hd) { return ATTN_WAVES * ATTN_NI * (64u / (hd / 8u)); }
+static inline uint32_t attn_ni(uint32_t hd, uint32_t max_seq) {
+  const uint32_t cs4 = ATTN_WAVES * 4u * (64u / (hd / 8u));
+  return (max_seq + cs4 - 1) / cs4 > NLG_ATTN_MAX_CHUNKS ? 8u : 4u;
+}
+static inline uint32_t attn_chunks(uint32_t hd, uint32_t max_seq) {
+  const uint32_t cs = ATTN_WAVES * attn_ni(hd, max_seq) * (64u / (hd / 8u));
+  return (max_seq + cs - 1) / cs;
+}
+uint32_t nlg_attn_chunk_count(uint32_t head_dim, uint32_t max_seq) { return attn_chunks(head_dim, max_seq); }
 
 // Pass 1: one workgroup per (chunk, kv head, sequence) scores its chunk's
 // positions for every query head of that kv head (K and V read once) and
@@ -640,11 +698,79 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ pc
 
 extern "C" size_t nlg_decode_attn_f16_workspace(uint32_t batch, uint32_t heads, uint32_t kvheads,
                                                 uint32_t head_dim, uint32_t max_seq) {
-  if (!kvheads || (head_dim != 64 && head_dim != 128)) return 0;
-  (void)kvheads;
-  const size_t nchunk = (max_seq + attn_chunk(head_dim) - 1) / attn_chunk(head_dim);
+  if (!kvheads || (head_dim != 64 && head_dim != 128) || !max_seq) return 0;
+  const size_t nchunk = attn_chunks(head_dim, max_seq);
   const size_t ctx = (size_t)batch * nchunk * heads * head_dim * 4;
   return (ctx + 255) / 256 * 256 + (size_t)batch * nchunk * heads * 2 * 4;
+}
+
+// Validate and lay out the workspace; fills everything but q/kc/vc/pos.
+static int attn_setup(AttnArgs &a, uint32_t batch, uint32_t heads, uint32_t kvheads, uint32_t head_dim,
+                      uint32_t max_seq, void *workspace, size_t workspace_bytes) {
+  if (!kvheads || !heads || heads % kvheads) return nlg_fail("decode attn: heads must be a multiple of kvheads");
+  const uint32_t G = heads / kvheads;
+  if (head_dim != 64 && head_dim != 128) return nlg_fail("decode attn: head_dim must be 64 or 128");
+  if (G != 1 && G != 2 && G != 4 && G != 8) return nlg_fail("decode attn: heads/kvheads must be 1, 2, 4 or 8");
+  if (!max_seq || batch > 65535 || kvheads > 65535) return nlg_fail("decode attn: bad max_seq/batch/kvheads");
+  const size_t need = nlg_decode_attn_f16_workspace(batch, heads, kvheads, head_dim, max_seq);
+  if (!workspace || workspace_bytes < need) return nlg_fail("decode attn: needs a %zu-byte workspace", need);
+  a.nchunk = attn_chunks(head_dim, max_seq);
+  const size_t ctx = (size_t)batch * a.nchunk * heads * head_dim * 4;
+  a.pctx = (float *)workspace;
+  a.pmz = (float *)((char *)workspace + (ctx + 255) / 256 * 256);
+  a.heads = heads; a.kvheads = kvheads; a.max_seq = max_seq;
+  a.coef = 1.0f / sqrtf((float)head_dim);  // (/ 1.0 (sqrt (float hd)))
+  return NLG_OK;
+}
+
+extern "C" int nlg_decode_attn_f16_chunks(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                                          const int32_t *pos, uint32_t batch, uint32_t heads,
+                                          uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
+                                          void *workspace, size_t workspace_bytes, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!batch) return NLG_OK;
+  AttnArgs a;
+  if (attn_setup(a, batch, heads, kvheads, head_dim, max_seq, workspace, workspace_bytes)) return NLG_ERR;
+  if (((uintptr_t)q & 15) || ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15))
+    return nlg_fail("decode attn: q and caches must be 16-byte aligned");
+  a.q = q; a.kc = kcache; a.vc = vcache; a.pos = pos;
+  const uint32_t G = heads / kvheads, ni = attn_ni(head_dim, max_seq);
+  const dim3 grid(a.nchunk, kvheads, batch), blk(ATTN_WAVES * 64);
+  hipStream_t st = nlg_stream(stream);
+#define AT(HD, GG)                                                                     \
+  do {                                                                                 \
+    if (ni == 8) hipLaunchKernelGGL((k_attn_part<HD, GG, 8>), grid, blk, 0, st, a);   \
+    else hipLaunchKernelGGL((k_attn_part<HD, GG, 4>), grid, blk, 0, st, a);           \
+  } while (0)
+  if (head_dim == 128) {
+    if (G == 1) AT(128, 1); else if (G == 2) AT(128, 2); else if (G == 4) AT(128, 4); else AT(128, 8);
+  } else {
+    if (G == 1) AT(64, 1); else if (G == 2) AT(64, 2); else if (G == 4) AT(64, 4); else AT(64, 8);
+  }
+#undef AT
+  NLG_LAUNCHED("decode attention (fp16 KV)");
+  return NLG_OK;
+}
+
+extern "C" int nlg_attn_ternary_linear_residual(const void *workspace, size_t workspace_bytes, uint32_t batch,
+                                                uint32_t heads, uint32_t kvheads, uint32_t head_dim,
+                                                uint32_t max_seq, const uint32_t *w2, const float *bias,
+                                                const float *beta, int beta_per_row, const float *res,
+                                                float *y, uint32_t out, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!batch) return NLG_OK;
+  AttnArgs t;
+  if (attn_setup(t, batch, heads, kvheads, head_dim, max_seq, (void *)workspace, workspace_bytes)) return NLG_ERR;
+  if (t.nchunk > NLG_ATTN_MAX_CHUNKS)
+    return nlg_fail("attention + linear: %u chunks (max_seq %u) exceed the %d the fused merge takes; "
+                    "use nlg_decode_attn_f16 and nlg_ternary_linear_residual", t.nchunk, max_seq,
+                    NLG_ATTN_MAX_CHUNKS);
+  if (!res) return nlg_fail("attention + linear: res is null");
+  FusedArgs a{};
+  a.x = t.pctx; a.attn_mz = t.pmz; a.attn_nc = t.nchunk; a.hd = head_dim;
+  a.w2 = w2; a.bias = bias; a.beta = beta; a.beta_per_row = beta_per_row;
+  a.seq = batch; a.out = out; a.cols = heads * head_dim; a.y = y; a.ystride = out; a.res = res; a.rstride = out;
+  return nlg_fused_launch(a, NLG_PRO_ATTN, NLG_EPI_RESID, 0, nlg_stream(stream));
 }
 
 extern "C" int nlg_decode_attn_f16(const float *q, const uint16_t *kcache, const uint16_t *vcache,
@@ -653,33 +779,12 @@ extern "C" int nlg_decode_attn_f16(const float *q, const uint16_t *kcache, const
                                    void *workspace, size_t workspace_bytes, void *stream) {
   if (nlg_ensure_init()) return NLG_ERR;
   if (!batch) return NLG_OK;
-  if (!kvheads || !heads || heads % kvheads) return nlg_fail("decode attn: heads must be a multiple of kvheads");
-  const uint32_t G = heads / kvheads;
-  if (head_dim != 64 && head_dim != 128) return nlg_fail("decode attn: head_dim must be 64 or 128");
-  if (G != 1 && G != 2 && G != 4 && G != 8) return nlg_fail("decode attn: heads/kvheads must be 1, 2, 4 or 8");
-  if (!max_seq || batch > 65535 || kvheads > 65535) return nlg_fail("decode attn: bad max_seq/batch/kvheads");
-  if (((uintptr_t)q & 15) || ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15))
-    return nlg_fail("decode attn: q and caches must be 16-byte aligned");
-  const size_t need = nlg_decode_attn_f16_workspace(batch, heads, kvheads, head_dim, max_seq);
-  if (!workspace || workspace_bytes < need) return nlg_fail("decode attn: needs a %zu-byte workspace", need);
+  if (nlg_decode_attn_f16_chunks(q, kcache, vcache, pos, batch, heads, kvheads, head_dim, max_seq, workspace,
+                                 workspace_bytes, stream))
+    return NLG_ERR;
   AttnArgs a;
-  a.q = q; a.kc = kcache; a.vc = vcache; a.pos = pos;
-  a.nchunk = (max_seq + attn_chunk(head_dim) - 1) / attn_chunk(head_dim);
-  const size_t ctx = (size_t)batch * a.nchunk * heads * head_dim * 4;
-  a.pctx = (float *)workspace;
-  a.pmz = (float *)((char *)workspace + (ctx + 255) / 256 * 256);
-  a.heads = heads; a.kvheads = kvheads; a.max_seq = max_seq;
-  a.coef = 1.0f / sqrtf((float)head_dim);  // (/ 1.0 (sqrt (float hd)))
-  const dim3 grid(a.nchunk, kvheads, batch), blk(ATTN_WAVES * 64);
+  attn_setup(a, batch, heads, kvheads, head_dim, max_seq, workspace, workspace_bytes);
   hipStream_t st = nlg_stream(stream);
-#define AT(HD, GG) hipLaunchKernelGGL((k_attn_part<HD, GG, ATTN_NI>), grid, blk, 0, st, a)
-  if (head_dim == 128) {
-    if (G == 1) AT(128, 1); else if (G == 2) AT(128, 2); else if (G == 4) AT(128, 4); else AT(128, 8);
-  } else {
-    if (G == 1) AT(64, 1); else if (G == 2) AT(64, 2); else if (G == 4) AT(64, 4); else AT(64, 8);
-  }
-#undef AT
-  NLG_LAUNCHED("decode attention (fp16 KV)");
   const uint64_t n = (uint64_t)batch * heads * head_dim;
   hipLaunchKernelGGL(k_attn_merge, dim3(nlg_blocks(n, 256)), dim3(256), 0, st, a.pctx, a.pmz, out, batch,
                      heads, head_dim, a.nchunk);

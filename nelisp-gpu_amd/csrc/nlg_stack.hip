@@ -180,6 +180,7 @@ struct nlg_stack {
   uint32_t nparts;
   void *attn_ws;
   size_t attn_ws_bytes;
+  bool attn_fused;  // merge folded into the output projection
   std::vector<void *> allocs;
   void *graph;
   uint32_t host_pos;
@@ -275,6 +276,7 @@ static int stack_alloc(nlg_stack *s) {
   s->greedy = (int32_t *)salloc(s, (size_t)B * c.max_seq * 4);
   s->attn_ws_bytes = nlg_decode_attn_f16_workspace(B, c.heads, c.kv_heads, c.head_dim, c.max_seq);
   s->attn_ws = salloc(s, s->attn_ws_bytes);
+  s->attn_fused = nlg_attn_chunk_count(c.head_dim, c.max_seq) <= NLG_ATTN_MAX_CHUNKS;
   if (!s->wlm || !s->blm || !s->gfinal || !s->emb || !s->co || !s->si || !s->x || !s->q || !s->att ||
       !s->h || !s->logits || !s->pval || !s->pidx || !s->pos || !s->plen || !s->prompt || !s->hist ||
       !s->greedy || !s->attn_ws)
@@ -352,6 +354,22 @@ extern "C" int nlg_stack_create(const nlg_stack_config *cfg, nlg_stack **out) {
   return NLG_OK;
 }
 
+// Attention and its output projection: chunk pass, then the merge folded
+// into the projection's prologue when the chunks fit it, else a separate
+// merge launch.
+static int stack_attention(nlg_stack *s, Layer &y) {
+  const nlg_stack_config &c = s->c;
+  const uint32_t B = c.batch, d = c.d_model;
+  if (s->attn_fused)
+    return nlg_decode_attn_f16_chunks(s->q, y.kc, y.vc, s->pos, B, c.heads, c.kv_heads, c.head_dim, c.max_seq,
+                                      s->attn_ws, s->attn_ws_bytes, nullptr) ||
+           nlg_attn_ternary_linear_residual(s->attn_ws, s->attn_ws_bytes, B, c.heads, c.kv_heads, c.head_dim,
+                                            c.max_seq, y.wo, nullptr, y.bo, 0, s->x, s->x, d, nullptr);
+  return nlg_decode_attn_f16(s->q, y.kc, y.vc, s->pos, s->att, B, c.heads, c.kv_heads, c.head_dim, c.max_seq,
+                             s->attn_ws, s->attn_ws_bytes, nullptr) ||
+         nlg_ternary_linear_residual(s->att, y.wo, nullptr, y.bo, 0, s->x, s->x, B, d, s->nq, nullptr);
+}
+
 // One token step for the whole batch, enqueued on the library stream.
 static int stack_enqueue(nlg_stack *s) {
   const nlg_stack_config &c = s->c;
@@ -361,9 +379,7 @@ static int stack_enqueue(nlg_stack *s) {
     if (nlg_rms_ternary_qkv_rope(s->x, y.gattn, c.rms_eps, y.wqkv, y.bqkv, 1, s->q, y.kc, y.vc, s->co,
                                  s->si, s->pos, B, c.heads, c.kv_heads, c.head_dim, c.max_seq, d,
                                  nullptr) ||
-        nlg_decode_attn_f16(s->q, y.kc, y.vc, s->pos, s->att, B, c.heads, c.kv_heads, c.head_dim,
-                            c.max_seq, s->attn_ws, s->attn_ws_bytes, nullptr) ||
-        nlg_ternary_linear_residual(s->att, y.wo, nullptr, y.bo, 0, s->x, s->x, B, d, s->nq, nullptr) ||
+        stack_attention(s, y) ||
         nlg_rms_ternary_swiglu(s->x, y.gffn, c.rms_eps, y.wgu, y.bgu, 1, s->h, B, f, d, nullptr) ||
         nlg_ternary_linear_residual(s->h, y.wd, nullptr, y.bd, 0, s->x, s->x, B, d, f, nullptr))
       return NLG_ERR;

@@ -100,6 +100,9 @@ def lib() -> C.CDLL:
         "nlg_rms_ternary_argmax_workspace": (sz, [u32, u32]),
         "nlg_decode_attn_f16": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, sz, vp]),
         "nlg_decode_attn_f16_workspace": (sz, [u32, u32, u32, u32, u32]),
+        "nlg_decode_attn_f16_chunks": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, sz, vp]),
+        "nlg_attn_ternary_linear_residual": (i32, [vp, sz, u32, u32, u32, u32, u32, vp, vp, vp, i32, vp,
+                                                   vp, u32, vp]),
         "nlg_stack_create": (i32, [C.POINTER(StackConfig), C.POINTER(vp)]),
         "nlg_stack_destroy": (None, [vp]),
         "nlg_stack_start": (i32, [vp, vp, u32]),
@@ -320,6 +323,21 @@ def decode_attn_f16(q, kc, vc, pos, out, batch, heads, kvheads, head_dim, max_se
     _check(lib().nlg_decode_attn_f16(q.ptr, kc.ptr, vc.ptr, pos.ptr, out.ptr, batch, heads, kvheads,
                                      head_dim, max_seq, workspace.ptr, workspace.nbytes, stream),
            "decode_attn_f16")
+
+
+def decode_attn_f16_chunks(q, kc, vc, pos, batch, heads, kvheads, head_dim, max_seq, workspace,
+                           stream=None) -> None:
+    _check(lib().nlg_decode_attn_f16_chunks(q.ptr, kc.ptr, vc.ptr, pos.ptr, batch, heads, kvheads,
+                                            head_dim, max_seq, workspace.ptr, workspace.nbytes, stream),
+           "decode_attn_f16_chunks")
+
+
+def attn_ternary_linear_residual(workspace, batch, heads, kvheads, head_dim, max_seq, w2, bias, beta,
+                                 res, y, out, beta_per_row=False, stream=None) -> None:
+    _check(lib().nlg_attn_ternary_linear_residual(workspace.ptr, workspace.nbytes, batch, heads, kvheads,
+                                                  head_dim, max_seq, w2.ptr, _ptr(bias), beta.ptr,
+                                                  int(beta_per_row), res.ptr, y.ptr, out, stream),
+           "attn_ternary_linear_residual")
 
 
 def decode_attn_f16_workspace(batch, heads, kvheads, head_dim, max_seq) -> int:

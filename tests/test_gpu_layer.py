@@ -191,3 +191,36 @@ def test_decode_attention_fp16(B, heads, kvh, hd, max_seq, positions):
         err = np.abs(got - want).max() / np.abs(want).max()
         print(f"  pos={pos} max err / max|out| = {err:.2e}", flush=True)
         assert err <= 2e-3
+
+
+@pytest.mark.parametrize("B,heads,kvh,hd,max_seq,pos", [(1, 20, 5, 128, 768, 640), (1, 20, 5, 128, 768, 0),
+                                                      (3, 8, 2, 64, 130, 129), (2, 16, 2, 128, 1024, 1000)])
+def test_attention_merge_folded_into_output_projection(B, heads, kvh, hd, max_seq, pos):
+    """chunks + fused merge/O-projection == full attention then the residual
+    linear, bit for bit (same merge arithmetic in both)."""
+    print(f"[gpu] attn+O B={B} heads={heads}/{kvh} hd={hd} max_seq={max_seq} pos={pos}", flush=True)
+    n = B * kvh * max_seq * hd
+    kc = nlgpu.to_device(nlgpu.normal(hd + 1, n).astype(np.float16).view(np.uint16))
+    vc = nlgpu.to_device(nlgpu.normal(hd + 2, n).astype(np.float16).view(np.uint16))
+    q = nlgpu.to_device(nlgpu.normal(hd + 3, B * heads * hd))
+    dpos = nlgpu.to_device(np.array([pos], np.int32))
+    d = 512
+    w2, beta = weights(d + hd, d, heads * hd, per_row=False)
+    dw, dbeta = nlgpu.to_device(w2), nlgpu.to_device(beta)
+    res = nlgpu.normal(d, B * d)
+    ws = nlgpu.DeviceArray(nlgpu.decode_attn_f16_workspace(B, heads, kvh, hd, max_seq))
+    att = nlgpu.DeviceArray(B * heads * hd * 4)
+    nlgpu.decode_attn_f16(q, kc, vc, dpos, att, B, heads, kvh, hd, max_seq, ws)
+    y_ref = nlgpu.to_device(res)
+    nlgpu.ternary_linear_residual(att, dw, None, dbeta, y_ref, y_ref, B, d, heads * hd)
+    y = nlgpu.to_device(res)
+    nlgpu.decode_attn_f16_chunks(q, kc, vc, dpos, B, heads, kvh, hd, max_seq, ws)
+    nlgpu.attn_ternary_linear_residual(ws, B, heads, kvh, hd, max_seq, dw, None, dbeta, y, y, d)
+    same_bits(y.download(f32, B * d), y_ref.download(f32, B * d))
+
+
+def test_folded_merge_rejects_too_many_chunks():
+    ws = nlgpu.DeviceArray(nlgpu.decode_attn_f16_workspace(1, 4, 1, 128, 2048))
+    d = nlgpu.DeviceArray(4 * 512)
+    with pytest.raises(nlgpu.NlgError, match="chunks"):
+        nlgpu.attn_ternary_linear_residual(ws, 1, 4, 1, 128, 2048, d, None, d, d, d, 4)
