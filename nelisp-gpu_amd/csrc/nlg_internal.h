@@ -182,14 +182,31 @@ struct FusedArgs {
   // (max, sum) per chunk and head in attn_mz [seq][attn_nc][cols/hd][2]
   const float *attn_mz;
   uint32_t attn_nc;
+  // batched form: int8 activations + gamma ([seq x cols] bytes, then
+  // [seq] floats at a 256-byte boundary); null = the library's scratch
+  void *act_scratch;
+  size_t act_scratch_bytes;
   // EPI_ARGMAX: per wave (max, index), [seq x ceil(out/R)]
   float *pval;
   int32_t *pidx;
   uint32_t nparts;
 };
 // Launch the fused kernel; rows_per_wave 0 picks a default.  Requires
-// cols % 64 == 0, cols <= 16384 and 16-byte aligned x and w2.
+// cols % 64 == 0, cols <= 16384 and 16-byte aligned x and w2.  With
+// NLG_BATCHED_MIN or more tokens and cols % 256 == 0 it runs the batched
+// form instead (per-token quantisation into library scratch, then the int8
+// matrix-core GEMM with the same epilogue).
 int nlg_fused_launch(const FusedArgs &a, int pro, int epi, int rows_per_wave, hipStream_t st);
+#define NLG_BATCHED_MIN 8
+bool nlg_batched(uint32_t seq, uint32_t cols);
+int nlg_batched_launch(const FusedArgs &a, int pro, int epi, hipStream_t st);
+// (max, index) partials per token an ARGMAX launch of `out` rows writes.
+uint32_t nlg_argmax_parts(uint32_t seq, uint32_t cols, uint32_t out);
+// Grow-only device scratch owned by the library (NULL on failure).  It
+// cannot grow while `st` is being captured into a graph.
+void *nlg_scratch(size_t bytes, hipStream_t st);
+// Bytes the batched form needs for seq tokens of cols columns.
+size_t nlg_batched_scratch_bytes(uint32_t seq, uint32_t cols);
 // The rows-per-wave the launcher uses for `out` rows in mode `epi`.
 int nlg_fused_rows_per_wave(uint32_t out, int epi);
 

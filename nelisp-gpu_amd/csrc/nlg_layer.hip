@@ -321,9 +321,16 @@ static void fused_go(const FusedArgs &a, dim3 grid, size_t lds, hipStream_t st) 
 #undef FZ
 }
 
+uint32_t nlg_argmax_parts(uint32_t seq, uint32_t cols, uint32_t out) {
+  if (nlg_batched(seq, cols)) return (out + 63) / 64;  // one per GEMM workgroup
+  const uint32_t rpw = (uint32_t)nlg_fused_rows_per_wave(out, NLG_EPI_ARGMAX);
+  return (out + rpw - 1) / rpw;
+}
+
 int nlg_fused_launch(const FusedArgs &a0, int pro, int epi, int rpw, hipStream_t st) {
   FusedArgs a = a0;
   if (!a.seq || !a.out) return NLG_OK;
+  if (nlg_batched(a.seq, a.cols)) return nlg_batched_launch(a, pro, epi, st);
   if (a.cols % 64 || a.cols > 16384 || !a.cols)
     return nlg_fail("fused ternary linear: cols must be a multiple of 64 in [64, 16384] (got %u)", a.cols);
   if (((uintptr_t)a.x & 15) || ((uintptr_t)a.w2 & 15) || (pro == NLG_PRO_RMS && ((uintptr_t)a.gain & 15)))
@@ -459,9 +466,11 @@ __global__ __launch_bounds__(1024) void k_argmax_parts(const float *pval, const 
 }
 
 extern "C" size_t nlg_rms_ternary_argmax_workspace(uint32_t seq, uint32_t vocab) {
+  // the larger of the two forms' partial counts, whatever cols the call uses
   const int rpw = nlg_fused_rows_per_wave(vocab, NLG_EPI_ARGMAX);
-  const size_t nparts = (vocab + rpw - 1) / rpw;
-  return seq * nparts * 8;
+  size_t nparts = (vocab + rpw - 1) / rpw;
+  if ((size_t)(vocab + 63) / 64 > nparts) nparts = (vocab + 63) / 64;
+  return (size_t)seq * nparts * 8;
 }
 
 extern "C" int nlg_rms_ternary_argmax(const float *x, const float *gain, float eps, const uint32_t *w2,
@@ -475,7 +484,7 @@ extern "C" int nlg_rms_ternary_argmax(const float *x, const float *gain, float e
     return nlg_fail("rms ternary argmax: needs a %zu-byte workspace", need);
   hipStream_t st = nlg_stream(stream);
   const int rpw = nlg_fused_rows_per_wave(vocab, NLG_EPI_ARGMAX);
-  const uint32_t nparts = (vocab + rpw - 1) / rpw;
+  const uint32_t nparts = nlg_argmax_parts(seq, cols, vocab);
   FusedArgs a{};
   a.x = x; a.gain = gain; a.eps = eps; a.w2 = w2; a.beta = beta; a.beta_per_row = beta_per_row;
   a.seq = seq; a.out = vocab; a.cols = cols; a.y = logits; a.ystride = vocab;

@@ -9,6 +9,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+#include <vector>
+
 #include "nlg_internal.h"
 
 static thread_local char g_err[1024];
@@ -61,9 +64,43 @@ int nlg_num_cu(void) { return g_num_cu; }
 
 hipStream_t nlg_stream(void *s) { return s ? (hipStream_t)s : g_stream; }
 
+// Library scratch for the batched linears' int8 activations: grown by
+// allocating a larger buffer; older ones stay allocated (a captured graph may
+// still use them) until nlg_shutdown.
+static std::vector<void *> g_scratch;
+static size_t g_scratch_bytes = 0;
+static std::mutex g_scratch_mu;
+
+void *nlg_scratch(size_t bytes, hipStream_t st) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (bytes <= g_scratch_bytes) return g_scratch.back();
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+    nlg_fail("batched linear: its %zu-byte scratch must be reserved before graph capture "
+             "(run the call once outside the capture first)", bytes);
+    return nullptr;
+  }
+  size_t want = g_scratch_bytes ? g_scratch_bytes : (1u << 20);
+  while (want < bytes) want *= 2;
+  void *p = nullptr;
+  if (hipMalloc(&p, want) != hipSuccess) {
+    nlg_fail("scratch: hipMalloc(%zu) failed", want);
+    return nullptr;
+  }
+  g_scratch.push_back(p);
+  g_scratch_bytes = want;
+  return p;
+}
+
 extern "C" int nlg_shutdown(void) {
   if (!g_inited) return NLG_OK;
   (void)hipDeviceSynchronize();
+  {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    for (void *p : g_scratch) (void)hipFree(p);
+    g_scratch.clear();
+    g_scratch_bytes = 0;
+  }
   if (g_stage) {
     (void)hipEventDestroy(g_stage_ev[0]);
     (void)hipEventDestroy(g_stage_ev[1]);

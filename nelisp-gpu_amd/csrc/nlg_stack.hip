@@ -265,8 +265,7 @@ static int stack_alloc(nlg_stack *s) {
   s->att = (float *)salloc(s, (size_t)B * s->nq * 4);
   s->h = (float *)salloc(s, (size_t)B * f * 4);
   s->logits = (float *)salloc(s, (size_t)B * c.vocab * 4);
-  const int rpw = nlg_fused_rows_per_wave(c.vocab, NLG_EPI_ARGMAX);
-  s->nparts = (c.vocab + rpw - 1) / rpw;  // one (max, index) per wave with rows
+  s->nparts = nlg_argmax_parts(B, d, c.vocab);
   s->pval = (float *)salloc(s, (size_t)B * s->nparts * 4);
   s->pidx = (int32_t *)salloc(s, (size_t)B * s->nparts * 4);
   s->pos = (int32_t *)salloc(s, 4);
@@ -277,6 +276,11 @@ static int stack_alloc(nlg_stack *s) {
   s->attn_ws_bytes = nlg_decode_attn_f16_workspace(B, c.heads, c.kv_heads, c.head_dim, c.max_seq);
   s->attn_ws = salloc(s, s->attn_ws_bytes);
   s->attn_fused = nlg_attn_chunk_count(c.head_dim, c.max_seq) <= NLG_ATTN_MAX_CHUNKS;
+  {  // reserve the batched linears' scratch now: it cannot grow under capture
+    uint32_t widest = d > f ? d : f;
+    widest = widest > s->nq ? widest : s->nq;
+    if (!nlg_scratch(nlg_batched_scratch_bytes(B, widest), nlg_stream(nullptr))) return NLG_ERR;
+  }
   if (!s->wlm || !s->blm || !s->gfinal || !s->emb || !s->co || !s->si || !s->x || !s->q || !s->att ||
       !s->h || !s->logits || !s->pval || !s->pidx || !s->pos || !s->plen || !s->prompt || !s->hist ||
       !s->greedy || !s->attn_ws)

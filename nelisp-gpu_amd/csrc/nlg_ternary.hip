@@ -449,8 +449,9 @@ extern "C" int nlg_ternary_linear_cfg(const float *x, const uint32_t *w2, const 
   if (nlg_ensure_init()) return NLG_ERR;
   if (!seq || !out) return NLG_OK;
   hipStream_t st = nlg_stream(stream);
-  const bool fusable = (cols % 64 == 0) && cols <= 16384 && (((uintptr_t)x & 15) == 0) &&
-                       (((uintptr_t)w2 & 15) == 0) && seq <= 4;
+  const bool aligned = (((uintptr_t)x & 15) == 0) && (((uintptr_t)w2 & 15) == 0);
+  // one launch for a few tokens; many tokens take the batched matrix-core form
+  const bool fusable = (cols % 64 == 0) && cols <= 16384 && aligned && (seq <= 4 || nlg_batched(seq, cols));
   if (fusable) {
     FusedArgs a{};
     a.x = x; a.w2 = w2; a.bias = bias; a.beta = beta; a.beta_per_row = beta_per_row;

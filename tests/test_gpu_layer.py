@@ -53,7 +53,8 @@ def same_bits(a, b):
     assert bad.size == 0, f"{bad.size} differ, first {bad[:4]}: {a[bad[:3]]} vs {b[bad[:3]]}"
 
 
-@pytest.mark.parametrize("seq,out,cols", [(1, 3840, 2560), (3, 100, 256), (2, 64, 6912), (1, 2560, 2560)])
+@pytest.mark.parametrize("seq,out,cols", [(1, 3840, 2560), (3, 100, 256), (2, 64, 6912), (1, 2560, 2560),
+                                          (16, 3840, 2560), (32, 2560, 2560), (9, 64, 6912)])
 def test_rms_linear_bit_exact_on_exact_sums(seq, out, cols):
     print(f"[gpu] rms linear seq={seq} out={out} cols={cols}", flush=True)
     x, g = int_rows(seq + out, seq * cols), gains(cols, cols)
@@ -86,7 +87,8 @@ def test_rms_linear_random_within_two_lanes(seq, out, cols):
 
 
 @pytest.mark.parametrize("inplace", [False, True])
-@pytest.mark.parametrize("seq,out,cols", [(1, 2560, 2560), (1, 2560, 6912), (3, 200, 320)])
+@pytest.mark.parametrize("seq,out,cols", [(1, 2560, 2560), (1, 2560, 6912), (3, 200, 320), (32, 2560, 6912),
+                                          (16, 2560, 2560)])
 def test_residual_linear_bit_exact(seq, out, cols, inplace):
     print(f"[gpu] residual seq={seq} out={out} cols={cols} inplace={inplace}", flush=True)
     x, res = nlgpu.normal(cols, seq * cols), nlgpu.normal(out, seq * out)
@@ -99,7 +101,8 @@ def test_residual_linear_bit_exact(seq, out, cols, inplace):
     same_bits(dy.download(f32, seq * out), want)
 
 
-@pytest.mark.parametrize("seq,dff,cols", [(1, 6912, 2560), (2, 96, 256), (1, 128, 6912)])
+@pytest.mark.parametrize("seq,dff,cols", [(1, 6912, 2560), (2, 96, 256), (1, 128, 6912), (32, 6912, 2560),
+                                          (8, 96, 256)])
 def test_swiglu(seq, dff, cols):
     print(f"[gpu] swiglu seq={seq} dff={dff} cols={cols}", flush=True)
     x, g = int_rows(dff + seq, seq * cols), gains(cols + 2, cols)
@@ -115,7 +118,8 @@ def test_swiglu(seq, dff, cols):
 
 
 QKV = [(1, 20, 5, 128, 2560, 768, 0), (1, 20, 5, 128, 2560, 768, 517), (2, 4, 2, 64, 256, 80, 79),
-       (3, 8, 8, 64, 512, 16, 3), (1, 4, 2, 64, 256, 80, 80)]
+       (3, 8, 8, 64, 512, 16, 3), (1, 4, 2, 64, 256, 80, 80), (32, 20, 5, 128, 2560, 768, 640),
+       (8, 4, 2, 64, 256, 80, 0)]
 
 
 @pytest.mark.parametrize("B,heads,kvh,hd,cols,max_seq,pos", QKV)
@@ -150,7 +154,8 @@ def test_qkv_rope_and_fp16_append(B, heads, kvh, hd, cols, max_seq, pos):
     assert np.all(kc == 0x7BCD) and np.all(vc == 0x7BCD)  # nothing else written
 
 
-@pytest.mark.parametrize("seq,vocab,cols,dup", [(1, 128256, 2560, False), (2, 1000, 256, True), (1, 37, 64, True)])
+@pytest.mark.parametrize("seq,vocab,cols,dup", [(1, 128256, 2560, False), (2, 1000, 256, True), (1, 37, 64, True),
+                                                (32, 128256, 2560, False), (8, 1000, 256, True)])
 def test_lm_head_argmax(seq, vocab, cols, dup):
     print(f"[gpu] argmax seq={seq} vocab={vocab} cols={cols}", flush=True)
     x, g = int_rows(vocab, seq * cols), gains(cols + 9, cols)
@@ -194,7 +199,8 @@ def test_decode_attention_fp16(B, heads, kvh, hd, max_seq, positions):
 
 
 @pytest.mark.parametrize("B,heads,kvh,hd,max_seq,pos", [(1, 20, 5, 128, 768, 640), (1, 20, 5, 128, 768, 0),
-                                                      (3, 8, 2, 64, 130, 129), (2, 16, 2, 128, 1024, 1000)])
+                                                      (3, 8, 2, 64, 130, 129), (2, 16, 2, 128, 1024, 1000),
+                                                      (32, 20, 5, 128, 768, 640), (8, 4, 2, 64, 80, 33)])
 def test_attention_merge_folded_into_output_projection(B, heads, kvh, hd, max_seq, pos):
     """chunks + fused merge/O-projection == full attention then the residual
     linear, bit for bit (same merge arithmetic in both)."""

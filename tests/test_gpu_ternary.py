@@ -119,7 +119,29 @@ def test_fused_linear_bit_exact(seq, out, cols, rpw):
     assert np.array_equal(dy.download(np.float32, seq * out).view(np.uint32), y_ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("seq,out,cols", [(16, 300, 2560), (2, 50, 1000), (5, 64, 4096)])
+BATCHED = [(8, 64, 256), (16, 300, 2560), (17, 2560, 2560), (32, 13824, 2560), (33, 2560, 6912),
+           (64, 512, 4096), (100, 256, 1024), (512, 2560, 2560), (512, 6912, 2560)]
+
+
+@pytest.mark.parametrize("seq,out,cols", BATCHED)
+def test_batched_matrix_core_linear_bit_exact(seq, out, cols):
+    """8+ tokens and cols % 256 == 0: per-token quantisation, then the int8
+    MFMA GEMM; same int32 accumulators and epilogue bits as the reference."""
+    print(f"[gpu] batched ternary seq={seq} out={out} cols={cols}", flush=True)
+    per_row = out % 2 == 0
+    t, w2, x, bias, beta = make(seq * 5 + out + cols, seq, out, cols, per_row=per_row)
+    xq, g = orc.pack_act_rows(x, seq, cols)
+    y_ref = orc.ternary_linear_i8(xq, g, w2, bias, beta, seq, out, cols, beta_per_row=per_row)
+    dy, dg = nlgpu.DeviceArray(seq * out * 4), nlgpu.DeviceArray(seq * 4)
+    nlgpu.ternary_linear(nlgpu.to_device(x), nlgpu.to_device(w2), nlgpu.to_device(bias), nlgpu.to_device(beta),
+                         dy, seq, out, cols, beta_per_row=per_row, gamma_out=dg)
+    assert np.array_equal(dg.download(np.float32, seq).view(np.uint32), g.view(np.uint32))
+    y = dy.download(np.float32, seq * out)
+    bad = np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} differ, first {bad[:5]}: {y[bad[:3]]} vs {y_ref[bad[:3]]}"
+
+
+@pytest.mark.parametrize("seq,out,cols", [(16, 300, 2496), (2, 50, 1000), (5, 64, 4096)])
 def test_linear_two_launch_path_with_workspace(seq, out, cols):
     t, w2, x, bias, beta = make(77 + seq, seq, out, cols)
     xq, g = orc.pack_act_rows(x, seq, cols)
