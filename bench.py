@@ -18,6 +18,7 @@ the same GEMV kernel over all 128 copies stacked into one [524288 x 4096]
 launch (launch cost amortised: the kernel's streaming rate), and the
 measured launch floor (an empty kernel, back to back).
 cpu_baseline: the CPU restatement (oracle/) of the same step on host cores.
+softmax_config3 / swiglu_ffn_config4: configs 3 and 4 at their full sizes.
 decode: config 5, the 30-layer ternary decoder stack at batch 1 and 32 --
 tokens/s over 256 greedy steps after a 512-token prompt, the step's
 algorithmic bytes (every weight, the LM head, K/V of the cached positions)
@@ -257,6 +258,86 @@ def decode_bench(batch: int, stream):
             "launches_per_step": L * 5 + 2, "lm_head_bytes": int(lm_bytes), "per_kernel": per}
 
 
+# ---------------------------------------------------------------- config 3
+
+SM_HEADS, SM_N = 32, 4096
+SM_BYTES = 2 * 4 * SM_HEADS * SM_N * SM_N  # read + write of every f32, 4,294,967,296
+
+
+def softmax_bench(stream):
+    """Config 3: row softmax in place over [32 x 4096 x 4096] f32 scores,
+    N(0, 3^2) with -inf above each head's diagonal (drawn on the device)."""
+    import nlgpu
+    n = SM_HEADS * SM_N * SM_N
+    a = nlgpu.DeviceArray(n * 4)
+    nlgpu.fill_normal(a, n, 20260921 + 3, 3.0, SM_N, stream=stream)
+    rows = SM_HEADS * SM_N
+    nlgpu.softmax_rows(a, a, rows, SM_N, stream=stream)  # warm
+    e0, e1 = nlgpu.Event(), nlgpu.Event()
+    reps = 5
+    e0.record(stream)
+    for _ in range(reps):
+        nlgpu.softmax_rows(a, a, rows, SM_N, stream=stream)
+    e1.record(stream)
+    ms = e0.elapsed_ms(e1) / reps
+    a.free()
+    gbs = SM_BYTES / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "bytes": SM_BYTES, "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "shape": [SM_HEADS, SM_N, SM_N], "kernel": "k_softmax_reg (one workgroup per row, in place)"}
+
+
+# ---------------------------------------------------------------- config 4
+
+FFN_D, FFN_F, FFN_COPIES = 2560, 6912, 40
+INT8_PEAK_TOPS = 5000.0
+
+
+def ffn_bench(stream):
+    """Config 4: h = silu(x Wg) * (x Wu), y = h Wd, all ternary 2-bit with
+    per-tensor scales and int8 absmax activations, at 1, 16 and 512 tokens;
+    40 distinct FFN weight copies (531 MB) rotated so weights stream from HBM."""
+    import nlgpu
+    seed = 20260921 + 4
+    tg = nlgpu.trits(seed, (FFN_F, FFN_D))
+    tu = nlgpu.trits(seed + 1, (FFN_F, FFN_D))
+    td = nlgpu.trits(seed + 2, (FFN_D, FFN_F))
+    gu = np.empty((2 * FFN_F, FFN_D // 16), np.uint32)
+    gu[0::2], gu[1::2] = nlgpu.pack_ternary(tg), nlgpu.pack_ternary(tu)
+    wd = nlgpu.pack_ternary(td)
+    dgu = nlgpu.DeviceArray(gu.nbytes * FFN_COPIES)
+    dwd = nlgpu.DeviceArray(wd.nbytes * FFN_COPIES)
+    for c in range(FFN_COPIES):
+        dgu.upload(np.roll(gu, 2 * c, axis=0), offset=c * gu.nbytes)
+        dwd.upload(np.roll(wd, c, axis=0), offset=c * wd.nbytes)
+    bgu = nlgpu.to_device(np.full(2 * FFN_F, 1.0 / np.sqrt(FFN_D / 2), np.float32))
+    bd = nlgpu.to_device(np.array([1.0 / np.sqrt(FFN_F / 2)], np.float32))
+    wbytes = gu.nbytes + wd.nbytes
+    out = {}
+    for B in (1, 16, 512):
+        x = nlgpu.to_device(nlgpu.normal(seed + 10 + B, B * FFN_D))
+        h = nlgpu.DeviceArray(B * FFN_F * 4)
+        y = nlgpu.DeviceArray(B * FFN_D * 4)
+
+        def ffn(i):
+            c = i % FFN_COPIES
+            nlgpu.rms_ternary_swiglu(x, None, 0.0, _Ptr(dgu.ptr + c * gu.nbytes, gu.nbytes), bgu, h, B, FFN_F,
+                                     FFN_D, stream=stream)
+            nlgpu.ternary_linear(h, _Ptr(dwd.ptr + c * wd.nbytes, wd.nbytes), None, bd, y, B, FFN_D, FFN_F,
+                                 stream=stream)
+        ffn(0)  # reserves the batched scratch outside the capture
+        us = _per_launch_us(ffn, FFN_COPIES, stream)
+        nbytes = wbytes + 2 * B * FFN_D * 4
+        ops = 2 * B * (2 * FFN_F * FFN_D + FFN_D * FFN_F)
+        r = {"us": round(us, 3), "bytes": int(nbytes), "gbs": round(nbytes / us / 1e3, 1),
+             "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "tops": round(ops / us / 1e6, 2),
+             "frac_int8_mfma": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
+             "path": "fused GEMV (2 launches)" if B < 8 else "per-token quantise + int8 MFMA GEMM (4 launches)"}
+        out[f"B{B}"] = r
+    dgu.free()
+    dwd.free()
+    return out
+
+
 def cpu_baseline(x, w_one, seconds: float):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import nlg_oracle as orc
@@ -295,6 +376,12 @@ def main():
         stream = nlgpu.lib().nlg_default_stream()
         for b in (1, 32):
             decode[f"batch{b}"] = decode_bench(b, stream)
+    extra = {}
+    if not args.no_decode:
+        import nlgpu
+        stream = nlgpu.lib().nlg_default_stream()
+        extra["softmax_config3"] = softmax_bench(stream)
+        extra["swiglu_ffn_config4"] = ffn_bench(stream)
     value = STEP_BYTES / (r["step_ms"] * 1e-3) / 1e9
     gemv_gbs = GEMV_BYTES / (r["gemv_ms"] * 1e-3) / 1e9
     stacked_gbs = GEMV_BYTES * COPIES / (r["stacked_ms"] * 1e-3) / 1e9
@@ -332,6 +419,7 @@ def main():
         out["decode"] = dict(decode, model="30-layer ternary decoder, d 2560, 20/5 heads x 128, d_ff 6912, "
                                            "vocab 128256 (ternary LM head), fp16 KV, random-init seeded weights, "
                                            "prompt 512 random ids then 256 greedy tokens")
+    out.update(extra)
     if "sweep_us" in r:
         out["sweep_us"] = r["sweep_us"]
     print(json.dumps(out), flush=True)

@@ -206,7 +206,8 @@ int nlg_ternary_linear_residual(const float *x, const uint32_t *w2, const float 
 
 /* SwiGLU: w2gu holds 2*dff rows, row 2j = gate row j, row 2j+1 = up row j;
  * g, u = linear(rmsnorm(x)); h[j] = (g * (1/(1 + exp(0 - g)))) * u
- * (silu-mul, kernels.el:186-193).  beta indexes the interleaved rows. */
+ * (silu-mul, kernels.el:186-193).  beta indexes the interleaved rows.
+ * gain NULL: no RMSNorm (g, u = linear(x)). */
 int nlg_rms_ternary_swiglu(const float *x, const float *gain, float eps, const uint32_t *w2gu,
                            const float *beta, int beta_per_row, float *h, uint32_t seq,
                            uint32_t dff, uint32_t cols, void *stream);
@@ -266,6 +267,12 @@ int nlg_attn_ternary_linear_residual(const void *workspace, size_t workspace_byt
                                      uint32_t max_seq, const uint32_t *w2, const float *bias,
                                      const float *beta, int beta_per_row, const float *res, float *y,
                                      uint32_t out, void *stream);
+
+/* Synthetic data: n floats of sigma * N(0,1) from a counter-based
+ * SplitMix64 stream (element 2p, 2p+1 = Box-Muller pair p); causal > 0 treats
+ * the data as [.. x causal x causal] score tiles and writes -inf above each
+ * tile's diagonal (the config-3 softmax input). */
+int nlg_fill_normal(float *dev, uint64_t n, uint64_t seed, float sigma, uint32_t causal, void *stream);
 
 /* ------------------------------------------------------------------------
  * A random-initialised ternary decoder stack (pre-norm, SwiGLU, GQA, RoPE,

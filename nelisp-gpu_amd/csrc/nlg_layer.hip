@@ -358,6 +358,7 @@ int nlg_fused_launch(const FusedArgs &a0, int pro, int epi, int rpw, hipStream_t
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_STORE) PE(NLG_PRO_RMS, NLG_EPI_STORE);
   else if (pro == NLG_PRO_NONE && epi == NLG_EPI_RESID) PE(NLG_PRO_NONE, NLG_EPI_RESID);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_SWIGLU) PE(NLG_PRO_RMS, NLG_EPI_SWIGLU);
+  else if (pro == NLG_PRO_NONE && epi == NLG_EPI_SWIGLU) PE(NLG_PRO_NONE, NLG_EPI_SWIGLU);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_QKV) PE(NLG_PRO_RMS, NLG_EPI_QKV);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_ARGMAX) PE(NLG_PRO_RMS, NLG_EPI_ARGMAX);
   else if (pro == NLG_PRO_ATTN && epi == NLG_EPI_RESID) {
@@ -403,7 +404,7 @@ extern "C" int nlg_rms_ternary_swiglu(const float *x, const float *gain, float e
   FusedArgs a{};
   a.x = x; a.gain = gain; a.eps = eps; a.w2 = w2gu; a.beta = beta; a.beta_per_row = beta_per_row;
   a.seq = seq; a.out = 2 * dff; a.cols = cols; a.y = h; a.ystride = dff;
-  return nlg_fused_launch(a, NLG_PRO_RMS, NLG_EPI_SWIGLU, 0, nlg_stream(stream));
+  return nlg_fused_launch(a, gain ? NLG_PRO_RMS : NLG_PRO_NONE, NLG_EPI_SWIGLU, 0, nlg_stream(stream));
 }
 
 extern "C" int nlg_rms_ternary_qkv_rope(const float *x, const float *gain, float eps, const uint32_t *w2qkv,

@@ -69,14 +69,30 @@ __global__ void k_gen_uniform(float *dst, uint64_t n, uint64_t seed, double lo, 
 
 // Element 2p and 2p+1 share the pair (u1 = 1 - u(2p), u2 = u(2p+1)):
 // r cos(2 pi u2) and r sin(2 pi u2), r = sqrt(-2 ln u1).
-__global__ void k_gen_normal(float *dst, uint64_t n, uint64_t seed) {
+// sigma * that; with causal > 0 the data is [.. x causal x causal] score
+// tiles and entries with column > row are -inf.
+__global__ void k_gen_normal(float *dst, uint64_t n, uint64_t seed, float sigma, uint32_t causal) {
   for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n;
        i += (uint64_t)gridDim.x * blockDim.x) {
     const uint64_t p = i >> 1;
     const double u1 = 1.0 - sm_uniform(seed, 2 * p), u2 = sm_uniform(seed, 2 * p + 1);
     const double r = sqrt(-2.0 * log(u1)), t = 6.283185307179586 * u2;
-    dst[i] = (float)(r * ((i & 1) ? sin(t) : cos(t)));
+    float v = (float)(r * ((i & 1) ? sin(t) : cos(t)));
+    if (sigma != 1.0f) v = v * sigma;
+    if (causal && (i % causal) > (i / causal) % causal) v = -INFINITY;
+    dst[i] = v;
   }
+}
+
+extern "C" int nlg_fill_normal(float *dev, uint64_t n, uint64_t seed, float sigma, uint32_t causal,
+                               void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!n) return NLG_OK;
+  const uint64_t g = n / 256 + 1 < 65536 ? n / 256 + 1 : 65536;
+  hipLaunchKernelGGL(k_gen_normal, dim3((uint32_t)g), dim3(256), 0, nlg_stream(stream), dev, n, seed, sigma,
+                     causal);
+  NLG_LAUNCHED("fill normal");
+  return NLG_OK;
 }
 
 __global__ void k_fill_f32(float *dst, uint64_t n, float v) {
@@ -218,7 +234,7 @@ static int gen_uniform(float *d, uint64_t n, uint64_t seed, double lo, double hi
   return NLG_OK;
 }
 static int gen_normal(float *d, uint64_t n, uint64_t seed) {
-  hipLaunchKernelGGL(k_gen_normal, dim3(gen_grid(n)), dim3(256), 0, nlg_stream(nullptr), d, n, seed);
+  hipLaunchKernelGGL(k_gen_normal, dim3(gen_grid(n)), dim3(256), 0, nlg_stream(nullptr), d, n, seed, 1.0f, 0u);
   NLG_LAUNCHED("generate normal");
   return NLG_OK;
 }

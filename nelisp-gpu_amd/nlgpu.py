@@ -103,6 +103,7 @@ def lib() -> C.CDLL:
         "nlg_decode_attn_f16_chunks": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, sz, vp]),
         "nlg_attn_ternary_linear_residual": (i32, [vp, sz, u32, u32, u32, u32, u32, vp, vp, vp, i32, vp,
                                                    vp, u32, vp]),
+        "nlg_fill_normal": (i32, [vp, C.c_uint64, C.c_uint64, C.c_float, u32, vp]),
         "nlg_stack_create": (i32, [C.POINTER(StackConfig), C.POINTER(vp)]),
         "nlg_stack_destroy": (None, [vp]),
         "nlg_stack_start": (i32, [vp, vp, u32]),
@@ -295,7 +296,7 @@ def ternary_linear_residual(x, w2, bias, beta, res, y, seq, out, cols, beta_per_
 
 def rms_ternary_swiglu(x, gain, eps, w2gu, beta, h, seq, dff, cols, beta_per_row=True,
                        stream=None) -> None:
-    _check(lib().nlg_rms_ternary_swiglu(x.ptr, gain.ptr, eps, w2gu.ptr, beta.ptr, int(beta_per_row),
+    _check(lib().nlg_rms_ternary_swiglu(x.ptr, _ptr(gain), eps, w2gu.ptr, beta.ptr, int(beta_per_row),
                                         h.ptr, seq, dff, cols, stream), "rms_ternary_swiglu")
 
 
@@ -342,6 +343,10 @@ def attn_ternary_linear_residual(workspace, batch, heads, kvheads, head_dim, max
 
 def decode_attn_f16_workspace(batch, heads, kvheads, head_dim, max_seq) -> int:
     return lib().nlg_decode_attn_f16_workspace(batch, heads, kvheads, head_dim, max_seq)
+
+
+def fill_normal(dev, n: int, seed: int, sigma: float = 1.0, causal: int = 0, stream=None) -> None:
+    _check(lib().nlg_fill_normal(dev.ptr, n, seed, sigma, causal, stream), "fill_normal")
 
 
 class Stack:
