@@ -43,6 +43,8 @@ OUT, COLS = 4096, 4096
 COPIES = 128
 STEP_BYTES = OUT * COLS // 4 + COLS * 4 + 4 + OUT * 4          # 4,227,076
 GEMV_BYTES = OUT * COLS // 4 + COLS + 4 + 4 + OUT * 4          # 4,214,792
+# HBM bytes per step measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+STEP_TRAFFIC = 4521484 + 16384
 METRIC = "ternary GEMV GB/s (% HBM peak) at 4096²; decode tok/s, 2B ternary model, batch 1"
 
 
@@ -356,6 +358,33 @@ def cpu_baseline(x, w_one, seconds: float):
                        f"restatement of the reference kernels, OpenMP over output rows) in {dt:.1f} s")
 
 
+def pmc_probe():
+    """Launches for rocprofv3 --pmc runs: 64 config-2 steps (eager, one
+    dispatch each, rotating weight copies) and 4 device-to-device copies of
+    64 MiB, whose FETCH_SIZE / WRITE_SIZE calibrate the counters' scale."""
+    import nlgpu
+    nlgpu.init()
+    seed = 20260921 + 1
+    w_one = nlgpu.pack_ternary(nlgpu.trits(seed, (OUT, COLS)))
+    wbytes = w_one.nbytes
+    dW = nlgpu.DeviceArray(wbytes * COPIES)
+    for c in range(COPIES):
+        dW.upload(np.roll(w_one, c, axis=0), offset=c * wbytes)
+    dx = nlgpu.to_device(nlgpu.normal(seed + 100, COLS))
+    dbeta = nlgpu.to_device(np.array([1.0], np.float32))
+    dy = nlgpu.DeviceArray(OUT * 4)
+    L = nlgpu.lib()
+    for i in range(64):
+        L.nlg_ternary_linear_cfg(dx.ptr, dW.ptr + (i % COPIES) * wbytes, None, dbeta.ptr, 0, dy.ptr, None, 1,
+                                 OUT, COLS, 0, None, 0, None)
+    nlgpu.sync()
+    a, b = nlgpu.DeviceArray(64 << 20), nlgpu.DeviceArray(64 << 20)
+    for _ in range(4):
+        L.nlg_copy_d2d(b.ptr, a.ptr, 64 << 20, None)
+    nlgpu.sync()
+    print("pmc probe: 64 steps of k_tern_fused (4096x4096), 4 copies of 64 MiB", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -364,7 +393,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decoder stack")
+    ap.add_argument("--pmc-probe", action="store_true", help="only the launches the PMC profiles count")
     args = ap.parse_args()
+    if args.pmc_probe:
+        pmc_probe()
+        return
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the decode path is not sharded); "
               "run with --gpus 1", file=sys.stderr)
@@ -404,7 +437,9 @@ def main():
                    "out": OUT, "cols": COLS, "batch": 1, "weight_copies": COPIES,
                    "step": "one launch: pack-act-rows quantisation fused into the ternary GEMV"},
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": STEP_TRAFFIC,
+                     "traffic_source": "profiles/ternary_gemv_4096_decode_pmc_traffic.md (FETCH_SIZE x 1.9993 "
+                                       "+ WRITE_SIZE, calibrated on a 64 MiB copy)",
                      "kernel": "k_tern_fused", "bytes_per_launch": STEP_BYTES,
                      "us_per_launch": round(r["step_ms"] * 1e3, 3)},
         "gemv_prequantised": {"gbs": round(gemv_gbs, 2), "us_per_launch": round(r["gemv_ms"] * 1e3, 3),
