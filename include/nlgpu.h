@@ -293,6 +293,13 @@ int nlg_stack_create(const nlg_stack_config *cfg, nlg_stack **out);
 void nlg_stack_destroy(nlg_stack *s);
 /* Begin `batch` sequences with prompts [batch x n_prompt] (host int32). */
 int nlg_stack_start(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt);
+/* Begin `batch` sequences and run every prompt token through the stack at
+ * once (batch x n_prompt rows through the batched linears, causal attention
+ * over the cache), then the LM head on each sequence's last prompt token:
+ * the state is then that of nlg_stack_start + n_prompt steps (position
+ * n_prompt, the first greedy token chosen), except that greedy choices are
+ * kept only for the last prompt position.  batch x n_prompt <= 65535. */
+int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt);
 /* Run `steps` token steps: the token at the current position goes through
  * every layer, its K/V are cached, and the next token is the prompt's while
  * the prompt lasts, else the greedy choice.  use_graph != 0 replays one

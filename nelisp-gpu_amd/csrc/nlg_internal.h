@@ -152,6 +152,12 @@ enum {
 // the decode attention splits max_seq positions into.
 #define NLG_ATTN_MAX_CHUNKS 4
 uint32_t nlg_attn_chunk_count(uint32_t head_dim, uint32_t max_seq);
+// The chunk pass over `rows` query rows: decode (qper 0: row = sequence, all
+// at position pos[0]) or prefill (row r = sequence r / qper at position
+// pos[0] + r % qper, causal over the cache).  Workspace sized for `rows`.
+int nlg_attn_chunks(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *pos, uint32_t rows,
+                    uint32_t qper, uint32_t heads, uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
+                    void *workspace, size_t workspace_bytes, hipStream_t st);
 enum {
   NLG_EPI_STORE = 0,   // y = bias + (beta*gamma)*acc
   NLG_EPI_RESID = 1,   // y = res + that
@@ -175,6 +181,9 @@ struct FusedArgs {
   float *gamma_out;      // [seq] or null
   // EPI_QKV: q -> y; k, v -> caches [seq][kvheads][max_seq][hd] (fp16 bits)
   uint32_t nq, nkv, hd, kvheads, max_seq;
+  // 0: row s is sequence s at position pos[0] (decode); else rows are
+  // qper consecutive positions pos[0].. of each sequence (prefill)
+  uint32_t qper;
   const float *co, *si;  // RoPE tables [max_seq x hd/2]
   const int32_t *pos;    // device position (one for every row of the batch)
   uint16_t *kc, *vc;

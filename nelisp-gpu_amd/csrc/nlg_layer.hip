@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   uint32_t dd = 0, p = 0;
   bool pos_ok = false;
   if (EPI == NLG_EPI_QKV) {
-    const int32_t pr = a.pos[0];
+    const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(tok % a.qper) : 0);
     pos_ok = pr >= 0 && (uint32_t)pr < a.max_seq;
     p = pos_ok ? (uint32_t)pr : 0u;
     const uint32_t sec = orow < a.nq ? orow : (orow < a.nq + a.nkv ? orow - a.nq : orow - a.nq - a.nkv);
@@ -268,7 +268,8 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
         const bool isk = orow < a.nq + a.nkv;
         const uint32_t sec = isk ? orow - a.nq : orow - a.nq - a.nkv;
         const uint32_t kh = sec / a.hd;
-        const size_t at = (((size_t)tok * a.kvheads + kh) * a.max_seq + p) * a.hd + dd;
+        const uint32_t sq = a.qper ? tok / a.qper : tok;
+        const size_t at = (((size_t)sq * a.kvheads + kh) * a.max_seq + p) * a.hd + dd;
         if (isk) a.kc[at] = f32_to_f16_bits(rot);
         else a.vc[at] = f32_to_f16_bits(val);
       }
@@ -506,6 +507,7 @@ struct AttnArgs {
   float *pctx;              // [B][nchunk][heads*hd]: sum of e*V over the chunk
   float *pmz;               // [B][nchunk][heads][2]: chunk max, sum of e
   uint32_t heads, kvheads, max_seq, nchunk;
+  uint32_t qper;            // 0: row z = sequence z at pos[0]; else sequence z/qper at pos[0] + z%qper
   float coef;               // 1/sqrt(hd)
 };
 
@@ -548,8 +550,9 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   asm volatile("" ::"s"(a.q), "s"(a.kc), "s"(a.vc), "s"(a.pos), "s"(a.pctx), "s"(a.pmz), "s"(a.heads),
                "s"(a.kvheads), "s"(a.max_seq), "s"(a.nchunk), "s"(a.coef));
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const uint32_t c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const size_t cb = (size_t)b * a.nchunk + c;
+  const uint32_t c = blockIdx.x, kvh = blockIdx.y, qr = blockIdx.z;  // qr: query row
+  const uint32_t b = a.qper ? qr / a.qper : qr;                         // its sequence
+  const size_t cb = (size_t)qr * a.nchunk + c;
   float *pctx = a.pctx + cb * a.heads * HD + (size_t)kvh * G * HD;
   float *pmz = a.pmz + (cb * a.heads + (size_t)kvh * G) * 2;
   const uint32_t p0 = c * CS;
@@ -569,7 +572,7 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
     kr[i] = *(const uint4 *)(kb + (size_t)pc * HD);
     vr[i] = *(const uint4 *)(vb + (size_t)pc * HD);
   }
-  const float *qb = a.q + (size_t)b * a.heads * HD + (size_t)kvh * G * HD + d0;
+  const float *qb = a.q + (size_t)qr * a.heads * HD + (size_t)kvh * G * HD + d0;
   float q[G][8];
 #pragma unroll
   for (int h = 0; h < G; h++) {
@@ -577,7 +580,7 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
     q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
     q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
   }
-  const int32_t pr = a.pos[0];
+  const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(qr % a.qper) : 0);
   const uint32_t len = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
   if (p0 >= len) {  // block-uniform: a chunk past the position adds nothing
     for (int i = threadIdx.x; i < G * HD; i += NW * 64) pctx[i] = 0.0f;
@@ -733,20 +736,17 @@ static int attn_setup(AttnArgs &a, uint32_t batch, uint32_t heads, uint32_t kvhe
   return NLG_OK;
 }
 
-extern "C" int nlg_decode_attn_f16_chunks(const float *q, const uint16_t *kcache, const uint16_t *vcache,
-                                          const int32_t *pos, uint32_t batch, uint32_t heads,
-                                          uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
-                                          void *workspace, size_t workspace_bytes, void *stream) {
-  if (nlg_ensure_init()) return NLG_ERR;
-  if (!batch) return NLG_OK;
+int nlg_attn_chunks(const float *q, const uint16_t *kcache, const uint16_t *vcache, const int32_t *pos,
+                    uint32_t rows, uint32_t qper, uint32_t heads, uint32_t kvheads, uint32_t head_dim,
+                    uint32_t max_seq, void *workspace, size_t workspace_bytes, hipStream_t st) {
+  if (!rows) return NLG_OK;
   AttnArgs a;
-  if (attn_setup(a, batch, heads, kvheads, head_dim, max_seq, workspace, workspace_bytes)) return NLG_ERR;
+  if (attn_setup(a, rows, heads, kvheads, head_dim, max_seq, workspace, workspace_bytes)) return NLG_ERR;
   if (((uintptr_t)q & 15) || ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15))
     return nlg_fail("decode attn: q and caches must be 16-byte aligned");
-  a.q = q; a.kc = kcache; a.vc = vcache; a.pos = pos;
+  a.q = q; a.kc = kcache; a.vc = vcache; a.pos = pos; a.qper = qper;
   const uint32_t G = heads / kvheads, ni = attn_ni(head_dim, max_seq);
-  const dim3 grid(a.nchunk, kvheads, batch), blk(ATTN_WAVES * 64);
-  hipStream_t st = nlg_stream(stream);
+  const dim3 grid(a.nchunk, kvheads, rows), blk(ATTN_WAVES * 64);
 #define AT(HD, GG)                                                                     \
   do {                                                                                 \
     if (ni == 8) hipLaunchKernelGGL((k_attn_part<HD, GG, 8>), grid, blk, 0, st, a);   \
@@ -760,6 +760,15 @@ extern "C" int nlg_decode_attn_f16_chunks(const float *q, const uint16_t *kcache
 #undef AT
   NLG_LAUNCHED("decode attention (fp16 KV)");
   return NLG_OK;
+}
+
+extern "C" int nlg_decode_attn_f16_chunks(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                                          const int32_t *pos, uint32_t batch, uint32_t heads,
+                                          uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
+                                          void *workspace, size_t workspace_bytes, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  return nlg_attn_chunks(q, kcache, vcache, pos, batch, 0, heads, kvheads, head_dim, max_seq, workspace,
+                         workspace_bytes, nlg_stream(stream));
 }
 
 extern "C" int nlg_attn_ternary_linear_residual(const void *workspace, size_t workspace_bytes, uint32_t batch,

@@ -198,6 +198,11 @@ struct nlg_stack {
   size_t attn_ws_bytes;
   bool attn_fused;  // merge folded into the output projection
   std::vector<void *> allocs;
+  // prefill rows (batch x prompt tokens), allocated at the first prefill
+  float *px, *pq, *ph;
+  void *pattn_ws;
+  size_t pattn_ws_bytes;
+  uint32_t pcap;
   void *graph;
   uint32_t host_pos;
   bool started;
@@ -243,6 +248,8 @@ extern "C" void nlg_stack_destroy(nlg_stack *s) {
   if (!s) return;
   if (s->graph) nlg_graph_destroy(s->graph);
   for (void *p : s->allocs) nlg_free(p);
+  for (void *p : {(void *)s->px, (void *)s->pq, (void *)s->ph, s->pattn_ws})
+    if (p) nlg_free(p);
   delete s;
 }
 
@@ -390,6 +397,9 @@ static int stack_attention(nlg_stack *s, Layer &y) {
          nlg_ternary_linear_residual(s->att, y.wo, nullptr, y.bo, 0, s->x, s->x, B, d, s->nq, nullptr);
 }
 
+static int stack_head(nlg_stack *s);
+static int upload_prompt(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt, bool all_hist);
+
 // One token step for the whole batch, enqueued on the library stream.
 static int stack_enqueue(nlg_stack *s) {
   const nlg_stack_config &c = s->c;
@@ -404,6 +414,13 @@ static int stack_enqueue(nlg_stack *s) {
         nlg_ternary_linear_residual(s->h, y.wd, nullptr, y.bd, 0, s->x, s->x, B, d, f, nullptr))
       return NLG_ERR;
   }
+  return stack_head(s);
+}
+
+// Final norm, LM head with the greedy partials, then the next token.
+static int stack_head(nlg_stack *s) {
+  const nlg_stack_config &c = s->c;
+  const uint32_t d = c.d_model, B = c.batch;
   FusedArgs a{};
   a.x = s->x; a.gain = s->gfinal; a.eps = c.rms_eps; a.w2 = s->wlm; a.beta = s->blm;
   a.seq = B; a.out = c.vocab; a.cols = d; a.y = s->logits; a.ystride = c.vocab;
@@ -422,25 +439,108 @@ static int stack_enqueue(nlg_stack *s) {
 extern "C" int nlg_stack_start(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt) {
   if (!s || !prompts) return nlg_fail("stack start: null argument");
   const nlg_stack_config &c = s->c;
-  if (!n_prompt || n_prompt > c.max_seq) return nlg_fail("stack start: prompt length must be 1..max_seq");
-  std::vector<int32_t> pr((size_t)c.batch * c.max_seq, 0), hist((size_t)c.batch * c.max_seq, -1);
-  for (uint32_t b = 0; b < c.batch; b++)
-    for (uint32_t i = 0; i < n_prompt; i++) {
-      const int32_t t = prompts[(size_t)b * n_prompt + i];
-      if (t < 0 || (uint32_t)t >= c.vocab) return nlg_fail("stack start: token %d out of range", t);
-      pr[(size_t)b * c.max_seq + i] = t;
-    }
-  for (uint32_t b = 0; b < c.batch; b++) hist[(size_t)b * c.max_seq] = pr[(size_t)b * c.max_seq];
-  const int32_t zero = 0, plen = (int32_t)n_prompt;
-  if (nlg_upload(s->prompt, pr.data(), pr.size() * 4) || nlg_upload(s->hist, hist.data(), hist.size() * 4) ||
-      nlg_upload(s->greedy, std::vector<int32_t>(hist.size(), -1).data(), hist.size() * 4) ||
-      nlg_upload(s->pos, &zero, 4) || nlg_upload(s->plen, &plen, 4))
-    return NLG_ERR;
+  if (upload_prompt(s, prompts, n_prompt, false)) return NLG_ERR;
   hipLaunchKernelGGL(k_embed_rows, dim3(nlg_blocks(c.d_model, 256), c.batch), dim3(256), 0,
                      nlg_stream(nullptr), s->emb, s->prompt, c.max_seq, s->x, c.d_model);
   NLG_LAUNCHED("embed");
   NLG_HIP(hipStreamSynchronize(nlg_stream(nullptr)));
   s->host_pos = 0;
+  s->started = true;
+  return NLG_OK;
+}
+
+// Prefill rows: row z = sequence z / P, prompt position z % P.
+__global__ void k_embed_prompt(const float *emb, const int32_t *prompt, uint32_t max_seq, uint32_t P,
+                               float *x, uint32_t dim) {
+  const uint32_t z = blockIdx.y, b = z / P, t = z % P;
+  const int32_t tok = prompt[(size_t)b * max_seq + t];
+  for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < dim; j += gridDim.x * blockDim.x)
+    x[(size_t)z * dim + j] = emb[(size_t)tok * dim + j];
+}
+__global__ void k_last_rows(const float *px, uint32_t P, float *x, uint32_t dim) {
+  const uint32_t b = blockIdx.y;
+  for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < dim; j += gridDim.x * blockDim.x)
+    x[(size_t)b * dim + j] = px[((size_t)b * P + P - 1) * dim + j];
+}
+
+static int upload_prompt(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt, bool all_hist) {
+  const nlg_stack_config &c = s->c;
+  if (!n_prompt || n_prompt > c.max_seq) return nlg_fail("stack: prompt length must be 1..max_seq");
+  std::vector<int32_t> pr((size_t)c.batch * c.max_seq, 0), hist((size_t)c.batch * c.max_seq, -1);
+  for (uint32_t b = 0; b < c.batch; b++)
+    for (uint32_t i = 0; i < n_prompt; i++) {
+      const int32_t t = prompts[(size_t)b * n_prompt + i];
+      if (t < 0 || (uint32_t)t >= c.vocab) return nlg_fail("stack: token %d out of range", t);
+      pr[(size_t)b * c.max_seq + i] = t;
+      if (all_hist || i == 0) hist[(size_t)b * c.max_seq + i] = t;
+    }
+  const int32_t zero = 0, plen = (int32_t)n_prompt;
+  if (nlg_upload(s->prompt, pr.data(), pr.size() * 4) || nlg_upload(s->hist, hist.data(), hist.size() * 4) ||
+      nlg_upload(s->greedy, std::vector<int32_t>(hist.size(), -1).data(), hist.size() * 4) ||
+      nlg_upload(s->pos, &zero, 4) || nlg_upload(s->plen, &plen, 4))
+    return NLG_ERR;
+  return NLG_OK;
+}
+
+extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt) {
+  if (!s || !prompts) return nlg_fail("stack prefill: null argument");
+  const nlg_stack_config &c = s->c;
+  const uint32_t d = c.d_model, f = c.d_ff, B = c.batch, P = n_prompt;
+  if (upload_prompt(s, prompts, n_prompt, true)) return NLG_ERR;
+  const uint64_t T64 = (uint64_t)B * P;
+  if (T64 > 65535) return nlg_fail("stack prefill: batch x prompt = %llu rows > 65535", (unsigned long long)T64);
+  const uint32_t T = (uint32_t)T64;
+  hipStream_t st = nlg_stream(nullptr);
+  if (T > s->pcap) {  // grow the prefill rows (eager, outside any capture)
+    NLG_HIP(hipStreamSynchronize(st));
+    for (void *p : {(void *)s->px, (void *)s->pq, (void *)s->ph, s->pattn_ws})
+      if (p) nlg_free(p);
+    s->px = (float *)nlg_malloc((size_t)T * d * 4);
+    s->pq = (float *)nlg_malloc((size_t)T * s->nq * 4);
+    s->ph = (float *)nlg_malloc((size_t)T * f * 4);
+    s->pattn_ws_bytes = nlg_decode_attn_f16_workspace(T, c.heads, c.kv_heads, c.head_dim, c.max_seq);
+    s->pattn_ws = nlg_malloc(s->pattn_ws_bytes);
+    if (!s->px || !s->pq || !s->ph || !s->pattn_ws) return NLG_ERR;
+    s->pcap = T;
+  }
+  hipLaunchKernelGGL(k_embed_prompt, dim3(nlg_blocks(d, 256), T), dim3(256), 0, st, s->emb, s->prompt,
+                     c.max_seq, P, s->px, d);
+  NLG_LAUNCHED("embed prompt");
+  const uint32_t nchunk = nlg_attn_chunk_count(c.head_dim, c.max_seq);
+  const size_t pctx_bytes = ((size_t)T * nchunk * s->nq * 4 + 255) / 256 * 256;
+  for (uint32_t l = 0; l < c.layers; l++) {
+    Layer &y = s->L[l];
+    FusedArgs q{};
+    q.x = s->px; q.gain = y.gattn; q.eps = c.rms_eps; q.w2 = y.wqkv; q.beta = y.bqkv; q.beta_per_row = 1;
+    q.seq = T; q.nq = s->nq; q.nkv = s->nkv; q.out = s->nq + 2 * s->nkv; q.cols = d; q.y = s->pq;
+    q.ystride = s->nq; q.hd = c.head_dim; q.kvheads = c.kv_heads; q.max_seq = c.max_seq; q.co = s->co;
+    q.si = s->si; q.pos = s->pos; q.kc = y.kc; q.vc = y.vc; q.qper = P;
+    if (nlg_fused_launch(q, NLG_PRO_RMS, NLG_EPI_QKV, 0, st)) return NLG_ERR;
+    if (nlg_attn_chunks(s->pq, y.kc, y.vc, s->pos, T, P, c.heads, c.kv_heads, c.head_dim, c.max_seq,
+                        s->pattn_ws, s->pattn_ws_bytes, st))
+      return NLG_ERR;
+    FusedArgs o{};
+    o.x = (const float *)s->pattn_ws; o.attn_mz = (const float *)((char *)s->pattn_ws + pctx_bytes);
+    o.attn_nc = nchunk; o.hd = c.head_dim; o.w2 = y.wo; o.beta = y.bo; o.seq = T; o.out = d; o.cols = s->nq;
+    o.y = s->px; o.ystride = d; o.res = s->px; o.rstride = d;
+    if (nchunk > NLG_ATTN_MAX_CHUNKS) return nlg_fail("stack prefill: max_seq too long for the folded merge");
+    if (nlg_fused_launch(o, NLG_PRO_ATTN, NLG_EPI_RESID, 0, st)) return NLG_ERR;
+    FusedArgs g{};
+    g.x = s->px; g.gain = y.gffn; g.eps = c.rms_eps; g.w2 = y.wgu; g.beta = y.bgu; g.beta_per_row = 1;
+    g.seq = T; g.out = 2 * f; g.cols = d; g.y = s->ph; g.ystride = f;
+    if (nlg_fused_launch(g, NLG_PRO_RMS, NLG_EPI_SWIGLU, 0, st)) return NLG_ERR;
+    FusedArgs w{};
+    w.x = s->ph; w.w2 = y.wd; w.beta = y.bd; w.seq = T; w.out = d; w.cols = f; w.y = s->px; w.ystride = d;
+    w.res = s->px; w.rstride = d;
+    if (nlg_fused_launch(w, NLG_PRO_NONE, NLG_EPI_RESID, 0, st)) return NLG_ERR;
+  }
+  hipLaunchKernelGGL(k_last_rows, dim3(nlg_blocks(d, 256), B), dim3(256), 0, st, s->px, P, s->x, d);
+  NLG_LAUNCHED("last prompt rows");
+  const int32_t last = (int32_t)P - 1;
+  NLG_HIP(hipMemcpyAsync(s->pos, &last, 4, hipMemcpyHostToDevice, st));
+  if (stack_head(s)) return NLG_ERR;
+  NLG_HIP(hipStreamSynchronize(st));
+  s->host_pos = P;
   s->started = true;
   return NLG_OK;
 }

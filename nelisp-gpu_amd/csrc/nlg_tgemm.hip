@@ -182,7 +182,7 @@ struct GemmArgs {
   const float *co, *si;
   const int32_t *pos;
   uint16_t *kc, *vc;
-  int prefill;         // QKV: tokens are positions pos[0]+s of sequence 0 (else sequence s at pos[0])
+  uint32_t qper;       // QKV: 0 = token s is sequence s at pos[0]; else sequence s/qper at pos[0] + s%qper
   // EPI_ARGMAX: per (token, workgroup) max and first index
   float *pval;
   int32_t *pidx;
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
             a.y[(size_t)tk * a.ystride + (row >> 1)] = (val * sg) * pv;
           }
         } else if (live) {
-          const int32_t pr = a.pos[0] + (a.prefill ? (int32_t)tk : 0);
+          const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(tk % a.qper) : 0);
           const bool pos_ok = pr >= 0 && (uint32_t)pr < a.max_seq;
           const uint32_t p = pos_ok ? (uint32_t)pr : 0u;
           const uint32_t sec = row < a.nq ? row : (row < a.nq + a.nkv ? row - a.nq : row - a.nq - a.nkv);
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
             a.y[(size_t)tk * a.ystride + row] = rot;
           } else if (pos_ok) {
             const bool isk = row < a.nq + a.nkv;
-            const uint32_t kh = sec / a.hd, sq = a.prefill ? 0u : tk;
+            const uint32_t kh = sec / a.hd, sq = a.qper ? tk / a.qper : tk;
             const size_t at = (((size_t)sq * a.kvheads + kh) * a.max_seq + p) * a.hd + dd;
             if (isk) a.kc[at] = __builtin_bit_cast(uint16_t, (_Float16)rot);
             else a.vc[at] = __builtin_bit_cast(uint16_t, (_Float16)val);
@@ -457,7 +457,7 @@ int nlg_batched_launch(const FusedArgs &f, int pro, int epi, hipStream_t st) {
   g.xq = xq; g.gamma = gamma; g.w2 = f.w2; g.bias = f.bias; g.beta = f.beta; g.beta_per_row = f.beta_per_row;
   g.seq = f.seq; g.out = f.out; g.cols = f.cols; g.y = f.y; g.ystride = f.ystride; g.res = f.res;
   g.rstride = f.rstride; g.nq = f.nq; g.nkv = f.nkv; g.hd = f.hd; g.kvheads = f.kvheads; g.max_seq = f.max_seq;
-  g.co = f.co; g.si = f.si; g.pos = f.pos; g.kc = f.kc; g.vc = f.vc; g.prefill = 0;
+  g.co = f.co; g.si = f.si; g.pos = f.pos; g.kc = f.kc; g.vc = f.vc; g.qper = f.qper;
   g.pval = f.pval; g.pidx = f.pidx;
   return nlg_tgemm_launch(g, epi, st);
 }

@@ -107,6 +107,7 @@ def lib() -> C.CDLL:
         "nlg_stack_create": (i32, [C.POINTER(StackConfig), C.POINTER(vp)]),
         "nlg_stack_destroy": (None, [vp]),
         "nlg_stack_start": (i32, [vp, vp, u32]),
+        "nlg_stack_prefill": (i32, [vp, vp, u32]),
         "nlg_stack_step": (i32, [vp, u32, i32]),
         "nlg_stack_position": (i32, [vp, C.POINTER(u32)]),
         "nlg_stack_tokens": (i32, [vp, vp, vp]),
@@ -364,6 +365,11 @@ class Stack:
         p = np.ascontiguousarray(prompts, np.int32)
         assert p.ndim == 2 and p.shape[0] == self.cfg.batch
         _check(lib().nlg_stack_start(self.h, p.ctypes.data, p.shape[1]), "stack_start")
+
+    def prefill(self, prompts: np.ndarray) -> None:
+        p = np.ascontiguousarray(prompts, np.int32)
+        assert p.ndim == 2 and p.shape[0] == self.cfg.batch
+        _check(lib().nlg_stack_prefill(self.h, p.ctypes.data, p.shape[1]), "stack_prefill")
 
     def step(self, steps: int = 1, graph: bool = True) -> None:
         _check(lib().nlg_stack_step(self.h, steps, int(graph)), "stack_step")
