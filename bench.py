@@ -261,7 +261,9 @@ def decode_bench(batch: int, stream):
             "prefill_tok_s": round(batch * PROMPT / (prefill_ms * 1e-3), 1),
             "step_bytes": int(step_bytes), "step_gbs": round(step_bytes / (ms_tok * 1e-3) / 1e9, 1),
             "step_frac": round(step_bytes / (ms_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "launches_per_step": L * 5 + 2, "lm_head_bytes": int(lm_bytes), "per_kernel": per}
+            # per layer: 5 launches, or 9 when the linears take the batched (quantise + GEMM) form
+            "launches_per_step": L * (9 if batch >= 8 else 5) + (3 if batch >= 8 else 2),
+            "lm_head_bytes": int(lm_bytes), "per_kernel": per}
 
 
 # ---------------------------------------------------------------- config 3
