@@ -508,6 +508,7 @@ struct AttnArgs {
   float *pmz;               // [B][nchunk][heads][2]: chunk max, sum of e
   uint32_t heads, kvheads, max_seq, nchunk;
   uint32_t qper;            // 0: row z = sequence z at pos[0]; else sequence z/qper at pos[0] + z%qper
+  uint32_t grp;             // query heads per kv head (a workgroup takes G <= grp of them)
   float coef;               // 1/sqrt(hd)
 };
 
@@ -550,11 +551,12 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   asm volatile("" ::"s"(a.q), "s"(a.kc), "s"(a.vc), "s"(a.pos), "s"(a.pctx), "s"(a.pmz), "s"(a.heads),
                "s"(a.kvheads), "s"(a.max_seq), "s"(a.nchunk), "s"(a.coef));
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const uint32_t c = blockIdx.x, kvh = blockIdx.y, qr = blockIdx.z;  // qr: query row
+  // workgroup: chunk c, query heads h0 .. h0+G-1 (all of one kv head), query row qr
+  const uint32_t c = blockIdx.x, h0 = blockIdx.y * G, qr = blockIdx.z, kvh = h0 / a.grp;
   const uint32_t b = a.qper ? qr / a.qper : qr;                         // its sequence
   const size_t cb = (size_t)qr * a.nchunk + c;
-  float *pctx = a.pctx + cb * a.heads * HD + (size_t)kvh * G * HD;
-  float *pmz = a.pmz + (cb * a.heads + (size_t)kvh * G) * 2;
+  float *pctx = a.pctx + cb * a.heads * HD + (size_t)h0 * HD;
+  float *pmz = a.pmz + (cb * a.heads + h0) * 2;
   const uint32_t p0 = c * CS;
   // K, V and q are fetched before the position arrives (addresses clamped
   // to the cache, not to the position), so the position's fetch is not a
@@ -572,7 +574,7 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
     kr[i] = *(const uint4 *)(kb + (size_t)pc * HD);
     vr[i] = *(const uint4 *)(vb + (size_t)pc * HD);
   }
-  const float *qb = a.q + (size_t)qr * a.heads * HD + (size_t)kvh * G * HD + d0;
+  const float *qb = a.q + (size_t)qr * a.heads * HD + (size_t)h0 * HD + d0;
   float q[G][8];
 #pragma unroll
   for (int h = 0; h < G; h++) {
@@ -744,9 +746,13 @@ int nlg_attn_chunks(const float *q, const uint16_t *kcache, const uint16_t *vcac
   if (attn_setup(a, rows, heads, kvheads, head_dim, max_seq, workspace, workspace_bytes)) return NLG_ERR;
   if (((uintptr_t)q & 15) || ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15))
     return nlg_fail("decode attn: q and caches must be 16-byte aligned");
-  a.q = q; a.kc = kcache; a.vc = vcache; a.pos = pos; a.qper = qper;
-  const uint32_t G = heads / kvheads, ni = attn_ni(head_dim, max_seq);
-  const dim3 grid(a.nchunk, kvheads, rows), blk(ATTN_WAVES * 64);
+  a.q = q; a.kc = kcache; a.vc = vcache; a.pos = pos; a.qper = qper; a.grp = heads / kvheads;
+  // A workgroup scores every query head of its kv head (K and V read once)
+  // unless there are too few workgroups to spread over the CUs: then one
+  // head each (K and V come from L2 for the others).
+  const uint32_t ni = attn_ni(head_dim, max_seq);
+  const uint32_t G = (uint64_t)rows * kvheads * a.nchunk >= 128 ? a.grp : 1;
+  const dim3 grid(a.nchunk, heads / G, rows), blk(ATTN_WAVES * 64);
 #define AT(HD, GG)                                                                     \
   do {                                                                                 \
     if (ni == 8) hipLaunchKernelGGL((k_attn_part<HD, GG, 8>), grid, blk, 0, st, a);   \
