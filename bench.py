@@ -18,7 +18,8 @@ the same GEMV kernel over all 128 copies stacked into one [524288 x 4096]
 launch (launch cost amortised: the kernel's streaming rate), and the
 measured launch floor (an empty kernel, back to back).
 cpu_baseline: the CPU restatement (oracle/) of the same step on host cores.
-softmax_config3 / swiglu_ffn_config4: configs 3 and 4 at their full sizes.
+matmul_config1 / softmax_config3 / swiglu_ffn_config4: configs 1, 3 and 4 at
+their full sizes.
 decode: config 5, the 30-layer ternary decoder stack at batch 1 and 32 --
 tokens/s over 256 greedy steps after a 512-token prompt, the step's
 algorithmic bytes (every weight, the LM head, K/V of the cached positions)
@@ -266,6 +267,36 @@ def decode_bench(batch: int, stream):
             "lm_head_bytes": int(lm_bytes), "per_kernel": per}
 
 
+# ---------------------------------------------------------------- config 1
+
+def matmul_bench(stream):
+    """Config 1: f32 C[256x256] = A[256x256] B[256x256], A, B ~ U[-1,1] from
+    a seed, through the by-name kernels (the vkmatmul path), each variant
+    graph-timed; checked against a float64 product."""
+    import nlgpu
+    M = K = N = 256
+    a = (nlgpu.uniform(20260921 + 10, M * K) * 2 - 1).astype(np.float32)
+    b = (nlgpu.uniform(20260921 + 11, K * N) * 2 - 1).astype(np.float32)
+    da, db, dc = nlgpu.to_device(a), nlgpu.to_device(b), nlgpu.DeviceArray(M * N * 4)
+    want = a.reshape(M, K).astype(np.float64) @ b.reshape(K, N).astype(np.float64)
+    flops = 2 * M * K * N
+    out = {}
+    for name, groups in (("matmul", (M * N + 63) // 64), ("matmul-tiled", (M // 16) * (N // 16)),
+                         ("matmul-reg", ((M // 4) * (N // 4) + 63) // 64)):
+        fn = lambda i: nlgpu.dispatch(name, [da, db, dc], [M, K, N], groups, stream=stream)
+        fn(0)
+        nlgpu.sync()
+        err = float(np.abs(dc.download(np.float32, M * N).reshape(M, N) - want).max() / np.abs(want).max())
+        us = _per_launch_us(fn, 128, stream)
+        out[name] = {"us": round(us, 3), "gflops": round(flops / us / 1e3, 1), "max_rel_err": err}
+    best = min(out, key=lambda k: out[k]["us"])
+    out["flops"] = flops
+    out["best"] = best
+    out["frac_fp32_peak"] = round(out[best]["gflops"] / 157300.0, 5)
+    out["note"] = "33.5 MFLOP: launch/latency-bound (0.2 us of fp32 peak)"
+    return out
+
+
 # ---------------------------------------------------------------- config 3
 
 SM_HEADS, SM_N = 32, 4096
@@ -419,6 +450,7 @@ def main():
     if not args.no_decode:
         import nlgpu
         stream = nlgpu.lib().nlg_default_stream()
+        extra["matmul_config1"] = matmul_bench(stream)
         extra["softmax_config3"] = softmax_bench(stream)
         extra["swiglu_ffn_config4"] = ffn_bench(stream)
     value = STEP_BYTES / (r["step_ms"] * 1e-3) / 1e9

@@ -102,36 +102,38 @@ def test_logits_follow_the_reference_kernels():
     s.close()
 
 
-def test_prefill_matches_teacher_forced_steps():
-    """All prompt rows at once (batched linears, causal attention over the
-    cache) against the same prompt fed one token per step: same state, and
-    logits / caches within the lane-flip bar (the two paths round RMSNorm's
-    sum in different orders)."""
-    print("[gpu] stack prefill vs teacher-forced steps", flush=True)
-    P = prompts(TINY["batch"], 12, TINY["vocab"], seed=11)
+@pytest.mark.parametrize("n", [12, 64])
+def test_prefill_matches_teacher_forced_steps(n):
+    """All prompt rows at once (batched linears -- the 128 x 128 matrix-core
+    tiles from 128 rows on -- and causal attention over the cache) against
+    the same prompt fed one token per step: same state, and logits / caches
+    within the lane-flip bar (the two paths round RMSNorm's sum in different
+    orders)."""
+    print(f"[gpu] stack prefill vs teacher-forced steps, prompt {n}", flush=True)
+    P = prompts(TINY["batch"], n, TINY["vocab"], seed=11)
     a, b = nlgpu.Stack(**TINY), nlgpu.Stack(**TINY)
     a.start(P)
-    a.step(12, graph=False)
+    a.step(n, graph=False)
     b.prefill(P)
-    assert a.position() == b.position() == 12
+    assert a.position() == b.position() == n
     la, lb = a.logits(), b.logits()
     err = np.abs(la - lb).max() / np.abs(la).max()
     print(f"  logits max|d|/max = {err:.2e}", flush=True)
     assert err <= 5e-2
     ta, ga = a.tokens()
     tb, gb = b.tokens()
-    assert np.array_equal(tb[:, :12], P) and np.array_equal(ta[:, :12], P)
-    assert np.array_equal(gb[:, 11], np.argmax(lb, axis=1)) and np.array_equal(tb[:, 12], gb[:, 11])
-    assert np.all(gb[:, :11] == -1)
+    assert np.array_equal(tb[:, :n], P) and np.array_equal(ta[:, :n], P)
+    assert np.array_equal(gb[:, n - 1], np.argmax(lb, axis=1)) and np.array_equal(tb[:, n], gb[:, n - 1])
+    assert np.all(gb[:, :n - 1] == -1)
     c = a.cfg
     for l in range(c.layers):
         for name in ("kc", "vc"):
-            ka = a.tensor(name, l, np.float16).reshape(c.batch, c.kv_heads, c.max_seq, c.head_dim)[:, :, :12]
-            kb = b.tensor(name, l, np.float16).reshape(c.batch, c.kv_heads, c.max_seq, c.head_dim)[:, :, :12]
+            ka = a.tensor(name, l, np.float16).reshape(c.batch, c.kv_heads, c.max_seq, c.head_dim)[:, :, :n]
+            kb = b.tensor(name, l, np.float16).reshape(c.batch, c.kv_heads, c.max_seq, c.head_dim)[:, :, :n]
             d = np.abs(ka.astype(np.float32) - kb.astype(np.float32)).max()
             assert d <= 5e-2 * np.abs(ka.astype(np.float32)).max(), (l, name, d)
     b.step(5)  # decoding continues from the prefilled state
     tb2, _ = b.tokens()
-    assert np.array_equal(tb2[:, :13], tb[:, :13]) and np.all(tb2[:, 13:18] >= 0)
+    assert np.array_equal(tb2[:, :n + 1], tb[:, :n + 1]) and np.all(tb2[:, n + 1:n + 6] >= 0)
     a.close()
     b.close()
