@@ -189,6 +189,46 @@ struct GemmArgs {
   uint32_t nparts;
 };
 
+// One output element of the batched linear (every lane calls it: the SwiGLU
+// and RoPE pairs are exchanged across lanes l, l^1, which hold rows 2j, 2j+1).
+template <int EPI>
+__device__ __forceinline__ void tg_store(const GemmArgs &a, int lane, uint32_t row, uint32_t tk, bool live,
+                                         float val) {
+  if (EPI == NLG_EPI_STORE || EPI == NLG_EPI_ARGMAX) {
+    if (live) a.y[(size_t)tk * a.ystride + row] = val;
+  } else if (EPI == NLG_EPI_RESID) {
+    if (live) a.y[(size_t)tk * a.ystride + row] = __fadd_rn(a.res[(size_t)tk * a.rstride + row], val);
+  } else if (EPI == NLG_EPI_SWIGLU || EPI == NLG_EPI_QKV) {
+    const float pv = __int_as_float(nlg_dpp<0xB1>(__float_as_int(val)));  // row ^ 1
+    if (EPI == NLG_EPI_SWIGLU) {
+      if (live && !(lane & 1)) {
+        const float sg = 1.0f / (1.0f + expf(0.0f - val));
+        a.y[(size_t)tk * a.ystride + (row >> 1)] = (val * sg) * pv;
+      }
+    } else if (live) {
+      const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(tk % a.qper) : 0);
+      const bool pos_ok = pr >= 0 && (uint32_t)pr < a.max_seq;
+      const uint32_t p = pos_ok ? (uint32_t)pr : 0u;
+      const uint32_t sec = row < a.nq ? row : (row < a.nq + a.nkv ? row - a.nq : row - a.nq - a.nkv);
+      const uint32_t dd = sec % a.hd, half = a.hd >> 1, ci = p * half + (dd >> 1);
+      const float cs = a.co[ci], sn = a.si[ci];
+      const bool odd = lane & 1;
+      const float a0 = odd ? pv : val, a1 = odd ? val : pv;
+      const float rot = odd ? __fadd_rn(__fmul_rn(a0, sn), __fmul_rn(a1, cs))
+                            : __fsub_rn(__fmul_rn(a0, cs), __fmul_rn(a1, sn));
+      if (row < a.nq) {
+        a.y[(size_t)tk * a.ystride + row] = rot;
+      } else if (pos_ok) {
+        const bool isk = row < a.nq + a.nkv;
+        const uint32_t kh = sec / a.hd, sq = a.qper ? tk / a.qper : tk;
+        const size_t at = (((size_t)sq * a.kvheads + kh) * a.max_seq + p) * a.hd + dd;
+        if (isk) a.kc[at] = __builtin_bit_cast(uint16_t, (_Float16)rot);
+        else a.vc[at] = __builtin_bit_cast(uint16_t, (_Float16)val);
+      }
+    }
+  }
+}
+
 #define TG_KC 256                 // columns per chunk (16 2-bit words of a row)
 #define TG_PH 8                   // chunks per phase
 #define TG_PITCH (TG_PH * TG_KC + 16)  // LDS row pitch in bytes (staggers the banks)
@@ -291,39 +331,7 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
       const float gm = a.gamma[tkc];
       // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
       const float val = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, gm), (float)(acc[m][r] >> 6)));
-      if (EPI == NLG_EPI_STORE || EPI == NLG_EPI_ARGMAX) {
-        if (live) a.y[(size_t)tk * a.ystride + row] = val;
-      } else if (EPI == NLG_EPI_RESID) {
-        if (live) a.y[(size_t)tk * a.ystride + row] = __fadd_rn(a.res[(size_t)tk * a.rstride + row], val);
-      } else if (EPI == NLG_EPI_SWIGLU || EPI == NLG_EPI_QKV) {
-        const float pv = __int_as_float(nlg_dpp<0xB1>(__float_as_int(val)));  // row ^ 1
-        if (EPI == NLG_EPI_SWIGLU) {
-          if (live && !(lane & 1)) {
-            const float sg = 1.0f / (1.0f + expf(0.0f - val));
-            a.y[(size_t)tk * a.ystride + (row >> 1)] = (val * sg) * pv;
-          }
-        } else if (live) {
-          const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(tk % a.qper) : 0);
-          const bool pos_ok = pr >= 0 && (uint32_t)pr < a.max_seq;
-          const uint32_t p = pos_ok ? (uint32_t)pr : 0u;
-          const uint32_t sec = row < a.nq ? row : (row < a.nq + a.nkv ? row - a.nq : row - a.nq - a.nkv);
-          const uint32_t dd = sec % a.hd, half = a.hd >> 1, ci = p * half + (dd >> 1);
-          const float cs = a.co[ci], sn = a.si[ci];
-          const bool odd = lane & 1;
-          const float a0 = odd ? pv : val, a1 = odd ? val : pv;
-          const float rot = odd ? __fadd_rn(__fmul_rn(a0, sn), __fmul_rn(a1, cs))
-                                : __fsub_rn(__fmul_rn(a0, cs), __fmul_rn(a1, sn));
-          if (row < a.nq) {
-            a.y[(size_t)tk * a.ystride + row] = rot;
-          } else if (pos_ok) {
-            const bool isk = row < a.nq + a.nkv;
-            const uint32_t kh = sec / a.hd, sq = a.qper ? tk / a.qper : tk;
-            const size_t at = (((size_t)sq * a.kvheads + kh) * a.max_seq + p) * a.hd + dd;
-            if (isk) a.kc[at] = __builtin_bit_cast(uint16_t, (_Float16)rot);
-            else a.vc[at] = __builtin_bit_cast(uint16_t, (_Float16)val);
-          }
-        }
-      }
+      tg_store<EPI>(a, lane, row, tk, live, val);
       if (EPI == NLG_EPI_ARGMAX) {
         // first maximum over the wave's 16 rows for this token
         float bv = live && val == val ? val : -INFINITY;
@@ -360,6 +368,196 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
   }
 }
 
+// ------------------------------------------------------------ k_tgemm_l
+//
+// Many tokens (prefill): a workgroup owns 32 NB WR output rows x 128 tokens;
+// its 2 WR waves 32 NB rows x 64 tokens each (NB x 2 blocks of
+// v_mfma_i32_32x32x32_i8, whose layout, checked on gfx950, is
+// C[i][j] = sum over lane groups g = 0..1 and bytes b of
+// A[lane 32g + i][b] * B[lane 32g + j][b], lane l's result r at row
+// (r % 4) + 8 (r / 4) + 4 (l / 32), column l % 32).  Columns go in chunks
+// of 256 (8 MFMA steps): lane group g at step t covers 2-bit word 8g + t
+// of the chunk, so a lane's weights for a chunk are 8 consecutive words
+// (32 bytes) of its row.  Loads run two chunks ahead of the matrix cores:
+// chunk c+2's weights and activations are fetched while chunk c computes
+// and chunk c+1's wait in registers to go to LDS.  Every decoded B operand
+// feeds two MFMAs.
+
+#define TL_PITCH (TG_KC + 16)   // LDS row pitch (bytes) of the activation stage
+
+template <int NB, int WR, int EPI>
+__global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
+  typedef int v16i __attribute__((ext_vector_type(16)));
+  typedef uint32_t wvec __attribute__((ext_vector_type(8 * NB)));
+  constexpr int AI = 16 / WR;  // 16-byte activation pieces per thread and chunk
+  typedef uint32_t avec __attribute__((ext_vector_type(4 * AI)));
+  extern __shared__ __align__(16) uint8_t s_a[];  // [2][128 tokens][TL_PITCH]
+  asm volatile("" ::"s"(a.xq), "s"(a.gamma), "s"(a.w2), "s"(a.bias), "s"(a.beta), "s"(a.y), "s"(a.seq),
+               "s"(a.out), "s"(a.cols), "s"(a.wng), "s"(a.ystride), "s"(a.beta_per_row));
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w & 1, wn = w >> 1;  // wave's token half, row block (of WR)
+  const int li = lane & 31, lg = lane >> 5;
+  const uint32_t rbase = blockIdx.x * (32 * NB * WR) + wn * (32 * NB);
+  const uint32_t tok0 = blockIdx.y * 128;
+  const uint32_t nchunks = a.cols / TG_KC;
+  // weight rows of this lane: rbase + 32 nt + li
+  const uint32_t rw0 = rbase + li, rw1 = rbase + 32 + li;
+  const uint32_t rc0 = rw0 < a.out ? rw0 : a.out - 1, rc1 = rw1 < a.out ? rw1 : a.out - 1;
+  const uint4 *w0 = (const uint4 *)(a.w2 + (size_t)rc0 * a.wng) + 2 * lg;
+  const uint4 *w1 = (const uint4 *)(a.w2 + (size_t)rc1 * a.wng) + 2 * lg;
+  // activation staging: thread t copies token t/16 + 8 WR i (i < AI), slot t % 16
+  const uint32_t slot = threadIdx.x % 16u, tsub = threadIdx.x / 16u;
+  const uint8_t *xb[AI];
+#pragma unroll
+  for (int i = 0; i < AI; i++) {
+    const uint32_t tk = tok0 + tsub + 8 * WR * i < a.seq ? tok0 + tsub + 8 * WR * i : a.seq - 1;
+    xb[i] = a.xq + (size_t)tk * a.cols + 16 * slot;
+  }
+#define TL_LOADW(c, dst)                                                                   \
+  do {                                                                                     \
+    const uint4 u0 = w0[4 * (c)], u1 = w0[4 * (c) + 1];                                    \
+    dst[0] = u0.x; dst[1] = u0.y; dst[2] = u0.z; dst[3] = u0.w;                             \
+    dst[4] = u1.x; dst[5] = u1.y; dst[6] = u1.z; dst[7] = u1.w;                             \
+    if (NB == 2) {                                                                         \
+      const uint4 u2 = w1[4 * (c)], u3 = w1[4 * (c) + 1];                                  \
+      dst[8 % (8 * NB)] = u2.x; dst[9 % (8 * NB)] = u2.y; dst[10 % (8 * NB)] = u2.z;       \
+      dst[11 % (8 * NB)] = u2.w; dst[12 % (8 * NB)] = u3.x; dst[13 % (8 * NB)] = u3.y;     \
+      dst[14 % (8 * NB)] = u3.z; dst[15 % (8 * NB)] = u3.w;                                \
+    }                                                                                      \
+  } while (0)
+#define TL_LOADA(c, dst)                                                                   \
+  do {                                                                                     \
+    _Pragma("unroll") for (int i = 0; i < AI; i++) {                                       \
+      const uint4 u = *(const uint4 *)(xb[i] + (size_t)(c) * TG_KC);                       \
+      dst[4 * i] = u.x; dst[4 * i + 1] = u.y; dst[4 * i + 2] = u.z; dst[4 * i + 3] = u.w;  \
+    }                                                                                      \
+  } while (0)
+#define TL_STOREA(buf, src)                                                                \
+  do {                                                                                     \
+    _Pragma("unroll") for (int i = 0; i < AI; i++)                                         \
+      *(uint4 *)(s_a + (size_t)(buf) * 128 * TL_PITCH + (tsub + 8 * WR * i) * TL_PITCH + 16 * slot) = \
+          make_uint4(src[4 * i], src[4 * i + 1], src[4 * i + 2], src[4 * i + 3]);          \
+  } while (0)
+  // Weights run two chunks ahead in three register sets that rotate through
+  // a three-chunk unrolled loop, so no set is ever copied (a copy would wait
+  // on the loads still in flight); activations run one chunk ahead.
+  wvec wA, wB, wC;
+  avec aX;
+  const uint32_t c1 = nchunks > 1 ? 1 : 0;
+  TL_LOADW(0, wA);
+  TL_LOADA(0, aX);
+  TL_LOADW(c1, wB);
+  const float *bsrc = a.bias ? a.bias : a.beta;
+  const float bo0 = a.bias ? bsrc[rc0] : 0.0f, bo1 = a.bias ? bsrc[rc1] : 0.0f;
+  const float be0 = a.beta[a.beta_per_row ? rc0 : 0], be1 = a.beta[a.beta_per_row ? rc1 : 0];
+  TL_STOREA(0, aX);
+  v16i acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};  // [token block][row block]
+  const uint8_t *sa0 = s_a + (size_t)(wm * 64 + li) * TL_PITCH + 16 * (8 * lg);
+  const uint8_t *sa1 = sa0 + 32 * TL_PITCH;
+#define TL_MMA(buf, WCUR)                                                                    \
+  _Pragma("unroll") for (int t = 0; t < 8; t++) {                                             \
+    const uint32_t x0 = WCUR[t];                                                              \
+    const v4i b0 = {(int)((x0 << 6) & 0xC0C0C0C0u), (int)((x0 << 4) & 0xC0C0C0C0u),           \
+                    (int)((x0 << 2) & 0xC0C0C0C0u), (int)(x0 & 0xC0C0C0C0u)};                  \
+    const uint4 av0 = *(const uint4 *)(sa0 + (buf) * 128 * TL_PITCH + 16 * t);                \
+    const uint4 av1 = *(const uint4 *)(sa1 + (buf) * 128 * TL_PITCH + 16 * t);                \
+    const v4i a0 = {(int)av0.x, (int)av0.y, (int)av0.z, (int)av0.w};                          \
+    const v4i a1 = {(int)av1.x, (int)av1.y, (int)av1.z, (int)av1.w};                          \
+    acc00 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc00, 0, 0, 0);                    \
+    acc10 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc10, 0, 0, 0);                    \
+    if (NB == 2) {                                                                            \
+      const uint32_t x1 = WCUR[(8 + t) % (8 * NB)];                                           \
+      const v4i b1 = {(int)((x1 << 6) & 0xC0C0C0C0u), (int)((x1 << 4) & 0xC0C0C0C0u),         \
+                      (int)((x1 << 2) & 0xC0C0C0C0u), (int)(x1 & 0xC0C0C0C0u)};                \
+      acc01 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, acc01, 0, 0, 0);                  \
+      acc11 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc11, 0, 0, 0);                  \
+    }                                                                                         \
+  }
+  // chunk c: fetch chunk c + 1's activations, then chunk c + 2's weights
+  // (in that order: the staging store of the activations waits on its loads
+  // only), clamped so the last fetches repeat; multiply chunk c, stage c + 1
+#define TL_STEP(k, WCUR, WLOAD)                                                               \
+  {                                                                                           \
+    const uint32_t c = c0 + (k);                                                              \
+    TL_LOADA(c + 1 < nchunks ? c + 1 : nchunks - 1, aX);                                      \
+    TL_LOADW(c + 2 < nchunks ? c + 2 : nchunks - 1, WLOAD);                                   \
+    __syncthreads();                                                                          \
+    TL_MMA(c & 1, WCUR);                                                                      \
+    TL_STOREA((c + 1) & 1, aX);                                                               \
+  }
+  // whole groups of three chunks without branches (a conditional step would
+  // merge register sets at its join and copy them), then the last one or two
+  uint32_t c0 = 0;
+  for (; c0 + 3 <= nchunks; c0 += 3) {
+    TL_STEP(0, wA, wC)
+    TL_STEP(1, wB, wA)
+    TL_STEP(2, wC, wB)
+  }
+  if (c0 < nchunks) TL_STEP(0, wA, wC)
+  if (c0 + 1 < nchunks) TL_STEP(1, wB, wA)
+#undef TL_STEP
+#undef TL_MMA
+#undef TL_LOADW
+#undef TL_LOADA
+#undef TL_STOREA
+  // epilogue: acc[mt][nt] register r is token tok0 + 64 wm + 32 mt + (r%4) + 8 (r/4) + 4 lg,
+  // row rbase + 32 nt + li
+  const bool l0 = rw0 < a.out, l1 = NB == 2 && rw1 < a.out;
+  if (EPI == NLG_EPI_SWIGLU) {
+    // Gate row 2j and up row 2j+1 sit in lanes l, l^1.  Each lane of a pair
+    // finishes half of the pair's tokens: the even lane registers 0..7, the
+    // odd lane 8..15, after swapping the other half's value with its partner.
+    const bool odd = lane & 1;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+#pragma unroll
+      for (int nt = 0; nt < NB; nt++) {
+        const v16i q = mt ? (nt ? acc11 : acc10) : (nt ? acc01 : acc00);
+        const float bo = nt ? bo1 : bo0, be = nt ? be1 : be0;
+        const uint32_t row = nt ? rw1 : rw0;
+        const bool lr = nt ? l1 : l0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          const uint32_t tlo = tok0 + 64 * wm + 32 * mt + (k % 4) + 8 * (k / 4) + 4 * lg;
+          const uint32_t thi = tlo + 16;  // register k + 8
+          const float glo = a.gamma[tlo < a.seq ? tlo : a.seq - 1];
+          const float ghi = a.gamma[thi < a.seq ? thi : a.seq - 1];
+          // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
+          const float vlo = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, glo), (float)(q[k] >> 6)));
+          const float vhi = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, ghi), (float)(q[k + 8] >> 6)));
+          const float keep = odd ? vhi : vlo, give = odd ? vlo : vhi;
+          const float got = __int_as_float(nlg_dpp<0xB1>(__float_as_int(give)));  // from lane ^ 1
+          const float g = odd ? got : keep, u = odd ? keep : got;
+          const uint32_t tk = odd ? thi : tlo;
+          if (lr && tk < a.seq) {
+            const float sg = 1.0f / (1.0f + expf(0.0f - g));
+            a.y[(size_t)tk * a.ystride + (row >> 1)] = (g * sg) * u;
+          }
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const uint32_t tk = tok0 + 64 * wm + 32 * mt + (r % 4) + 8 * (r / 4) + 4 * lg;
+      const uint32_t tkc = tk < a.seq ? tk : a.seq - 1;
+      const float gm = a.gamma[tkc];
+      const int q0 = mt ? acc10[r] : acc00[r];
+      // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
+      const float v0 = __fadd_rn(bo0, __fmul_rn(__fmul_rn(be0, gm), (float)(q0 >> 6)));
+      tg_store<EPI>(a, lane, rw0, tk, l0 && tk < a.seq, v0);
+      if (NB == 2) {
+        const int q1 = mt ? acc11[r] : acc01[r];
+        const float v1 = __fadd_rn(bo1, __fmul_rn(__fmul_rn(be1, gm), (float)(q1 >> 6)));
+        tg_store<EPI>(a, lane, rw1, tk, l1 && tk < a.seq, v1);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------ launchers
 
 int nlg_act_q_launch(const float *x, const float *gain, float eps, const float *attn_mz, uint32_t attn_nc,
@@ -389,6 +587,32 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   if (a.cols % TG_KC || !a.cols) return nlg_fail("ternary GEMM: cols must be a multiple of %d", TG_KC);
   if (((uintptr_t)a.w2 & 15) || ((uintptr_t)a.xq & 15)) return nlg_fail("ternary GEMM: 16-byte alignment");
   a.wng = a.cols / 16;
+  if (a.seq >= 128 && epi != NLG_EPI_ARGMAX) {
+    // the largest row tile (256, 128 or 64 rows) whose grid still fills the CUs
+    const uint32_t ty = (a.seq + 127) / 128;
+    const int tile = (uint64_t)nlg_blocks(a.out, 256) * ty >= 256   ? 256
+                     : (uint64_t)nlg_blocks(a.out, 128) * ty >= 256 ? 128
+                                                                    : 64;
+    const dim3 grid(nlg_blocks(a.out, tile), ty), blk(tile == 256 ? 512 : 256);
+    if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
+    const size_t lds = (size_t)2 * 128 * TL_PITCH;
+#define TLG(E)                                                                            \
+  do {                                                                                    \
+    if (tile == 256) hipLaunchKernelGGL((k_tgemm_l<2, 4, E>), grid, blk, lds, st, a);     \
+    else if (tile == 128) hipLaunchKernelGGL((k_tgemm_l<2, 2, E>), grid, blk, lds, st, a); \
+    else hipLaunchKernelGGL((k_tgemm_l<1, 2, E>), grid, blk, lds, st, a);                 \
+  } while (0)
+    switch (epi) {
+      case NLG_EPI_STORE: TLG(NLG_EPI_STORE); break;
+      case NLG_EPI_RESID: TLG(NLG_EPI_RESID); break;
+      case NLG_EPI_SWIGLU: TLG(NLG_EPI_SWIGLU); break;
+      case NLG_EPI_QKV: TLG(NLG_EPI_QKV); break;
+      default: return nlg_fail("ternary GEMM: unknown epilogue %d", epi);
+    }
+#undef TLG
+    NLG_LAUNCHED("ternary GEMM (int8 MFMA, 128 x 128 tiles)");
+    return NLG_OK;
+  }
   // up to 32 tokens per workgroup: the 32 x 2064-byte activation block
   // stays under the 64 KiB a workgroup may hold
   const int MB = a.seq <= 16 ? 1 : 2;
