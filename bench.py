@@ -422,6 +422,40 @@ def pmc_probe():
     print("pmc probe: 64 steps of k_tern_fused (4096x4096), 4 copies of 64 MiB", flush=True)
 
 
+def profile_eager():
+    """Launch, without graphs (rocprofv3's kernel trace follows eager launches
+    only), what the rocprof summaries cover: the config-5 decoder stack at
+    batch 1 and 32 (512-row prefill, then 16 decode steps) and the config-4
+    FFN at 512 and 16384 tokens (10 passes each).  Prints one line per phase."""
+    import nlgpu
+    nlgpu.init()
+    c = STACK
+    for batch in (1, 32):
+        s = nlgpu.Stack(**c, max_seq=PROMPT + DECODE, batch=batch, seed=20260921 + 5)
+        ids = (nlgpu.uniform(20260921 + 55, batch * PROMPT) * c["vocab"]).astype(np.int32).reshape(batch, PROMPT)
+        s.prefill(ids)
+        s.step(16, graph=False)
+        nlgpu.sync()
+        s.close()
+        print(f"profile: stack batch {batch}: prefill {PROMPT} rows + 16 eager decode steps", flush=True)
+    seed = 20260921 + 4
+    gu = np.empty((2 * FFN_F, FFN_D // 16), np.uint32)
+    gu[0::2] = nlgpu.pack_ternary(nlgpu.trits(seed, (FFN_F, FFN_D)))
+    gu[1::2] = nlgpu.pack_ternary(nlgpu.trits(seed + 1, (FFN_F, FFN_D)))
+    dgu, dwd = nlgpu.to_device(gu), nlgpu.to_device(nlgpu.pack_ternary(nlgpu.trits(seed + 2, (FFN_D, FFN_F))))
+    bgu = nlgpu.to_device(np.full(2 * FFN_F, 1.0 / np.sqrt(FFN_D / 2), np.float32))
+    bd = nlgpu.to_device(np.array([1.0 / np.sqrt(FFN_F / 2)], np.float32))
+    for B in (512, 16384):
+        x = nlgpu.to_device(nlgpu.normal(seed + 10 + B, B * FFN_D))
+        h, y = nlgpu.DeviceArray(B * FFN_F * 4), nlgpu.DeviceArray(B * FFN_D * 4)
+        for _ in range(10):
+            nlgpu.rms_ternary_swiglu(x, None, 0.0, dgu, bgu, h, B, FFN_F, FFN_D)
+            nlgpu.ternary_linear(h, dwd, None, bd, y, B, FFN_D, FFN_F)
+        nlgpu.sync()
+        print(f"profile: FFN {FFN_D}x{FFN_F} at {B} tokens, 10 passes", flush=True)
+        del x, h, y
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -431,9 +465,14 @@ def main():
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decoder stack")
     ap.add_argument("--pmc-probe", action="store_true", help="only the launches the PMC profiles count")
+    ap.add_argument("--profile-eager", action="store_true",
+                    help="only the eager stack and FFN launches the rocprof kernel summaries cover")
     args = ap.parse_args()
     if args.pmc_probe:
         pmc_probe()
+        return
+    if args.profile_eager:
+        profile_eager()
         return
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the decode path is not sharded); "

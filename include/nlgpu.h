@@ -268,6 +268,19 @@ int nlg_attn_ternary_linear_residual(const void *workspace, size_t workspace_byt
                                      const float *beta, int beta_per_row, const float *res, float *y,
                                      uint32_t out, void *stream);
 
+/* Causal GQA attention for a whole prompt: attn-causal-gqa's arithmetic
+ * (kernels.el:934-990: s = (q.k)/sqrt(head_dim) over positions 0..p,
+ * ctx = sum(exp(s - max) v) / sum(exp(s - max))) over the fp16 caches
+ * [rows/qper][kvheads][max_seq][head_dim] that nlg_rms_ternary_qkv_rope
+ * fills.  q and ctx are [rows][heads*head_dim] f32; row r is sequence
+ * r / qper at position pos[0] + r % qper.  head_dim 64 or 128, heads/kvheads
+ * in {1,2,4,8}, rows a multiple of qper; one launch, f16 matrix cores with
+ * q and the probabilities split into hi + lo halves (f32-grade products). */
+int nlg_prefill_attn_f16(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                         const int32_t *pos, uint32_t rows, uint32_t qper, uint32_t heads,
+                         uint32_t kvheads, uint32_t head_dim, uint32_t max_seq, float *ctx,
+                         void *stream);
+
 /* Synthetic data: n floats of sigma * N(0,1) from a counter-based
  * SplitMix64 stream (element 2p, 2p+1 = Box-Muller pair p); causal > 0 treats
  * the data as [.. x causal x causal] score tiles and writes -inf above each

@@ -158,6 +158,12 @@ uint32_t nlg_attn_chunk_count(uint32_t head_dim, uint32_t max_seq);
 int nlg_attn_chunks(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *pos, uint32_t rows,
                     uint32_t qper, uint32_t heads, uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
                     void *workspace, size_t workspace_bytes, hipStream_t st);
+// Causal attention of `rows` prompt rows (row r = sequence r / qper at
+// position pos[0] + r % qper) over the fp16 caches on the matrix cores;
+// ctx [rows][heads * head_dim] f32, normalised.
+int nlg_prefill_attn(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *pos, uint32_t rows,
+                     uint32_t qper, uint32_t heads, uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
+                     float *ctx, hipStream_t st);
 enum {
   NLG_EPI_STORE = 0,   // y = bias + (beta*gamma)*acc
   NLG_EPI_RESID = 1,   // y = res + that

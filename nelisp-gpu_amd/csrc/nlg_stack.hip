@@ -498,7 +498,7 @@ extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t 
     s->px = (float *)nlg_malloc((size_t)T * d * 4);
     s->pq = (float *)nlg_malloc((size_t)T * s->nq * 4);
     s->ph = (float *)nlg_malloc((size_t)T * f * 4);
-    s->pattn_ws_bytes = nlg_decode_attn_f16_workspace(T, c.heads, c.kv_heads, c.head_dim, c.max_seq);
+    s->pattn_ws_bytes = (size_t)T * s->nq * 4;
     s->pattn_ws = nlg_malloc(s->pattn_ws_bytes);
     if (!s->px || !s->pq || !s->ph || !s->pattn_ws) return NLG_ERR;
     s->pcap = T;
@@ -506,8 +506,7 @@ extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t 
   hipLaunchKernelGGL(k_embed_prompt, dim3(nlg_blocks(d, 256), T), dim3(256), 0, st, s->emb, s->prompt,
                      c.max_seq, P, s->px, d);
   NLG_LAUNCHED("embed prompt");
-  const uint32_t nchunk = nlg_attn_chunk_count(c.head_dim, c.max_seq);
-  const size_t pctx_bytes = ((size_t)T * nchunk * s->nq * 4 + 255) / 256 * 256;
+  float *pctx = (float *)s->pattn_ws;  // [T][nq] attention output
   for (uint32_t l = 0; l < c.layers; l++) {
     Layer &y = s->L[l];
     FusedArgs q{};
@@ -516,15 +515,13 @@ extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t 
     q.ystride = s->nq; q.hd = c.head_dim; q.kvheads = c.kv_heads; q.max_seq = c.max_seq; q.co = s->co;
     q.si = s->si; q.pos = s->pos; q.kc = y.kc; q.vc = y.vc; q.qper = P;
     if (nlg_fused_launch(q, NLG_PRO_RMS, NLG_EPI_QKV, 0, st)) return NLG_ERR;
-    if (nlg_attn_chunks(s->pq, y.kc, y.vc, s->pos, T, P, c.heads, c.kv_heads, c.head_dim, c.max_seq,
-                        s->pattn_ws, s->pattn_ws_bytes, st))
+    if (nlg_prefill_attn(s->pq, y.kc, y.vc, s->pos, T, P, c.heads, c.kv_heads, c.head_dim, c.max_seq, pctx,
+                         st))
       return NLG_ERR;
     FusedArgs o{};
-    o.x = (const float *)s->pattn_ws; o.attn_mz = (const float *)((char *)s->pattn_ws + pctx_bytes);
-    o.attn_nc = nchunk; o.hd = c.head_dim; o.w2 = y.wo; o.beta = y.bo; o.seq = T; o.out = d; o.cols = s->nq;
+    o.x = pctx; o.w2 = y.wo; o.beta = y.bo; o.seq = T; o.out = d; o.cols = s->nq;
     o.y = s->px; o.ystride = d; o.res = s->px; o.rstride = d;
-    if (nchunk > NLG_ATTN_MAX_CHUNKS) return nlg_fail("stack prefill: max_seq too long for the folded merge");
-    if (nlg_fused_launch(o, NLG_PRO_ATTN, NLG_EPI_RESID, 0, st)) return NLG_ERR;
+    if (nlg_fused_launch(o, NLG_PRO_NONE, NLG_EPI_RESID, 0, st)) return NLG_ERR;
     FusedArgs g{};
     g.x = s->px; g.gain = y.gffn; g.eps = c.rms_eps; g.w2 = y.wgu; g.beta = y.bgu; g.beta_per_row = 1;
     g.seq = T; g.out = 2 * f; g.cols = d; g.y = s->ph; g.ystride = f;

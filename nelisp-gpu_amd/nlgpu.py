@@ -103,6 +103,7 @@ def lib() -> C.CDLL:
         "nlg_decode_attn_f16_chunks": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, sz, vp]),
         "nlg_attn_ternary_linear_residual": (i32, [vp, sz, u32, u32, u32, u32, u32, vp, vp, vp, i32, vp,
                                                    vp, u32, vp]),
+        "nlg_prefill_attn_f16": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp, vp]),
         "nlg_fill_normal": (i32, [vp, C.c_uint64, C.c_uint64, C.c_float, u32, vp]),
         "nlg_stack_create": (i32, [C.POINTER(StackConfig), C.POINTER(vp)]),
         "nlg_stack_destroy": (None, [vp]),
@@ -332,6 +333,14 @@ def decode_attn_f16_chunks(q, kc, vc, pos, batch, heads, kvheads, head_dim, max_
     _check(lib().nlg_decode_attn_f16_chunks(q.ptr, kc.ptr, vc.ptr, pos.ptr, batch, heads, kvheads,
                                             head_dim, max_seq, workspace.ptr, workspace.nbytes, stream),
            "decode_attn_f16_chunks")
+
+
+def prefill_attn_f16(q, kc, vc, pos, rows, qper, heads, kvheads, head_dim, max_seq, ctx,
+                     stream=None) -> None:
+    """Causal attention of rows prompt rows (row r = sequence r // qper at
+    position pos[0] + r % qper) over fp16 caches; ctx [rows][heads*head_dim]."""
+    _check(lib().nlg_prefill_attn_f16(q.ptr, kc.ptr, vc.ptr, pos.ptr, rows, qper, heads, kvheads, head_dim,
+                                      max_seq, ctx.ptr, stream), "prefill_attn_f16")
 
 
 def attn_ternary_linear_residual(workspace, batch, heads, kvheads, head_dim, max_seq, w2, bias, beta,

@@ -225,6 +225,46 @@ def test_attention_merge_folded_into_output_projection(B, heads, kvh, hd, max_se
     same_bits(y.download(f32, B * d), y_ref.download(f32, B * d))
 
 
+@pytest.mark.parametrize("B,heads,kvh,hd,max_seq,P,pos0", [
+    (1, 20, 5, 128, 768, 512, 0),     # the decoder stack's prompt
+    (2, 8, 2, 64, 130, 100, 30),      # ragged rows, later start, max_seq not a multiple of 32
+    (3, 16, 2, 128, 200, 45, 155),    # prompt ends at max_seq
+    (2, 4, 4, 64, 64, 33, 0),         # one query head per kv head
+    (1, 16, 2, 128, 96, 40, 10)])     # eight query heads per kv head
+def test_prefill_attention_fp16(B, heads, kvh, hd, max_seq, P, pos0):
+    """Whole-prompt causal attention on the matrix cores == the per-row
+    decode attention restatement at each row's position."""
+    print(f"[gpu] prefill attention B={B} heads={heads}/{kvh} hd={hd} max_seq={max_seq} P={P} pos0={pos0}",
+          flush=True)
+    n = B * kvh * max_seq * hd
+    kc = nlgpu.normal(hd + 5 * B, n).astype(np.float16).view(np.uint16)
+    vc = nlgpu.normal(hd + 5 * B + 1, n).astype(np.float16).view(np.uint16)
+    q = (nlgpu.normal(P + pos0, B * P * heads * hd) * f32(2.0)).astype(f32)
+    ctx = nlgpu.DeviceArray(B * P * heads * hd * 4)
+    nlgpu.prefill_attn_f16(nlgpu.to_device(q), nlgpu.to_device(kc), nlgpu.to_device(vc),
+                           nlgpu.to_device(np.array([pos0], np.int32)), B * P, P, heads, kvh, hd, max_seq, ctx)
+    got = ctx.download(f32, B * P * heads * hd).reshape(B, P, heads * hd)
+    qr = q.reshape(B, P, heads * hd)
+    per = kvh * max_seq * hd
+    worst = 0.0
+    for b in range(B):
+        for i in range(P):
+            want = orc.decode_attn_f16(qr[b, i], kc[b * per:(b + 1) * per], vc[b * per:(b + 1) * per], pos0 + i,
+                                       1, heads, kvh, hd, max_seq)
+            worst = max(worst, float(np.abs(got[b, i] - want).max() / np.abs(want).max()))
+    print(f"  max err / max|out| = {worst:.2e}", flush=True)
+    assert worst <= 1e-4
+
+
+def test_prefill_attention_rejects_bad_shapes():
+    d = nlgpu.DeviceArray(4096)
+    pos = nlgpu.to_device(np.array([0], np.int32))
+    with pytest.raises(nlgpu.NlgError, match="multiple"):
+        nlgpu.prefill_attn_f16(d, d, d, pos, 10, 4, 4, 2, 64, 16, d)
+    with pytest.raises(nlgpu.NlgError, match="head_dim"):
+        nlgpu.prefill_attn_f16(d, d, d, pos, 4, 4, 4, 2, 96, 16, d)
+
+
 def test_folded_merge_rejects_too_many_chunks():
     ws = nlgpu.DeviceArray(nlgpu.decode_attn_f16_workspace(1, 4, 1, 128, 2048))
     d = nlgpu.DeviceArray(4 * 512)
