@@ -263,7 +263,7 @@ def decode_bench(batch: int, stream):
             "step_bytes": int(step_bytes), "step_gbs": round(step_bytes / (ms_tok * 1e-3) / 1e9, 1),
             "step_frac": round(step_bytes / (ms_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             # per layer: 5 launches, or 9 when the linears take the batched (quantise + GEMM) form
-            "launches_per_step": L * (9 if batch >= 8 else 5) + (3 if batch >= 8 else 2),
+            "launches_per_step": L * (9 if batch >= 8 else 5) + (2 if batch >= 8 else 1) + (2 if batch > 1 else 1),
             "lm_head_bytes": int(lm_bytes), "per_kernel": per}
 
 

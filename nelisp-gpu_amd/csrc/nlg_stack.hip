@@ -131,9 +131,11 @@ struct SampleArgs {
   uint32_t dim, batch, max_seq, vocab;
 };
 
-// One workgroup: for each sequence, the greedy token after position p; the
-// next token is the prompt's while it lasts; its embedding becomes x; then
-// the position advances (after every thread has read it).
+// The greedy token after position p of one sequence (ONE: the only one,
+// and this workgroup then advances the position; otherwise sequence
+// blockIdx.x, and k_advance moves the position once every row is done); the
+// next token is the prompt's while it lasts; its embedding becomes x.
+template <bool ONE>
 __global__ __launch_bounds__(1024) void k_sample(SampleArgs a) {
   __shared__ float sv[16];
   __shared__ int32_t si[16];
@@ -141,40 +143,54 @@ __global__ __launch_bounds__(1024) void k_sample(SampleArgs a) {
   const int32_t p = a.pos[0];
   const int32_t plen = a.plen[0];
   const int nw = blockDim.x >> 6, w = threadIdx.x >> 6;
-  for (uint32_t b = 0; b < a.batch; b++) {
-    float v = -INFINITY;
-    int32_t i = -1;
-    for (uint32_t j = threadIdx.x; j < a.nparts; j += blockDim.x) {
-      const float ov = a.pval[(size_t)b * a.nparts + j];
-      const int32_t oi = a.pidx[(size_t)b * a.nparts + j];
-      if (better(ov, oi, v, i)) { v = ov; i = oi; }
+  const uint32_t b = ONE ? 0u : blockIdx.x;
+  const float *pv = a.pval + (size_t)b * a.nparts;
+  const int32_t *pi = a.pidx + (size_t)b * a.nparts;
+  float v = -INFINITY;
+  int32_t i = -1;
+  // eight partials per thread in flight at a time (independent loads)
+  for (uint32_t j0 = threadIdx.x; j0 < a.nparts; j0 += 8 * blockDim.x) {
+    float ov[8];
+    int32_t oi[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const uint32_t j = j0 + u * blockDim.x;
+      const uint32_t jc = j < a.nparts ? j : a.nparts - 1;
+      ov[u] = pv[jc];
+      oi[u] = j < a.nparts ? pi[jc] : -1;
     }
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(v, off);
-      const int32_t oi = __shfl_xor(i, off);
-      if (better(ov, oi, v, i)) { v = ov; i = oi; }
-    }
-    if ((threadIdx.x & 63) == 0) { sv[w] = v; si[w] = i; }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      v = sv[0]; i = si[0];
-      for (int k = 1; k < nw; k++)
-        if (better(sv[k], si[k], v, i)) { v = sv[k]; i = si[k]; }
-      const size_t row = (size_t)b * a.max_seq;
-      int32_t t = i < 0 ? 0 : i;
-      if (p + 1 < plen) t = a.prompt[row + p + 1];
-      if (t < 0 || (uint32_t)t >= a.vocab) t = 0;
-      if (p >= 0 && (uint32_t)p < a.max_seq) a.greedy[row + p] = i;
-      if (p + 1 >= 0 && (uint32_t)(p + 1) < a.max_seq) a.hist[row + p + 1] = t;
-      s_tok = t;
-    }
-    __syncthreads();
-    const int32_t t = s_tok;
-    for (uint32_t j = threadIdx.x; j < a.dim; j += blockDim.x)
-      a.x[(size_t)b * a.dim + j] = a.emb[(size_t)t * a.dim + j];
-    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      if (better(ov[u], oi[u], v, i)) { v = ov[u]; i = oi[u]; }
   }
-  if (threadIdx.x == 0) a.pos[0] = p + 1;
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(v, off);
+    const int32_t oi = __shfl_xor(i, off);
+    if (better(ov, oi, v, i)) { v = ov; i = oi; }
+  }
+  if ((threadIdx.x & 63) == 0) { sv[w] = v; si[w] = i; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    v = sv[0]; i = si[0];
+    for (int k = 1; k < nw; k++)
+      if (better(sv[k], si[k], v, i)) { v = sv[k]; i = si[k]; }
+    const size_t row = (size_t)b * a.max_seq;
+    int32_t t = i < 0 ? 0 : i;
+    if (p + 1 < plen) t = a.prompt[row + p + 1];
+    if (t < 0 || (uint32_t)t >= a.vocab) t = 0;
+    if (p >= 0 && (uint32_t)p < a.max_seq) a.greedy[row + p] = i;
+    if (p + 1 >= 0 && (uint32_t)(p + 1) < a.max_seq) a.hist[row + p + 1] = t;
+    s_tok = t;
+  }
+  __syncthreads();
+  const int32_t t = s_tok;
+  for (uint32_t j = threadIdx.x; j < a.dim; j += blockDim.x)
+    a.x[(size_t)b * a.dim + j] = a.emb[(size_t)t * a.dim + j];
+  if (ONE && threadIdx.x == 0) a.pos[0] = p + 1;  // every thread read p before the barrier
+}
+
+__global__ void k_advance(int32_t *pos) {
+  if (threadIdx.x == 0) pos[0] = pos[0] + 1;
 }
 
 // ------------------------------------------------------------ the stack
@@ -431,7 +447,12 @@ static int stack_head(nlg_stack *s) {
   sa.pval = s->pval; sa.pidx = s->pidx; sa.nparts = s->nparts; sa.prompt = s->prompt;
   sa.hist = s->hist; sa.greedy = s->greedy; sa.pos = s->pos; sa.plen = s->plen; sa.emb = s->emb;
   sa.x = s->x; sa.dim = d; sa.batch = B; sa.max_seq = c.max_seq; sa.vocab = c.vocab;
-  hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, nlg_stream(nullptr), sa);
+  if (B == 1) {
+    hipLaunchKernelGGL(k_sample<true>, dim3(1), dim3(1024), 0, nlg_stream(nullptr), sa);
+  } else {
+    hipLaunchKernelGGL(k_sample<false>, dim3(B), dim3(1024), 0, nlg_stream(nullptr), sa);
+    hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, nlg_stream(nullptr), s->pos);
+  }
   NLG_LAUNCHED("sample");
   return NLG_OK;
 }
