@@ -368,6 +368,109 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
   }
 }
 
+// ------------------------------------------------------------ k_tgemm_k
+//
+// Few tokens and few output rows (batch-32 decode: 2560..3840 rows): the
+// 64-row workgroups of k_tgemm leave most CUs idle, so here a workgroup owns
+// 16 output rows x 16 MB tokens and its four waves split the columns: wave w
+// takes chunks w*per .. (w+1)*per - 1 (per = ceil(chunks / 4)) and loads its
+// operands straight from global memory into registers in matrix-core order
+// (no LDS stage, no barrier until the end), three chunks in flight in
+// register sets that rotate through a three-chunk unrolled loop; chunks past
+// its range load a valid chunk with the weights masked to zero.  The four
+// int32 partial sums meet in LDS (integer adds: exact in any order) and wave
+// w finishes accumulator register w of every token block.
+
+template <int MB, int EPI>
+__global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
+  constexpr int NA = 4 * MB;  // 16-byte activation pieces per lane and chunk
+  typedef uint32_t kvec __attribute__((ext_vector_type(4 + 4 * NA)));
+  __shared__ v4i s_red[4][MB][64];
+  asm volatile("" ::"s"(a.xq), "s"(a.gamma), "s"(a.w2), "s"(a.bias), "s"(a.beta), "s"(a.y), "s"(a.seq),
+               "s"(a.out), "s"(a.cols), "s"(a.wng), "s"(a.ystride), "s"(a.beta_per_row));
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const uint32_t row = blockIdx.x * 16 + lr;  // this lane's output row (B column j)
+  const uint32_t rowc = row < a.out ? row : a.out - 1;
+  const uint32_t tok0 = blockIdx.y * 16 * MB;
+  const uint32_t nchunks = a.cols / TG_KC;
+  const uint32_t per = (nchunks + 3) / 4, cb = w * per;
+  const uint32_t ce = min(cb + per, nchunks);
+  const uint32_t nsteps = (per + 2) / 3 * 3;  // whole rotations
+  const uint4 *wrow = (const uint4 *)(a.w2 + (size_t)rowc * a.wng) + lg;
+  // token rows of this lane (A row i = lr of each 16-token block), at column 64 lg
+  const uint8_t *xa[MB];
+#pragma unroll
+  for (int m = 0; m < MB; m++) {
+    const uint32_t tk = tok0 + 16 * m + lr;
+    xa[m] = a.xq + (size_t)(tk < a.seq ? tk : a.seq - 1) * a.cols + 64 * lg;
+  }
+  // set layout: [0..3] the lane's 4 weight words (64 columns), then for each
+  // token block m and step t the 16 activation bytes of columns 64 lg + 16 t
+#define TK_LOAD(S, k)                                                                     \
+  do {                                                                                    \
+    const uint32_t c = cb + (k);                                                          \
+    const uint32_t cc = c < ce ? c : nchunks - 1;                                         \
+    const uint32_t keep = c < ce ? 0xffffffffu : 0u;                                      \
+    const uint4 u = wrow[4 * cc];                                                         \
+    S[0] = u.x & keep; S[1] = u.y & keep; S[2] = u.z & keep; S[3] = u.w & keep;            \
+    _Pragma("unroll") for (int m = 0; m < MB; m++) {                                      \
+      _Pragma("unroll") for (int t = 0; t < 4; t++) {                                     \
+        const uint4 v = *(const uint4 *)(xa[m] + (size_t)cc * TG_KC + 16 * t);             \
+        S[4 + 16 * m + 4 * t] = v.x; S[5 + 16 * m + 4 * t] = v.y;                         \
+        S[6 + 16 * m + 4 * t] = v.z; S[7 + 16 * m + 4 * t] = v.w;                         \
+      }                                                                                   \
+    }                                                                                     \
+  } while (0)
+#define TK_MMA(S)                                                                         \
+  do {                                                                                    \
+    _Pragma("unroll") for (int t = 0; t < 4; t++) {                                       \
+      const uint32_t wd = S[t];                                                           \
+      const v4i bop = {(int)((wd << 6) & 0xC0C0C0C0u), (int)((wd << 4) & 0xC0C0C0C0u),    \
+                       (int)((wd << 2) & 0xC0C0C0C0u), (int)(wd & 0xC0C0C0C0u)};           \
+      _Pragma("unroll") for (int m = 0; m < MB; m++) {                                    \
+        const v4i aop = {(int)S[4 + 16 * m + 4 * t], (int)S[5 + 16 * m + 4 * t],          \
+                         (int)S[6 + 16 * m + 4 * t], (int)S[7 + 16 * m + 4 * t]};         \
+        acc[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop, acc[m], 0, 0, 0);       \
+      }                                                                                   \
+    }                                                                                     \
+  } while (0)
+  v4i acc[MB];
+#pragma unroll
+  for (int m = 0; m < MB; m++) acc[m] = (v4i){0, 0, 0, 0};
+  kvec sA, sB, sC;
+  TK_LOAD(sA, 0);
+  TK_LOAD(sB, 1);
+  for (uint32_t k = 0; k < nsteps; k += 3) {
+    TK_LOAD(sC, k + 2);
+    TK_MMA(sA);
+    TK_LOAD(sA, k + 3);
+    TK_MMA(sB);
+    TK_LOAD(sB, k + 4);
+    TK_MMA(sC);
+  }
+#undef TK_LOAD
+#undef TK_MMA
+#pragma unroll
+  for (int m = 0; m < MB; m++) s_red[w][m][lane] = acc[m];
+  __syncthreads();
+  // wave w: register r = w of each token block (token tok0 + 16 m + 4 lg + w)
+  const bool rlive = row < a.out;
+  const float bo_raw = (a.bias ? a.bias : a.beta)[a.bias ? rowc : 0];
+  const float be = a.beta[a.beta_per_row ? rowc : 0];
+  const float bo = a.bias ? bo_raw : 0.0f;
+#pragma unroll
+  for (int m = 0; m < MB; m++) {
+    const int32_t q = s_red[0][m][lane][w] + s_red[1][m][lane][w] + s_red[2][m][lane][w] + s_red[3][m][lane][w];
+    const uint32_t tk = tok0 + 16 * m + 4 * lg + w;
+    const bool live = rlive && tk < a.seq;
+    const float gm = a.gamma[tk < a.seq ? tk : a.seq - 1];
+    // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
+    const float val = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, gm), (float)(q >> 6)));
+    tg_store<EPI>(a, lane, row, tk, live, val);
+  }
+}
+
 // ------------------------------------------------------------ k_tgemm_l
 //
 // Many tokens (prefill): a workgroup owns 32 NB WR output rows x 128 tokens;
@@ -617,6 +720,28 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   // stays under the 64 KiB a workgroup may hold
   const int MB = a.seq <= 16 ? 1 : 2;
   const uint32_t MT = 16u * MB;
+  if (epi != NLG_EPI_ARGMAX && (uint64_t)nlg_blocks(a.out, 64) * ((a.seq + MT - 1) / MT) < 128) {
+    // too few 64-row workgroups to fill half the CUs: 16-row ones with the
+    // columns split over the waves (measured at 32 tokens: 2560..3840 rows
+    // gain, 13,824 rows lose to the extra activation reads)
+    const dim3 grid(nlg_blocks(a.out, 16), (a.seq + MT - 1) / MT), blk(256);
+    if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
+#define TKG(E)                                                                            \
+  do {                                                                                    \
+    if (MB == 1) hipLaunchKernelGGL((k_tgemm_k<1, E>), grid, blk, 0, st, a);              \
+    else hipLaunchKernelGGL((k_tgemm_k<2, E>), grid, blk, 0, st, a);                      \
+  } while (0)
+    switch (epi) {
+      case NLG_EPI_STORE: TKG(NLG_EPI_STORE); break;
+      case NLG_EPI_RESID: TKG(NLG_EPI_RESID); break;
+      case NLG_EPI_SWIGLU: TKG(NLG_EPI_SWIGLU); break;
+      case NLG_EPI_QKV: TKG(NLG_EPI_QKV); break;
+      default: return nlg_fail("ternary GEMM: unknown epilogue %d", epi);
+    }
+#undef TKG
+    NLG_LAUNCHED("ternary GEMM (int8 MFMA, split columns)");
+    return NLG_OK;
+  }
   const dim3 grid(nlg_blocks(a.out, 64), (a.seq + MT - 1) / MT), blk(256);
   if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
   const size_t lds = (size_t)MT * TG_PITCH;
