@@ -377,6 +377,39 @@ def ffn_bench(stream):
     return out
 
 
+def repack_bench(stream):
+    """Weight ingest: the config-5 gate|up matrix (13,824 x 2,560 trits) repacked
+    into the 2-bit layout from int8 lanes and from base-4 codes (pk 12), 8
+    rotated input copies each; algorithmic bytes = input + output words."""
+    import nlgpu
+    out, cols, pk, ncp = 2 * FFN_F, FFN_D, 12, 8
+    t = nlgpu.trits(20260921 + 6, (out, cols)).astype(np.int64)
+    ng, wng, fcount = (cols + 3) // 4, (cols + 15) // 16, (cols + pk - 1) // pk
+    lanes = t.astype(np.int8).view(np.uint8).reshape(out, cols)
+    wp = np.zeros((out, 4 * ng), np.uint8)
+    wp[:, :cols] = lanes
+    wp = wp.view("<u4").reshape(out, ng)
+    codes = np.zeros((out, fcount * pk), np.int64)
+    codes[:, :cols] = t + 1
+    wpk = (codes.reshape(out, fcount, pk) * (4 ** np.arange(pk))).sum(axis=2).astype(np.float32)
+    w2 = nlgpu.DeviceArray(out * wng * 4)
+    res = {}
+    for name, host, fn in (
+            ("int8_lanes", wp, lambda src: nlgpu.repack_i8_to_2bit(src, out, cols, w2, stream=stream)),
+            ("base4_pk12", wpk, lambda src: nlgpu.repack_packed_to_2bit(src, out, cols, pk, fcount, w2,
+                                                                         stream=stream))):
+        dsrc = nlgpu.DeviceArray(host.nbytes * ncp)
+        for c in range(ncp):
+            dsrc.upload(host, offset=c * host.nbytes)
+        us = _per_launch_us(lambda i: fn(_Ptr(dsrc.ptr + (i % ncp) * host.nbytes, host.nbytes)), 4 * ncp, stream)
+        nbytes = host.nbytes + out * wng * 4
+        res[name] = {"us": round(us, 3), "bytes": int(nbytes), "gbs": round(nbytes / us / 1e3, 1),
+                     "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+        dsrc.free()
+    w2.free()
+    return res
+
+
 def cpu_baseline(x, w_one, seconds: float):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import nlg_oracle as orc
@@ -492,6 +525,7 @@ def main():
         extra["matmul_config1"] = matmul_bench(stream)
         extra["softmax_config3"] = softmax_bench(stream)
         extra["swiglu_ffn_config4"] = ffn_bench(stream)
+        extra["weight_ingest_repack"] = repack_bench(stream)
     value = STEP_BYTES / (r["step_ms"] * 1e-3) / 1e9
     gemv_gbs = GEMV_BYTES / (r["gemv_ms"] * 1e-3) / 1e9
     stacked_gbs = GEMV_BYTES * COPIES / (r["stacked_ms"] * 1e-3) / 1e9

@@ -281,6 +281,20 @@ int nlg_prefill_attn_f16(const float *q, const uint16_t *kcache, const uint16_t 
                          uint32_t kvheads, uint32_t head_dim, uint32_t max_seq, float *ctx,
                          void *stream);
 
+/* Weight ingest: the reference's other ternary formats repacked into the
+ * 2-bit layout of ternary-rows (kernels.el:700-746) that every ternary entry
+ * point here reads ([out x ceil(cols/16)] u32, 4x fewer bytes than int8
+ * lanes, same int32 accumulators).  From int8 lanes: WP [out x ceil(cols/4)]
+ * of bitlinear-dp4a-1f / -rows (kernels.el:619-653).  From base-4 codes:
+ * WPK [out x fcount] f32 of bitlinear-packed / -v (kernels.el:992-1040),
+ * pk codes per value (1..16).  A weight the 2-bit code cannot hold (an int8
+ * lane outside [-2, 1], a base-4 code 3) is written as 0 and added to the
+ * device counter *nbad (may be NULL).  One launch each, no host sync. */
+int nlg_repack_i8_to_2bit(const uint32_t *wp, uint32_t out, uint32_t cols, uint32_t *w2, uint32_t *nbad,
+                          void *stream);
+int nlg_repack_packed_to_2bit(const float *wpk, uint32_t out, uint32_t cols, uint32_t pk, uint32_t fcount,
+                              uint32_t *w2, uint32_t *nbad, void *stream);
+
 /* Synthetic data: n floats of sigma * N(0,1) from a counter-based
  * SplitMix64 stream (element 2p, 2p+1 = Box-Muller pair p); causal > 0 treats
  * the data as [.. x causal x causal] score tiles and writes -inf above each

@@ -104,6 +104,8 @@ def lib() -> C.CDLL:
         "nlg_attn_ternary_linear_residual": (i32, [vp, sz, u32, u32, u32, u32, u32, vp, vp, vp, i32, vp,
                                                    vp, u32, vp]),
         "nlg_prefill_attn_f16": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp, vp]),
+        "nlg_repack_i8_to_2bit": (i32, [vp, u32, u32, vp, vp, vp]),
+        "nlg_repack_packed_to_2bit": (i32, [vp, u32, u32, u32, u32, vp, vp, vp]),
         "nlg_fill_normal": (i32, [vp, C.c_uint64, C.c_uint64, C.c_float, u32, vp]),
         "nlg_stack_create": (i32, [C.POINTER(StackConfig), C.POINTER(vp)]),
         "nlg_stack_destroy": (None, [vp]),
@@ -341,6 +343,17 @@ def prefill_attn_f16(q, kc, vc, pos, rows, qper, heads, kvheads, head_dim, max_s
     position pos[0] + r % qper) over fp16 caches; ctx [rows][heads*head_dim]."""
     _check(lib().nlg_prefill_attn_f16(q.ptr, kc.ptr, vc.ptr, pos.ptr, rows, qper, heads, kvheads, head_dim,
                                       max_seq, ctx.ptr, stream), "prefill_attn_f16")
+
+
+def repack_i8_to_2bit(wp, out, cols, w2, nbad=None, stream=None) -> None:
+    """int8-lane ternary words [out x ceil(cols/4)] -> 2-bit words [out x ceil(cols/16)]."""
+    _check(lib().nlg_repack_i8_to_2bit(wp.ptr, out, cols, w2.ptr, _ptr(nbad), stream), "repack_i8_to_2bit")
+
+
+def repack_packed_to_2bit(wpk, out, cols, pk, fcount, w2, nbad=None, stream=None) -> None:
+    """base-4 codes in f32 [out x fcount] -> 2-bit words [out x ceil(cols/16)]."""
+    _check(lib().nlg_repack_packed_to_2bit(wpk.ptr, out, cols, pk, fcount, w2.ptr, _ptr(nbad), stream),
+           "repack_packed_to_2bit")
 
 
 def attn_ternary_linear_residual(workspace, batch, heads, kvheads, head_dim, max_seq, w2, bias, beta,

@@ -831,3 +831,49 @@ void or_set_threads(int n) {
   (void)n;
 #endif
 }
+
+/* ---------------------------------------------------------- weight ingest */
+
+/* Set column `col`'s 2-bit field in a zeroed [out x wng] buffer. */
+static inline void put2(uint32_t *w2row, uint32_t col, int32_t v) {
+  w2row[col / 16u] |= ((uint32_t)v & 3u) << (2u * (col % 16u));
+}
+
+/* int8 lanes -> 2-bit: column i is lane i%4 of word i/4 (kernels.el:619-653,
+ * OpSDot's byte order), the field its value's low two bits when it lies in
+ * [-2, 1] (the values ternary-rows' sign extension produces, kernels.el:728-743). */
+uint32_t or_repack_i8_2bit(const uint32_t *wp, uint32_t out, uint32_t cols, uint32_t *w2) {
+  const uint32_t ng = (cols + 3u) / 4u, wng = (cols + 15u) / 16u;
+  uint32_t bad = 0;
+  memset(w2, 0, (size_t)out * wng * 4);
+  for (uint32_t o = 0; o < out; o++)
+    for (uint32_t i = 0; i < cols; i++) {
+      int32_t v = (int32_t)(int8_t)(wp[(size_t)o * ng + i / 4u] >> (8u * (i % 4u)));
+      if (v < -2 || v > 1) bad++;
+      else put2(w2 + (size_t)o * wng, i, v);
+    }
+  return bad;
+}
+
+/* base-4 codes -> 2-bit, peeling codes as bitlinear-packed does
+ * (kernels.el:1002-1013: code = packed % 4, then packed = packed / 4). */
+uint32_t or_repack_packed_2bit(const float *wpk, uint32_t out, uint32_t cols, uint32_t pk, uint32_t fcount,
+                               uint32_t *w2) {
+  const uint32_t wng = (cols + 15u) / 16u;
+  uint32_t bad = 0;
+  memset(w2, 0, (size_t)out * wng * 4);
+  for (uint32_t o = 0; o < out; o++)
+    for (uint32_t f = 0; f < fcount; f++) {
+      uint32_t packed = f2u(wpk[(size_t)o * fcount + f]);
+      for (uint32_t z = 0; z < pk; z++) {
+        uint32_t i = f * pk + z;
+        if (i < cols) {
+          uint32_t code = packed % 4u;
+          if (code == 3u) bad++;
+          else put2(w2 + (size_t)o * wng, i, (int32_t)code - 1);
+        }
+        packed = packed / 4u;
+      }
+    }
+  return bad;
+}

@@ -57,6 +57,18 @@ void or_decode_attn_f16(const float *q, const uint16_t *kc, const uint16_t *vc, 
                         float *out, uint32_t B, uint32_t heads, uint32_t kvheads, uint32_t hd,
                         uint32_t max_seq);
 
+/* Weight ingest into the 2-bit layout of ternary-rows (kernels.el:700-746:
+ * field f of word w = column 16w+f, bits 2f..2f+1, sign-extended).
+ * From int8 lanes (bitlinear-dp4a-1f/-rows WP, kernels.el:619-653: lane l of
+ * word g = column 4g+l, signed byte): lanes outside [-2, 1] become 0 and are
+ * counted.  From base-4 codes in f32 values (bitlinear-packed(-v),
+ * kernels.el:992-1040: packed = (uint WPK[o*fcount+f]), column f*pk+z has
+ * code (packed/4^z)%4, weight code-1; no weight past fcount*pk): code 3
+ * becomes 0 and is counted.  Return: the count. */
+uint32_t or_repack_i8_2bit(const uint32_t *wp, uint32_t out, uint32_t cols, uint32_t *w2);
+uint32_t or_repack_packed_2bit(const float *wpk, uint32_t out, uint32_t cols, uint32_t pk, uint32_t fcount,
+                               uint32_t *w2);
+
 /* Number of OpenMP threads the parallel loops use (1 when built without
  * OpenMP); set_threads(0) keeps the runtime default. */
 int or_threads(void);

@@ -47,6 +47,10 @@ def lib() -> C.CDLL:
         L.or_rmsnorm_rows.argtypes = [vp, vp, C.c_float, vp, u32, u32]
         L.or_decode_attn_f16.restype = None
         L.or_decode_attn_f16.argtypes = [vp, vp, vp, u32, vp, u32, u32, u32, u32, u32]
+        L.or_repack_i8_2bit.restype = u32
+        L.or_repack_i8_2bit.argtypes = [vp, u32, u32, vp]
+        L.or_repack_packed_2bit.restype = u32
+        L.or_repack_packed_2bit.argtypes = [vp, u32, u32, u32, u32, vp]
         L.or_threads.restype = i32
         L.or_set_threads.argtypes = [i32]
         _lib = L
@@ -135,6 +139,20 @@ def decode_attn_f16(q, kc, vc, pos, B, heads, kvheads, hd, max_seq) -> np.ndarra
                              _p(np.ascontiguousarray(vc, np.uint16)), int(pos), _p(out), B, heads,
                              kvheads, hd, max_seq)
     return out
+
+
+def repack_i8_2bit(wp, out, cols):
+    """int8-lane words [out x ceil(cols/4)] -> (2-bit words [out x ceil(cols/16)], count unrepresentable)."""
+    w2 = np.empty((out, (cols + 15) // 16), np.uint32)
+    bad = lib().or_repack_i8_2bit(_p(np.ascontiguousarray(wp, np.uint32)), out, cols, _p(w2))
+    return w2, int(bad)
+
+
+def repack_packed_2bit(wpk, out, cols, pk, fcount):
+    """base-4 codes in f32 [out x fcount] -> (2-bit words, count of code 3)."""
+    w2 = np.empty((out, (cols + 15) // 16), np.uint32)
+    bad = lib().or_repack_packed_2bit(_p(np.ascontiguousarray(wpk, np.float32)), out, cols, pk, fcount, _p(w2))
+    return w2, int(bad)
 
 
 def threads() -> int:
