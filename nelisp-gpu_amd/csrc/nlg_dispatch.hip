@@ -55,6 +55,16 @@ static const KEntry kTable[] = {
     {"silu", 2, 1, L_silu},                             // :1306
     {"mul", 3, 1, L_mul},                               // :1322
     {"embed-gather", 3, 2, L_embed_gather},             // :1385
+    // long-context decode (StreamingLLM ring, paged KV)
+    {"cache-append-ring", 3, 3, L_cache_append_ring},   // :396
+    {"decode-attn-stream", 7, 5, L_decode_attn_stream}, // :409
+    {"attn-stream-entries", 7, 5, L_attn_stream_entries}, // :1056
+    {"cache-append-paged", 4, 4, L_cache_append_paged}, // :1099
+    {"decode-attn-paged", 6, 6, L_decode_attn_paged},   // :1112
+    {"block-copy", 1, 4, L_block_copy},                 // :1184
+    {"decode-rope-b-v", 6, 3, L_decode_rope_b_v},       // :1197
+    {"cache-append-paged-v", 4, 4, L_cache_append_paged_v}, // :1212
+    {"decode-attn-paged-v", 6, 6, L_decode_attn_paged_v},   // :1224
     // extension, no reference counterpart: 2-bit weights x pack-act-rows
     // activations, int32 accumulation (see nlg_ternary_linear_i8)
     {"ternary-i8", 6, 3, L_ternary_i8},

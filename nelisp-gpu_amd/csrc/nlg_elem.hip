@@ -110,6 +110,39 @@ __device__ void b_qkv_append(const EArgs &a, uint32_t idx) {
     rst(A(2), wbase + idx, rld(A(0), dim + (kvdim + idx)));
   }
 }
+// cache-append-ring (:396-403): SRC POS CACHE; push (kvdim nsink win).
+// Stream position pos lives in slot pos (a sink) or nsink + (pos-nsink) % win.
+__device__ void b_cache_append_ring(const EArgs &a, uint32_t idx) {
+  const uint32_t kvdim = P(0), nsink = P(1), win = P(2);
+  if (idx < kvdim) {
+    const uint32_t pos = nlg_f2u(rld(A(1), 0));
+    uint32_t slot = pos;
+    if (pos >= nsink) slot = nsink + umod(pos - nsink, win);
+    rst(A(2), slot * kvdim + idx, rld(A(0), idx));
+  }
+}
+// cache-append-paged (:1099-1108) / -v (:1211-1220): SRC POS|LENS TABLE POOL;
+// push (B kvdim bs mbps).  Row s goes to block TABLE[s*mbps + pos/bs],
+// offset pos % bs, at the shared POS[0] or at its own LENS[s].
+template <bool PER_SEQ>
+__device__ void b_cache_append_paged(const EArgs &a, uint32_t idx) {
+  const uint32_t B = P(0), kvdim = P(1), bs = P(2), mbps = P(3);
+  if (idx < B * kvdim) {
+    const uint32_t s = udiv(idx, kvdim), t = umod(idx, kvdim);
+    const uint32_t pos = nlg_f2u(rld(A(1), PER_SEQ ? s : 0u));
+    const uint32_t lb = udiv(pos, bs), off = umod(pos, bs);
+    const uint32_t phys = nlg_f2u(rld(A(2), s * mbps + lb));
+    rst(A(3), (phys * bs + off) * kvdim + t, rld(A(0), idx));
+  }
+}
+// block-copy (:1182-1189): POOL; push (bs kvdim src dst) -- block src to
+// block dst of the same pool (distinct blocks never overlap; src == dst
+// rewrites each element with itself).
+__device__ void b_block_copy(const EArgs &a, uint32_t i) {
+  const uint32_t bs = P(0), kvdim = P(1), src = P(2), dst = P(3);
+  const uint32_t bn = bs * kvdim;
+  if (i < bn) rst(A(0), dst * bn + i, rld(A(0), src * bn + i));
+}
 // The rotation shared by the table-driven RoPE kernels.
 __device__ __forceinline__ void rot_pair(const EArgs &a, int ix, int ic, int is, int isg, int ic_out,
                                          uint32_t ci, uint32_t i0, uint32_t i1) {
@@ -137,6 +170,19 @@ __device__ void b_decode_rope_b(const EArgs &a, uint32_t idx) {
     const uint32_t bb = udiv(idx, rh), rem = umod(idx, rh);
     const uint32_t m = umod(rem, half), h = udiv(rem, half);
     const uint32_t pos = nlg_f2u(rld(A(4), 0)), ci = pos * half + m;
+    const uint32_t i0 = (bb * cols + h * hd) + 2 * m;
+    rot_pair(a, 0, 1, 2, 3, 5, ci, i0, i0 + 1);
+  }
+}
+// decode-rope-b-v (:1195-1209): X CO SI SG LENS C; push (B cols heads) --
+// decode-rope-b with row bb rotated at its own position LENS[bb]
+__device__ void b_decode_rope_b_v(const EArgs &a, uint32_t idx) {
+  const uint32_t B = P(0), cols = P(1), heads = P(2);
+  const uint32_t hd = udiv(cols, heads), half = udiv(hd, 2), rh = heads * half;
+  if (idx < B * rh) {
+    const uint32_t bb = udiv(idx, rh), rem = umod(idx, rh);
+    const uint32_t m = umod(rem, half), h = udiv(rem, half);
+    const uint32_t pos = nlg_f2u(rld(A(4), bb)), ci = pos * half + m;
     const uint32_t i0 = (bb * cols + h * hd) + 2 * m;
     rot_pair(a, 0, 1, 2, 3, 5, ci, i0, i0 + 1);
   }
@@ -214,4 +260,9 @@ E(L_qkv_append, b_qkv_append, 3, 3, p[1])
 E(L_decode_rope, b_decode_rope, 6, 2, (p[1] * ((p[1] ? p[0] / p[1] : 0u) / 2u)))
 E(L_decode_rope_b, b_decode_rope_b, 6, 3, p[0] * (p[2] * ((p[2] ? p[1] / p[2] : 0u) / 2u)))
 E(L_rope_apply, b_rope_apply, 5, 3, (p[0] * p[2]) * ((p[2] ? p[1] / p[2] : 0u) / 2u))
+E(L_decode_rope_b_v, b_decode_rope_b_v, 6, 3, p[0] * (p[2] * ((p[2] ? p[1] / p[2] : 0u) / 2u)))
+E(L_cache_append_ring, b_cache_append_ring, 3, 3, p[0])
+E(L_cache_append_paged, b_cache_append_paged<false>, 4, 4, p[0] * p[1])
+E(L_cache_append_paged_v, b_cache_append_paged<true>, 4, 4, p[0] * p[1])
+E(L_block_copy, b_block_copy, 1, 4, p[0] * p[1])
 E(L_rope_half, b_rope_half, 2, 5, (p[0] * p[1]) * (p[2] / 2u))

@@ -266,3 +266,12 @@ NLG_DECL(L_decode_attn);
 NLG_DECL(L_decode_attn_b);
 NLG_DECL(L_attn_causal_gqa);
 NLG_DECL(L_ternary_i8);
+NLG_DECL(L_decode_rope_b_v);
+NLG_DECL(L_cache_append_ring);
+NLG_DECL(L_cache_append_paged);
+NLG_DECL(L_cache_append_paged_v);
+NLG_DECL(L_block_copy);
+NLG_DECL(L_decode_attn_stream);
+NLG_DECL(L_attn_stream_entries);
+NLG_DECL(L_decode_attn_paged);
+NLG_DECL(L_decode_attn_paged_v);

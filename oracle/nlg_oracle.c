@@ -594,6 +594,165 @@ static void kn_attn_causal_gqa(const K *k, uint32_t idx) {
   }
 }
 
+/* ---- long-context decode ---------------------------------------------- */
+
+/* cache-append-ring, kernels.el:396-403 */
+static void kn_cache_append_ring(const K *k, uint32_t idx) {
+  uint32_t kvdim = P(0), nsink = P(1), win = P(2);
+  if (idx < kvdim) {
+    uint32_t pos = f2u(ld(k, 1, 0));
+    uint32_t slot = pos;
+    if (pos >= nsink) slot = nsink + umod(pos - nsink, win);
+    st(k, 2, slot * kvdim + idx, ld(k, 0, idx));
+  }
+}
+/* The q.k product of decode-attn-stream / attn-stream-entries: K row kb
+ * rotated by cache-relative position crel, q by qcrel, pairs (2m, 2m+1)
+ * (kernels.el:425-433, :1069-1077). */
+static float stream_dot(const K *k, uint32_t kb, uint32_t crel, uint32_t qcrel, uint32_t c0q, uint32_t half) {
+  float acc = 0.0f;
+  for (uint32_t m = 0; m < half; m++) {
+    uint32_t ci = crel * half + m;
+    float cc = ld(k, 4, ci), ss = ld(k, 5, ci);
+    float k0 = ld(k, 1, kb + 2 * m), k1 = ld(k, 1, kb + (2 * m + 1));
+    float kr0 = (k0 * cc) - (k1 * ss), kr1 = (k0 * ss) + (k1 * cc);
+    uint32_t qci = qcrel * half + m;
+    float qcc = ld(k, 4, qci), qss = ld(k, 5, qci);
+    float q0 = ld(k, 0, c0q + 2 * m), q1 = ld(k, 0, c0q + (2 * m + 1));
+    float qr0 = (q0 * qcc) - (q1 * qss), qr1 = (q0 * qss) + (q1 * qcc);
+    acc = acc + ((qr0 * kr0) + (qr1 * kr1));
+  }
+  return acc;
+}
+/* decode-attn-stream, kernels.el:404-451: Q CK CV POS CO SI C; push (dim heads kvheads nsink win) */
+static void kn_decode_attn_stream(const K *k, uint32_t idx) {
+  uint32_t dim = P(0), heads = P(1), kvheads = P(2), nsink = P(3), win = P(4);
+  uint32_t hd = udiv(dim, heads), grp = udiv(heads, kvheads), kvdim = kvheads * hd, half = udiv(hd, 2);
+  if (idx < dim) {
+    uint32_t h = udiv(idx, hd), t = umod(idx, hd), kvh = udiv(h, grp);
+    uint32_t pos = f2u(ld(k, 3, 0)), cap = nsink + win;
+    uint32_t len = pos + 1;
+    if (len > cap) len = cap;
+    uint32_t start = nsink;
+    if (pos >= cap) start = (pos - win) + 1;
+    uint32_t woff = umod(start - nsink, win);
+    uint32_t qcrel = pos;
+    if (qcrel >= cap) qcrel = cap - 1;
+    uint32_t c0q = h * hd;
+    float coef = 1.0f / sqrtf((float)hd), mx = NEG_BIG;
+    for (uint32_t r = 0; r < len; r++) {
+      uint32_t slot = r;
+      if (r >= nsink) slot = nsink + umod(woff + (r - nsink), win);
+      uint32_t kb = slot * kvdim + kvh * hd;
+      float s = stream_dot(k, kb, r, qcrel, c0q, half) * coef;
+      if (s > mx) mx = s;
+    }
+    float z = 0.0f, ctx = 0.0f;
+    for (uint32_t r = 0; r < len; r++) {
+      uint32_t slot = r;
+      if (r >= nsink) slot = nsink + umod(woff + (r - nsink), win);
+      uint32_t kb = slot * kvdim + kvh * hd;
+      float e = expf(stream_dot(k, kb, r, qcrel, c0q, half) * coef - mx);
+      z = z + e;
+      ctx = ctx + e * ld(k, 2, slot * kvdim + (kvh * hd + t));
+    }
+    st(k, 6, idx, ctx / z);
+  }
+}
+/* attn-stream-entries, kernels.el:1050-1090: Q CK CV ENT CO SI C; push (dim heads kvheads ne qcrel) */
+static void kn_attn_stream_entries(const K *k, uint32_t idx) {
+  uint32_t dim = P(0), heads = P(1), kvheads = P(2), ne = P(3), qcrel = P(4);
+  uint32_t hd = udiv(dim, heads), grp = udiv(heads, kvheads), half = udiv(hd, 2);
+  if (idx < dim) {
+    uint32_t h = udiv(idx, hd), t = umod(idx, hd), kvh = udiv(h, grp);
+    uint32_t c0q = h * hd;
+    float coef = 1.0f / sqrtf((float)hd), mx = NEG_BIG;
+    for (uint32_t r = 0; r < ne; r++) {
+      uint32_t base = f2u(ld(k, 3, 2 * r)), crel = f2u(ld(k, 3, 2 * r + 1));
+      float s = stream_dot(k, base + kvh * hd, crel, qcrel, c0q, half) * coef;
+      if (s > mx) mx = s;
+    }
+    float z = 0.0f, ctx = 0.0f;
+    for (uint32_t r = 0; r < ne; r++) {
+      uint32_t base = f2u(ld(k, 3, 2 * r)), crel = f2u(ld(k, 3, 2 * r + 1));
+      float e = expf(stream_dot(k, base + kvh * hd, crel, qcrel, c0q, half) * coef - mx);
+      z = z + e;
+      ctx = ctx + e * ld(k, 2, base + (kvh * hd + t));
+    }
+    st(k, 6, idx, ctx / z);
+  }
+}
+/* cache-append-paged, kernels.el:1099-1108 (per_seq 0, position POS[0]) and
+ * cache-append-paged-v, :1211-1220 (per_seq 1, position LENS[s]) */
+static void cache_append_paged(const K *k, uint32_t idx, int per_seq) {
+  uint32_t B = P(0), kvdim = P(1), bs = P(2), mbps = P(3);
+  if (idx < B * kvdim) {
+    uint32_t s = udiv(idx, kvdim), t = umod(idx, kvdim);
+    uint32_t pos = f2u(ld(k, 1, per_seq ? s : 0u));
+    uint32_t lb = udiv(pos, bs), off = umod(pos, bs);
+    uint32_t phys = f2u(ld(k, 2, s * mbps + lb));
+    st(k, 3, (phys * bs + off) * kvdim + t, ld(k, 0, idx));
+  }
+}
+static void kn_cache_append_paged(const K *k, uint32_t idx) { cache_append_paged(k, idx, 0); }
+static void kn_cache_append_paged_v(const K *k, uint32_t idx) { cache_append_paged(k, idx, 1); }
+/* decode-attn-paged, kernels.el:1110-1136 (per_seq 0) and decode-attn-paged-v,
+ * :1222-1246 (per_seq 1): Q CK CV POS|LENS TABLE C; push (B dim heads kvheads bs mbps) */
+static void decode_attn_paged(const K *k, uint32_t idx, int per_seq) {
+  uint32_t B = P(0), dim = P(1), heads = P(2), kvheads = P(3), bs = P(4), mbps = P(5);
+  uint32_t hd = udiv(dim, heads), grp = udiv(heads, kvheads), kvdim = kvheads * hd;
+  if (idx < B * dim) {
+    uint32_t s = udiv(idx, dim), c = umod(idx, dim);
+    uint32_t h = udiv(c, hd), t = umod(c, hd), kvh = udiv(h, grp);
+    uint32_t pos = f2u(ld(k, 3, per_seq ? s : 0u)), len = pos + 1;
+    uint32_t c0q = s * dim + h * hd;
+    float coef = 1.0f / sqrtf((float)hd), mx = NEG_BIG;
+    for (uint32_t j = 0; j < len; j++) {
+      uint32_t lb = udiv(j, bs), off = umod(j, bs);
+      uint32_t phys = f2u(ld(k, 4, s * mbps + lb));
+      uint32_t kb = (phys * bs + off) * kvdim + kvh * hd;
+      float acc = 0.0f;
+      for (uint32_t tt = 0; tt < hd; tt++) acc = acc + ld(k, 0, c0q + tt) * ld(k, 1, kb + tt);
+      float sc = acc * coef;
+      if (sc > mx) mx = sc;
+    }
+    float z = 0.0f, ctx = 0.0f;
+    for (uint32_t j = 0; j < len; j++) {
+      uint32_t lb = udiv(j, bs), off = umod(j, bs);
+      uint32_t phys = f2u(ld(k, 4, s * mbps + lb));
+      uint32_t kb = (phys * bs + off) * kvdim + kvh * hd;
+      float acc = 0.0f;
+      for (uint32_t tt = 0; tt < hd; tt++) acc = acc + ld(k, 0, c0q + tt) * ld(k, 1, kb + tt);
+      float e = expf(acc * coef - mx);
+      z = z + e;
+      ctx = ctx + e * ld(k, 2, kb + t);
+    }
+    st(k, 5, idx, ctx / z);
+  }
+}
+static void kn_decode_attn_paged(const K *k, uint32_t idx) { decode_attn_paged(k, idx, 0); }
+static void kn_decode_attn_paged_v(const K *k, uint32_t idx) { decode_attn_paged(k, idx, 1); }
+/* block-copy, kernels.el:1182-1189: POOL; push (bs kvdim src dst) */
+static void kn_block_copy(const K *k, uint32_t i) {
+  uint32_t bs = P(0), kvdim = P(1), src = P(2), dst = P(3), bn = bs * kvdim;
+  if (i < bn) st(k, 0, dst * bn + i, ld(k, 0, src * bn + i));
+}
+/* decode-rope-b-v, kernels.el:1195-1209: decode-rope-b with row bb at LENS[bb] */
+static void kn_decode_rope_b_v(const K *k, uint32_t idx) {
+  uint32_t B = P(0), cols = P(1), heads = P(2);
+  uint32_t hd = udiv(cols, heads), half = udiv(hd, 2), rh = heads * half;
+  if (idx < B * rh) {
+    uint32_t bb = udiv(idx, rh), rem = umod(idx, rh);
+    uint32_t m = umod(rem, half), h = udiv(rem, half);
+    uint32_t pos = f2u(ld(k, 4, bb)), ci = pos * half + m;
+    float cc = ld(k, 1, ci), ss = ld(k, 2, ci) * ld(k, 3, 0);
+    uint32_t b0 = bb * cols + h * hd, i0 = b0 + 2 * m, i1 = i0 + 1;
+    float a0 = ld(k, 0, i0), a1 = ld(k, 0, i1);
+    st(k, 5, i0, (a0 * cc) - (a1 * ss));
+    st(k, 5, i1, (a0 * ss) + (a1 * cc));
+  }
+}
+
 /* ---- the table -------------------------------------------------------- */
 
 typedef void (*kfn)(const K *, uint32_t);
@@ -641,6 +800,15 @@ static const entry TABLE[] = {
     {"silu", 2, 1, 64, kn_silu},
     {"mul", 3, 1, 64, kn_mul},
     {"embed-gather", 3, 2, 64, kn_embed_gather},
+    {"cache-append-ring", 3, 3, 64, kn_cache_append_ring},
+    {"decode-attn-stream", 7, 5, 64, kn_decode_attn_stream},
+    {"attn-stream-entries", 7, 5, 64, kn_attn_stream_entries},
+    {"cache-append-paged", 4, 4, 64, kn_cache_append_paged},
+    {"decode-attn-paged", 6, 6, 64, kn_decode_attn_paged},
+    {"block-copy", 1, 4, 64, kn_block_copy},
+    {"decode-rope-b-v", 6, 3, 64, kn_decode_rope_b_v},
+    {"cache-append-paged-v", 4, 4, 64, kn_cache_append_paged_v},
+    {"decode-attn-paged-v", 6, 6, 64, kn_decode_attn_paged_v},
 };
 #define NTABLE ((int)(sizeof TABLE / sizeof TABLE[0]))
 

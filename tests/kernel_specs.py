@@ -176,6 +176,43 @@ def cases(seed: int = 1234) -> list[Case]:
     cs.append(Case("attn-causal-gqa", [_f(rng, seq * heads * hd), _f(rng, seq * kvh * hd),
                                        _f(rng, seq * kvh * hd), _z(seq * heads * hd)], [seq, heads, kvh, hd],
                    g64(heads * seq), 1e-5))
+    # long-context decode: StreamingLLM ring (nsink 2 + win 6 slots) and a
+    # paged pool (blocks of 4 positions, 5 blocks per sequence)
+    kvd, nsink, win = 32, 2, 6
+    for pos in (4.0, 13.0):  # inside the first window; wrapped around it
+        cs.append(Case("cache-append-ring", [_f(rng, kvd), np.array([pos], np.float32),
+                                            _f(rng, (nsink + win) * kvd)], [kvd, nsink, win], g64(kvd),
+                       label=f"pos={int(pos)}"))
+    dim, heads, kvh = 256, 4, 2  # hd 64
+    co, si = tables(32, 32)
+    for pos in (5.0, 20.0):  # before and after the window fills
+        cs.append(Case("decode-attn-stream", [_f(rng, dim), _f(rng, (nsink + win) * kvh * 64),
+                                             _f(rng, (nsink + win) * kvh * 64), np.array([pos], np.float32), co,
+                                             si, _z(dim)], [dim, heads, kvh, nsink, win], g64(dim), 1e-5,
+                       label=f"pos={int(pos)}"))
+    ne, qcrel = 7, 9
+    ent = np.array([[(r * 3 % 10) * kvh * 64, r + 2] for r in range(ne)], np.float32).ravel()
+    cs.append(Case("attn-stream-entries", [_f(rng, dim), _f(rng, 10 * kvh * 64), _f(rng, 10 * kvh * 64), ent, co,
+                                          si, _z(dim)], [dim, heads, kvh, ne, qcrel], g64(dim), 1e-5))
+    B, kvd, bs, mbps, nblk = 3, 32, 4, 5, 16
+    table = rng.permutation(nblk)[:B * mbps].astype(np.float32)
+    cs.append(Case("cache-append-paged", [_f(rng, B * kvd), np.array([9.0], np.float32), table,
+                                         _f(rng, nblk * bs * kvd)], [B, kvd, bs, mbps], g64(B * kvd)))
+    lens = np.array([3.0, 17.0, 10.0], np.float32)
+    cs.append(Case("cache-append-paged-v", [_f(rng, B * kvd), lens, table, _f(rng, nblk * bs * kvd)],
+                   [B, kvd, bs, mbps], g64(B * kvd)))
+    B, dim, heads, kvh = 3, 256, 4, 2  # hd 64, kvdim 128
+    pool = nblk * bs * kvh * 64
+    cs.append(Case("decode-attn-paged", [_f(rng, B * dim), _f(rng, pool), _f(rng, pool), np.array([13.0], np.float32),
+                                        table, _z(B * dim)], [B, dim, heads, kvh, bs, mbps], g64(B * dim), 1e-5))
+    cs.append(Case("decode-attn-paged-v", [_f(rng, B * dim), _f(rng, pool), _f(rng, pool), lens, table,
+                                          _z(B * dim)], [B, dim, heads, kvh, bs, mbps], g64(B * dim), 1e-5))
+    cs.append(Case("block-copy", [_f(rng, nblk * bs * kvd)], [bs, kvd, 3, 11], g64(bs * kvd)))
+    B, cols, heads = 3, 192, 3  # hd 64
+    co, si = tables(24, 32)
+    cs.append(Case("decode-rope-b-v", [_f(rng, B * cols), co, si, np.array([1.0], np.float32),
+                                       np.array([2.0, 17.0, 9.0], np.float32), _z(B * cols)], [B, cols, heads],
+                   g64(B * heads * 32)))
     return cs
 
 

@@ -91,8 +91,12 @@ def ref(case):
         ck[wbase:wbase + kvdim] = b[0][dim:dim + kvdim]
         cv[wbase:wbase + kvdim] = b[0][dim + kvdim:dim + 2 * kvdim]
         return {1: ck, 2: cv}
-    if nm in ("decode-rope", "decode-rope-b", "rope-apply"):
-        if nm == "decode-rope":
+    if nm in ("decode-rope", "decode-rope-b", "decode-rope-b-v", "rope-apply"):
+        if nm == "decode-rope-b-v":
+            B, cols, heads = p
+            rows, dim = B, cols
+            pos = b[4][:B].astype(np.int64)
+        elif nm == "decode-rope":
             cols, heads = p
             rows, pos = 1, np.array([int(b[4][0])])
             dim = cols
@@ -228,6 +232,82 @@ def ref(case):
         w = e / e.sum(axis=2, keepdims=True)
         del ms
         return {4: np.einsum("bhj,bjhd->bhd", w, cv).ravel()}
+    if nm == "cache-append-ring":
+        kvdim, nsink, win = p
+        pos = int(b[1][0])
+        slot = pos if pos < nsink else nsink + (pos - nsink) % win
+        c = b[2].copy()
+        c[slot * kvdim:(slot + 1) * kvdim] = b[0][:kvdim]
+        return {2: c}
+    if nm in ("cache-append-paged", "cache-append-paged-v"):
+        B, kvdim, bs, mbps = p
+        pool = b[3].copy()
+        for s_ in range(B):
+            pos = int(b[1][s_ if nm.endswith("-v") else 0])
+            phys = int(b[2][s_ * mbps + pos // bs])
+            row = phys * bs + pos % bs
+            pool[row * kvdim:(row + 1) * kvdim] = b[0][s_ * kvdim:(s_ + 1) * kvdim]
+        return {3: pool}
+    if nm == "block-copy":
+        bs, kvdim, src, dst = p
+        bn = bs * kvdim
+        pool = b[0].copy()
+        pool[dst * bn:(dst + 1) * bn] = b[0][src * bn:(src + 1) * bn]
+        return {0: pool}
+    if nm in ("decode-attn-stream", "attn-stream-entries"):
+        dim, heads, kvh = p[:3]
+        hd, grp = dim // heads, heads // kvh
+        half, kvdim = hd // 2, kvh * hd
+        if nm == "decode-attn-stream":
+            nsink, win = p[3], p[4]
+            pos, cap = int(b[3][0]), nsink + win
+            n = min(pos + 1, cap)
+            start = nsink if pos < cap else pos - win + 1
+            woff = (start - nsink) % win
+            slots = [r if r < nsink else nsink + (woff + r - nsink) % win for r in range(n)]
+            rows = [(sl * kvdim, r) for r, sl in enumerate(slots)]
+            qcrel = min(pos, cap - 1)
+        else:
+            ne, qcrel = p[3], p[4]
+            rows = [(int(b[3][2 * r]), int(b[3][2 * r + 1])) for r in range(ne)]
+        co = b[4].reshape(-1, half).astype(np.float64)
+        si = b[5].reshape(-1, half).astype(np.float64)
+
+        def rot(v, c):  # v [..., hd] pairs (2m, 2m+1) rotated by angle row c
+            v0, v1 = v[..., 0:2 * half:2], v[..., 1:2 * half:2]
+            return v0 * co[c] - v1 * si[c], v0 * si[c] + v1 * co[c]
+        q = b[0].reshape(heads, hd).astype(np.float64)
+        qr0, qr1 = rot(q, qcrel)
+        outp = np.zeros((heads, hd))
+        for h in range(heads):
+            kvo = (h // grp) * hd
+            sc = []
+            for base, crel in rows:
+                k = b[1][base + kvo: base + kvo + hd].astype(np.float64)
+                k0, k1 = rot(k, crel)
+                sc.append((qr0[h] * k0 + qr1[h] * k1).sum() / np.sqrt(hd))
+            sc = np.array(sc)
+            e = np.exp(sc - sc.max())
+            vv = np.array([b[2][base + kvo: base + kvo + hd] for base, _ in rows], np.float64)
+            outp[h] = (e[:, None] * vv).sum(axis=0) / e.sum()
+        return {6: outp.ravel()}
+    if nm in ("decode-attn-paged", "decode-attn-paged-v"):
+        B, dim, heads, kvh, bs, mbps = p
+        hd, grp = dim // heads, heads // kvh
+        kvdim = kvh * hd
+        outp = np.zeros((B, heads, hd))
+        for s_ in range(B):
+            n = int(b[3][s_ if nm.endswith("-v") else 0]) + 1
+            rows = [(int(b[4][s_ * mbps + j // bs]) * bs + j % bs) * kvdim for j in range(n)]
+            for h in range(heads):
+                kvo = (h // grp) * hd
+                q = b[0][s_ * dim + h * hd: s_ * dim + (h + 1) * hd].astype(np.float64)
+                K = np.array([b[1][r + kvo: r + kvo + hd] for r in rows], np.float64)
+                V = np.array([b[2][r + kvo: r + kvo + hd] for r in rows], np.float64)
+                sc = K @ q / np.sqrt(hd)
+                e = np.exp(sc - sc.max())
+                outp[s_, h] = (e[:, None] * V).sum(axis=0) / e.sum()
+        return {5: outp.ravel()}
     if nm == "attn-causal-gqa":
         seq, heads, kvh, hd = p
         grp = heads // kvh

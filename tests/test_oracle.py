@@ -23,12 +23,14 @@ import np_ref
 EXACT_PIN = {"vadd", "add2", "mul", "scale", "causal-mask", "rmsnorm-fwd", "embed-gather",
              "cache-append", "cache-append-b", "qkv-append", "decode-rope", "decode-rope-b",
              "rope-apply", "pack-act-rows", "quant-act", "dp4a-dot", "bitlinear-dp4a",
-             "bitlinear-dp4a-1f", "bitlinear-dp4a-rows"}
+             "bitlinear-dp4a-1f", "bitlinear-dp4a-rows", "cache-append-ring", "cache-append-paged",
+             "cache-append-paged-v", "block-copy", "decode-rope-b-v"}
 PIN_TOL = {"softmax": ks.ELEM(1e-5), "silu": 1e-6, "silu-mul": 1e-6, "rmsnorm-istd": 1e-5,
            "rmsnorm-heads": 1e-5, "rope-half": 1e-5, "ternary-rows": 1e-5, "bitlinear-packed": 1e-5,
            "bitlinear-packed-v": 1e-5, "matmul": 1e-5, "matmul-tiled": 1e-5, "matmul-reg": 1e-5,
            "linear": 1e-5, "attn-scores": 1e-5, "attn-context": 1e-5, "decode-attn": 1e-5,
-           "decode-attn-b": 1e-5, "attn-causal-gqa": 1e-5}
+           "decode-attn-b": 1e-5, "attn-causal-gqa": 1e-5, "decode-attn-stream": 1e-5,
+           "attn-stream-entries": 1e-5, "decode-attn-paged": 1e-5, "decode-attn-paged-v": 1e-5}
 
 CASES = ks.cases()
 
