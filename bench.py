@@ -161,6 +161,10 @@ class _Ptr:
     def __init__(self, ptr, nbytes):
         self.ptr, self.nbytes = ptr, nbytes
 
+    def as_buffer(self, nfloats=None):
+        import nlgpu
+        return nlgpu.Buffer(self.ptr, self.nbytes // 4 if nfloats is None else int(nfloats))
+
 
 def _tensor(s, name, layer=-1):
     import ctypes as C
@@ -410,6 +414,34 @@ def repack_bench(stream):
     return res
 
 
+def tlinear_bench(stream):
+    """The transposed linear ternary-rows-t (input gradient X = W'(BETA*G)) at
+    the down projection's shape, W [2560 x 6912] 2-bit, one position, 64
+    rotated weight copies; bytes = weights + block scales + G + X."""
+    import nlgpu
+    out, cols, seq, ncp = FFN_D, FFN_F, 1, 64
+    wng, nblk = (cols + 15) // 16, (cols + 127) // 128
+    w = nlgpu.pack_ternary(nlgpu.trits(20260921 + 7, (out, cols)))
+    dw = nlgpu.DeviceArray(w.nbytes * ncp)
+    for c in range(ncp):
+        dw.upload(w, offset=c * w.nbytes)
+    beta = nlgpu.to_device(np.full(out * nblk, 0.05, np.float32))
+    g = nlgpu.to_device(nlgpu.normal(20260921 + 8, seq * out))
+    x = nlgpu.DeviceArray(seq * cols * 4)
+    groups = (seq * cols + 63) // 64
+
+    def fn(i):
+        nlgpu.dispatch("ternary-rows-t", [(_Ptr(dw.ptr + (i % ncp) * w.nbytes, w.nbytes), out * wng),
+                                          (beta, out * nblk), (g, seq * out), (x, seq * cols)],
+                       [out, cols, nblk, wng, seq], groups, stream=stream)
+    us = _per_launch_us(fn, 2 * ncp, stream)
+    nbytes = w.nbytes + out * nblk * 4 + seq * (out + cols) * 4
+    dw.free()
+    return {"us": round(us, 3), "bytes": int(nbytes), "gbs": round(nbytes / us / 1e3, 1),
+            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "shape": [out, cols, seq],
+            "note": "each column summed over the 2560 rows in order (bit-identical to the reference's sum)"}
+
+
 def cpu_baseline(x, w_one, seconds: float):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import nlg_oracle as orc
@@ -526,6 +558,7 @@ def main():
         extra["softmax_config3"] = softmax_bench(stream)
         extra["swiglu_ffn_config4"] = ffn_bench(stream)
         extra["weight_ingest_repack"] = repack_bench(stream)
+        extra["transposed_linear"] = tlinear_bench(stream)
     value = STEP_BYTES / (r["step_ms"] * 1e-3) / 1e9
     gemv_gbs = GEMV_BYTES / (r["gemv_ms"] * 1e-3) / 1e9
     stacked_gbs = GEMV_BYTES * COPIES / (r["stacked_ms"] * 1e-3) / 1e9

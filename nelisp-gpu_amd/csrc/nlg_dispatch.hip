@@ -55,6 +55,9 @@ static const KEntry kTable[] = {
     {"silu", 2, 1, L_silu},                             // :1306
     {"mul", 3, 1, L_mul},                               // :1322
     {"embed-gather", 3, 2, L_embed_gather},             // :1385
+    // transposed linears (input gradients)
+    {"ternary-rows-t", 4, 5, L_ternary_rows_t},         // :750
+    {"dp4a-rows-t", 4, 4, L_dp4a_rows_t},               // :791
     // long-context decode (StreamingLLM ring, paged KV)
     {"cache-append-ring", 3, 3, L_cache_append_ring},   // :396
     {"decode-attn-stream", 7, 5, L_decode_attn_stream}, // :409

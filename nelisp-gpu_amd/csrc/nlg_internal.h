@@ -275,3 +275,5 @@ NLG_DECL(L_decode_attn_stream);
 NLG_DECL(L_attn_stream_entries);
 NLG_DECL(L_decode_attn_paged);
 NLG_DECL(L_decode_attn_paged_v);
+NLG_DECL(L_ternary_rows_t);
+NLG_DECL(L_dp4a_rows_t);

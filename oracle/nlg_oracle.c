@@ -594,6 +594,43 @@ static void kn_attn_causal_gqa(const K *k, uint32_t idx) {
   }
 }
 
+/* ---- transposed linears ------------------------------------------------ */
+
+/* ternary-rows-t, kernels.el:748-775: WP BETA G X; push (out cols nblk wng seq) */
+static void kn_ternary_rows_t(const K *k, uint32_t idx) {
+  uint32_t out = P(0), cols = P(1), nblk = P(2), wng = P(3), seq = P(4);
+  if (idx < seq * cols) {
+    uint32_t p = udiv(idx, cols), i = umod(idx, cols);
+    uint32_t b = i / 128u, wi = i / 16u, fd = i % 16u;
+    uint32_t sh = 30u - 2u * fd, gb = p * out;
+    float acc = 0.0f;
+    for (uint32_t o = 0; o < out; o++) {
+      uint32_t wpk = ldu(k, 0, o * wng + wi);
+      float sv = (float)((int32_t)(wpk << sh) >> 30);
+      acc = acc + sv * (ld(k, 1, o * nblk + b) * ld(k, 2, gb + o));
+    }
+    st(k, 3, idx, acc);
+  }
+}
+/* dp4a-rows-t, kernels.el:777-810: WP BETA G X; push (out cols ng seq) */
+static void kn_dp4a_rows_t(const K *k, uint32_t idx) {
+  uint32_t out = P(0), cols = P(1), ng = P(2), seq = P(3);
+  if (idx < seq * cols) {
+    uint32_t p = udiv(idx, cols), i = umod(idx, cols);
+    uint32_t word = i / 4u, lane = i % 4u, sh = 1u;
+    for (uint32_t l = 0; l < lane; l++) sh = sh * 256u;
+    uint32_t gb = p * out;
+    float acc = 0.0f;
+    for (uint32_t o = 0; o < out; o++) {
+      uint32_t wpk = ldu(k, 0, o * ng + word);
+      uint32_t b = (wpk / sh) % 256u;
+      float sv = (float)((b + 128u) % 256u) - 128.0f;
+      acc = acc + sv * (ld(k, 1, o) * ld(k, 2, gb + o));
+    }
+    st(k, 3, idx, acc);
+  }
+}
+
 /* ---- long-context decode ---------------------------------------------- */
 
 /* cache-append-ring, kernels.el:396-403 */
@@ -800,6 +837,8 @@ static const entry TABLE[] = {
     {"silu", 2, 1, 64, kn_silu},
     {"mul", 3, 1, 64, kn_mul},
     {"embed-gather", 3, 2, 64, kn_embed_gather},
+    {"ternary-rows-t", 4, 5, 64, kn_ternary_rows_t},
+    {"dp4a-rows-t", 4, 4, 64, kn_dp4a_rows_t},
     {"cache-append-ring", 3, 3, 64, kn_cache_append_ring},
     {"decode-attn-stream", 7, 5, 64, kn_decode_attn_stream},
     {"attn-stream-entries", 7, 5, 64, kn_attn_stream_entries},

@@ -176,6 +176,18 @@ def cases(seed: int = 1234) -> list[Case]:
     cs.append(Case("attn-causal-gqa", [_f(rng, seq * heads * hd), _f(rng, seq * kvh * hd),
                                        _f(rng, seq * kvh * hd), _z(seq * heads * hd)], [seq, heads, kvh, hd],
                    g64(heads * seq), 1e-5))
+    # transposed linears: X = W^T (BETA * G), seq positions at once
+    for (out, cols, nblk, seq) in ((40, 300, 3, 2), (7, 256, 2, 1)):
+        wng = (cols + 15) // 16
+        w = _u32_as_f32(rng.integers(0, 2 ** 32, out * wng, dtype=np.uint64))
+        cs.append(Case("ternary-rows-t", [w, np.abs(_f(rng, out * nblk)) * 0.05, _f(rng, seq * out),
+                                          _z(seq * cols)], [out, cols, nblk, wng, seq], g64(seq * cols), 1e-5,
+                       label=f"{out}x{cols}x{seq}"))
+    out, cols, seq = 40, 150, 3
+    ng = (cols + 3) // 4
+    w = _u32_as_f32(rng.integers(0, 2 ** 32, out * ng, dtype=np.uint64))
+    cs.append(Case("dp4a-rows-t", [w, np.abs(_f(rng, out)) * 0.05, _f(rng, seq * out), _z(seq * cols)],
+                   [out, cols, ng, seq], g64(seq * cols), 1e-5))
     # long-context decode: StreamingLLM ring (nsink 2 + win 6 slots) and a
     # paged pool (blocks of 4 positions, 5 blocks per sequence)
     kvd, nsink, win = 32, 2, 6

@@ -232,6 +232,21 @@ def ref(case):
         w = e / e.sum(axis=2, keepdims=True)
         del ms
         return {4: np.einsum("bhj,bjhd->bhd", w, cv).ravel()}
+    if nm in ("ternary-rows-t", "dp4a-rows-t"):
+        if nm == "ternary-rows-t":
+            out, cols, nblk, wng, seq = p
+            w = np.asarray(b[0], f32).view(np.uint32)[:out * wng].reshape(out, wng)
+            f = np.arange(cols)
+            fields = ((w[:, f // 16] >> (2 * (f % 16)).astype(np.uint32)) & 3).astype(np.int64)
+            wt = np.where(fields >= 2, fields - 4, fields).astype(np.float64)  # [out, cols]
+            be = b[1][:out * nblk].reshape(out, nblk)[:, f // 128].astype(np.float64)
+        else:
+            out, cols, ng, seq = p
+            wt = _i8(np.asarray(b[0], f32).view(np.uint32)[:out * ng]).reshape(out, ng * 4)[:, :cols]
+            wt = wt.astype(np.float64)
+            be = np.repeat(b[1][:out, None].astype(np.float64), cols, axis=1)
+        g = b[2][:seq * out].reshape(seq, out).astype(np.float64)
+        return {3: (g @ (wt * be)).ravel()}
     if nm == "cache-append-ring":
         kvdim, nsink, win = p
         pos = int(b[1][0])

@@ -30,7 +30,8 @@ PIN_TOL = {"softmax": ks.ELEM(1e-5), "silu": 1e-6, "silu-mul": 1e-6, "rmsnorm-is
            "bitlinear-packed-v": 1e-5, "matmul": 1e-5, "matmul-tiled": 1e-5, "matmul-reg": 1e-5,
            "linear": 1e-5, "attn-scores": 1e-5, "attn-context": 1e-5, "decode-attn": 1e-5,
            "decode-attn-b": 1e-5, "attn-causal-gqa": 1e-5, "decode-attn-stream": 1e-5,
-           "attn-stream-entries": 1e-5, "decode-attn-paged": 1e-5, "decode-attn-paged-v": 1e-5}
+           "attn-stream-entries": 1e-5, "decode-attn-paged": 1e-5, "decode-attn-paged-v": 1e-5,
+           "ternary-rows-t": 1e-5, "dp4a-rows-t": 1e-5}
 
 CASES = ks.cases()
 
@@ -306,3 +307,24 @@ def test_robust_access_never_faults_the_checker():
     out = np.full(4, 7, np.float32)
     orc.dispatch("embed-gather", [np.array([99.0], np.float32), np.ones(8, np.float32), out], [1, 4], 1)
     assert not out.any()
+
+
+def test_transposed_linear_adjoint_identity():
+    """ternary-rows and ternary-rows-t are adjoint: <W x, g> = <x, W' g>
+    (test/ternary-kernel-test.el:130-145), with the block scales
+    load-bearing (a different scale per (row, block))."""
+    rng = np.random.default_rng(20260921)
+    seq, out, cols, nblk = 3, 6, 256, 2
+    wng = (cols + 15) // 16
+    w = rng.integers(0, 2 ** 32, out * wng, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    beta = (np.abs(rng.standard_normal(out * nblk)) * 0.05 + 0.01).astype(np.float32)
+    x = rng.standard_normal(seq * cols).astype(np.float32)
+    g = rng.standard_normal(seq * out).astype(np.float32)
+    y = np.zeros(seq * out, np.float32)
+    orc.dispatch("ternary-rows", [x, w, np.zeros(out, np.float32), beta, y], [seq, out, cols, nblk, wng],
+                 (seq * out + 63) // 64)
+    xt = np.zeros(seq * cols, np.float32)
+    orc.dispatch("ternary-rows-t", [w, beta, g, xt], [out, cols, nblk, wng, seq], (seq * cols + 63) // 64)
+    left = float(np.dot(y.astype(np.float64), g))
+    right = float(np.dot(x.astype(np.float64), xt))
+    assert abs(left - right) <= 1e-5 * max(1e-6, abs(left))
