@@ -29,6 +29,7 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep]
 """
 import argparse
 import ctypes
+import ctypes as C
 import json
 import os
 import sys
@@ -442,6 +443,42 @@ def tlinear_bench(stream):
             "note": "each column summed over the 2560 rows in order (bit-identical to the reference's sum)"}
 
 
+def paged_bench(stream):
+    """PagedAttention over fp16 pools at the config-5 decode shape (20/5 heads
+    x 128, every sequence at position 767, blocks of 16 positions in a random
+    order), B = 1 and 32, 8 rotated pools; bytes = K and V of the attended
+    positions + q + out (+ the block table)."""
+    import nlgpu
+    heads, kvh, hd, bs, mbps, ncp = 20, 5, 128, 16, 48, 8
+    kvdim = kvh * hd
+    res = {}
+    for B in (1, 32):
+        npool = B * mbps
+        rng = np.random.default_rng(B)
+        table = rng.permutation(npool).reshape(B, mbps).astype(np.int32)
+        lens = np.full(B, bs * mbps - 1, np.int32)
+        pool_bytes = npool * bs * kvdim * 2
+        kp, vp = nlgpu.DeviceArray(pool_bytes * ncp), nlgpu.DeviceArray(pool_bytes * ncp)
+        nlgpu.lib().nlg_fill_normal(C.c_void_p(kp.ptr), pool_bytes * ncp // 4, 1, C.c_float(1.0), 0, stream)
+        nlgpu.lib().nlg_fill_normal(C.c_void_p(vp.ptr), pool_bytes * ncp // 4, 2, C.c_float(1.0), 0, stream)
+        q = nlgpu.to_device(nlgpu.normal(3, B * heads * hd))
+        out = nlgpu.DeviceArray(B * heads * hd * 4)
+        ws = nlgpu.DeviceArray(nlgpu.decode_attn_paged_f16_workspace(B, heads, kvh, hd, bs, mbps))
+        dl, dt = nlgpu.to_device(lens), nlgpu.to_device(table)
+
+        def fn(i):
+            c = i % ncp
+            nlgpu.decode_attn_paged_f16(q, _Ptr(kp.ptr + c * pool_bytes, pool_bytes),
+                                        _Ptr(vp.ptr + c * pool_bytes, pool_bytes), dl, dt, npool, out, B, heads,
+                                        kvh, hd, bs, mbps, ws, stream=stream)
+        us = _per_launch_us(fn, 4 * ncp, stream)
+        nbytes = B * bs * mbps * kvdim * 2 * 2 + B * heads * hd * 8 + table.nbytes
+        res[f"B{B}"] = {"us": round(us, 3), "bytes": int(nbytes), "gbs": round(nbytes / us / 1e3, 1),
+                        "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "launches": 2}
+        kp.free(); vp.free()
+    return res
+
+
 def cpu_baseline(x, w_one, seconds: float):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import nlg_oracle as orc
@@ -559,6 +596,7 @@ def main():
         extra["swiglu_ffn_config4"] = ffn_bench(stream)
         extra["weight_ingest_repack"] = repack_bench(stream)
         extra["transposed_linear"] = tlinear_bench(stream)
+        extra["paged_attention_f16"] = paged_bench(stream)
     value = STEP_BYTES / (r["step_ms"] * 1e-3) / 1e9
     gemv_gbs = GEMV_BYTES / (r["gemv_ms"] * 1e-3) / 1e9
     stacked_gbs = GEMV_BYTES * COPIES / (r["stacked_ms"] * 1e-3) / 1e9

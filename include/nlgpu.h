@@ -248,6 +248,28 @@ int nlg_decode_attn_f16(const float *q, const uint16_t *kcache, const uint16_t *
 size_t nlg_decode_attn_f16_workspace(uint32_t batch, uint32_t heads, uint32_t kvheads,
                                      uint32_t head_dim, uint32_t max_seq);
 
+/* Paged fp16 KV (PagedAttention): decode-attn-paged-v's arithmetic
+ * (kernels.el:1222-1246) over pools [block][bs][kvheads][head_dim] fp16
+ * shared by all sequences; sequence b attends positions 0..lens[b] through
+ * its row of the block table [batch x mbps] (position p in block
+ * table[b*mbps + p/bs], offset p%bs), so sequences of different lengths and
+ * shared prefix blocks mix in one batch.  Table entries outside
+ * [0, npool) read as zero K/V rows.  Same chunk pass and merge as
+ * nlg_decode_attn_f16; workspace from nlg_decode_attn_paged_f16_workspace. */
+int nlg_decode_attn_paged_f16(const float *q, const uint16_t *kpool, const uint16_t *vpool,
+                              const int32_t *lens, const int32_t *table, uint32_t npool, float *out,
+                              uint32_t batch, uint32_t heads, uint32_t kvheads, uint32_t head_dim,
+                              uint32_t bs, uint32_t mbps, void *workspace, size_t workspace_bytes,
+                              void *stream);
+size_t nlg_decode_attn_paged_f16_workspace(uint32_t batch, uint32_t heads, uint32_t kvheads,
+                                           uint32_t head_dim, uint32_t bs, uint32_t mbps);
+/* cache-append-paged-v (kernels.el:1211-1220) into an fp16 pool: row b of
+ * src [batch x kvdim] f32 goes to position lens[b] of sequence b (round to
+ * nearest even); positions or blocks out of range are skipped. */
+int nlg_cache_append_paged_f16(const float *src, const int32_t *lens, const int32_t *table, uint32_t npool,
+                               uint16_t *pool, uint32_t batch, uint32_t kvdim, uint32_t bs, uint32_t mbps,
+                               void *stream);
+
 /* The first of those launches alone: per chunk of positions and head, the
  * chunk's max score, sum of exp and exp-weighted sum of V, left in
  * `workspace` for nlg_attn_ternary_linear_residual. */

@@ -20,13 +20,8 @@
 // Its sum is a tree, not the reference's serial loop, so S can differ from
 // the reference in the last bit; everything after it is the reference's
 // arithmetic.
-//
-// k_attn_part + k_attn_merge: single-query GQA attention over fp16 KV
-// caches (decode-attn(-b), kernels.el:315-338, :366-390: scale 1/sqrt(hd),
-// max seeded at -1e30, C = sum(e*V)/sum(e)), split over chunks of positions.
-// Each workgroup of the first pass handles one (chunk, kv head, sequence)
-// for all the query heads of that kv head, so K and V are read from HBM once;
-// a second launch merges the chunks (max-rescaled sums).
+
+// The fp16 decode attention these layers feed lives in nlg_dattn.hip.
 #include <math.h>
 
 #include "nlg_quant.h"
@@ -35,11 +30,6 @@
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
   return __builtin_bit_cast(uint16_t, (_Float16)v);  // round to nearest even
-}
-// fp16 element e (0..7) of eight packed in a uint4, as f32 (exact)
-__device__ __forceinline__ float f16x8_at(const uint4 &u, int e) {
-  const uint32_t w = e < 2 ? u.x : e < 4 ? u.y : e < 6 ? u.z : u.w;
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu)));
 }
 
 // F4: float4s of the activation row per thread (cols <= 1024*F4).
@@ -498,321 +488,3 @@ extern "C" int nlg_rms_ternary_argmax(const float *x, const float *gain, float e
   return NLG_OK;
 }
 
-// -------------------------------------------------- fp16 decode attention
-
-struct AttnArgs {
-  const float *q;           // [B x heads*hd]
-  const uint16_t *kc, *vc;  // [B][kvheads][max_seq][hd] fp16 bits
-  const int32_t *pos;       // attend positions 0..pos[0]
-  float *pctx;              // [B][nchunk][heads*hd]: sum of e*V over the chunk
-  float *pmz;               // [B][nchunk][heads][2]: chunk max, sum of e
-  uint32_t heads, kvheads, max_seq, nchunk;
-  uint32_t qper;            // 0: row z = sequence z at pos[0]; else sequence z/qper at pos[0] + z%qper
-  uint32_t grp;             // query heads per kv head (a workgroup takes G <= grp of them)
-  float coef;               // 1/sqrt(hd)
-};
-
-// Sum over aligned groups of L lanes (L = 8 or 16); every lane gets its
-// group's sum.
-template <int L>
-__device__ __forceinline__ float group_sum(float v) {
-  v = v + __int_as_float(nlg_dpp<0xB1>(__float_as_int(v)));   // quad_perm [1,0,3,2]
-  v = v + __int_as_float(nlg_dpp<0x4E>(__float_as_int(v)));   // quad_perm [2,3,0,1]
-  v = v + __int_as_float(nlg_dpp<0x141>(__float_as_int(v)));  // row_half_mirror
-  if (L == 16) v = v + __int_as_float(nlg_dpp<0x140>(__float_as_int(v)));  // row_mirror
-  return v;
-}
-
-// Positions per workgroup for head dim HD: 8 waves x NI instructions x
-// (64 / (HD/8)) positions per instruction; NI = 8 when 4 would need more
-// chunks than the O-projection's prologue merges.
-#define ATTN_WAVES 8
-static inline uint32_t attn_ni(uint32_t hd, uint32_t max_seq) {
-  const uint32_t cs4 = ATTN_WAVES * 4u * (64u / (hd / 8u));
-  return (max_seq + cs4 - 1) / cs4 > NLG_ATTN_MAX_CHUNKS ? 8u : 4u;
-}
-static inline uint32_t attn_chunks(uint32_t hd, uint32_t max_seq) {
-  const uint32_t cs = ATTN_WAVES * attn_ni(hd, max_seq) * (64u / (hd / 8u));
-  return (max_seq + cs - 1) / cs;
-}
-uint32_t nlg_attn_chunk_count(uint32_t head_dim, uint32_t max_seq) { return attn_chunks(head_dim, max_seq); }
-
-// Pass 1: one workgroup per (chunk, kv head, sequence) scores its chunk's
-// positions for every query head of that kv head (K and V read once) and
-// stores the chunk's max m, sum z = sum(exp(s - m)) and sum(exp(s - m) * V).
-// Lanes hold 8 dimensions of one position: LPP = HD/8 lanes per position,
-// PPI = 64/LPP positions per wave instruction.  Every K and V load of the
-// workgroup is issued before the first score is computed.
-template <int HD, int G, int NI>
-__global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
-  constexpr int LPP = HD / 8, PPI = 64 / LPP, PW = NI * PPI, NW = ATTN_WAVES, CS = NW * PW;
-  __shared__ float s_m[NW][G], s_z[NW][G];
-  __shared__ float s_ctx[NW][G][HD];
-  asm volatile("" ::"s"(a.q), "s"(a.kc), "s"(a.vc), "s"(a.pos), "s"(a.pctx), "s"(a.pmz), "s"(a.heads),
-               "s"(a.kvheads), "s"(a.max_seq), "s"(a.nchunk), "s"(a.coef));
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  // workgroup: chunk c, query heads h0 .. h0+G-1 (all of one kv head), query row qr
-  const uint32_t c = blockIdx.x, h0 = blockIdx.y * G, qr = blockIdx.z, kvh = h0 / a.grp;
-  const uint32_t b = a.qper ? qr / a.qper : qr;                         // its sequence
-  const size_t cb = (size_t)qr * a.nchunk + c;
-  float *pctx = a.pctx + cb * a.heads * HD + (size_t)h0 * HD;
-  float *pmz = a.pmz + (cb * a.heads + h0) * 2;
-  const uint32_t p0 = c * CS;
-  // K, V and q are fetched before the position arrives (addresses clamped
-  // to the cache, not to the position), so the position's fetch is not a
-  // round trip ahead of theirs; positions past it are masked afterwards.
-  const int d0 = 8 * (lane % LPP), grp = lane / LPP;
-  const size_t slot = (size_t)b * a.kvheads + kvh;
-  const uint16_t *kb = a.kc + slot * a.max_seq * HD + d0;
-  const uint16_t *vb = a.vc + slot * a.max_seq * HD + d0;
-  uint4 kr[NI], vr[NI];
-  uint32_t pp[NI];
-#pragma unroll
-  for (int i = 0; i < NI; i++) {
-    pp[i] = p0 + w * PW + i * PPI + grp;
-    const uint32_t pc = pp[i] < a.max_seq ? pp[i] : a.max_seq - 1;
-    kr[i] = *(const uint4 *)(kb + (size_t)pc * HD);
-    vr[i] = *(const uint4 *)(vb + (size_t)pc * HD);
-  }
-  const float *qb = a.q + (size_t)qr * a.heads * HD + (size_t)h0 * HD + d0;
-  float q[G][8];
-#pragma unroll
-  for (int h = 0; h < G; h++) {
-    const float4 q0 = *(const float4 *)(qb + h * HD), q1 = *(const float4 *)(qb + h * HD + 4);
-    q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
-    q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
-  }
-  const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(qr % a.qper) : 0);
-  const uint32_t len = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
-  if (p0 >= len) {  // block-uniform: a chunk past the position adds nothing
-    for (int i = threadIdx.x; i < G * HD; i += NW * 64) pctx[i] = 0.0f;
-    if (threadIdx.x < G) {
-      pmz[2 * threadIdx.x] = -1.0e30f;
-      pmz[2 * threadIdx.x + 1] = 0.0f;
-    }
-    return;
-  }
-  float s[NI][G];
-#pragma unroll
-  for (int i = 0; i < NI; i++) {
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-      float d = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; j++) d = fmaf(q[h][j], f16x8_at(kr[i], j), d);
-      d = group_sum<LPP>(d);
-      s[i][h] = pp[i] < len ? d * a.coef : -INFINITY;
-    }
-  }
-  float m[G], z[G], ctx[G][8];
-#pragma unroll
-  for (int h = 0; h < G; h++) {
-    float mm = -1.0e30f;
-#pragma unroll
-    for (int i = 0; i < NI; i++) mm = s[i][h] > mm ? s[i][h] : mm;
-    for (int off = LPP; off < 64; off <<= 1) {
-      const float o = __shfl_xor(mm, off);
-      mm = o > mm ? o : mm;
-    }
-    m[h] = mm;
-    z[h] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) ctx[h][j] = 0.0f;
-  }
-#pragma unroll
-  for (int i = 0; i < NI; i++) {
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-      const float e = expf(s[i][h] - m[h]);
-      z[h] = z[h] + e;
-#pragma unroll
-      for (int j = 0; j < 8; j++) ctx[h][j] = fmaf(e, f16x8_at(vr[i], j), ctx[h][j]);
-    }
-  }
-#pragma unroll
-  for (int h = 0; h < G; h++) {
-    for (int off = LPP; off < 64; off <<= 1) {
-      z[h] = z[h] + __shfl_xor(z[h], off);
-#pragma unroll
-      for (int j = 0; j < 8; j++) ctx[h][j] = ctx[h][j] + __shfl_xor(ctx[h][j], off);
-    }
-    if (grp == 0) {
-#pragma unroll
-      for (int j = 0; j < 8; j++) s_ctx[w][h][d0 + j] = ctx[h][j];
-    }
-    if (lane == 0) {
-      s_m[w][h] = m[h];
-      s_z[w][h] = z[h];
-    }
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < G * HD; idx += NW * 64) {
-    const int h = idx / HD, d = idx % HD;
-    float mm = s_m[0][h];
-#pragma unroll
-    for (int k = 1; k < NW; k++) mm = s_m[k][h] > mm ? s_m[k][h] : mm;
-    float zz = 0.0f, cx = 0.0f;
-#pragma unroll
-    for (int k = 0; k < NW; k++) {
-      const float sc = expf(s_m[k][h] - mm);
-      zz = fmaf(s_z[k][h], sc, zz);
-      cx = fmaf(s_ctx[k][h][d], sc, cx);
-    }
-    pctx[idx] = cx;
-    if (d == 0) {
-      pmz[2 * h] = mm;
-      pmz[2 * h + 1] = zz;
-    }
-  }
-}
-
-// Pass 2: out = sum_c pctx_c * exp(m_c - M) / sum_c z_c * exp(m_c - M),
-// M = max_c m_c, one thread per output element.
-__global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ pctx,
-                                                    const float *__restrict__ pmz, float *__restrict__ out,
-                                                    uint32_t batch, uint32_t heads, uint32_t hd,
-                                                    uint32_t nchunk) {
-  const uint32_t nh = heads * hd;
-  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (uint64_t)batch * nh) return;
-  const uint32_t b = (uint32_t)(i / nh), e = (uint32_t)(i % nh), h = e / hd;
-  const float *mz = pmz + ((size_t)b * nchunk * heads + h) * 2;
-  const float *cx = pctx + (size_t)b * nchunk * nh + e;
-  // chunks in groups of 8 whose loads are all issued together (addresses
-  // clamped to the last chunk, weights of the extra ones zero)
-  float mm = -1.0e30f;
-  for (uint32_t c0 = 0; c0 < nchunk; c0 += 8) {
-    float2 v[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const uint32_t c = c0 + k < nchunk ? c0 + k : nchunk - 1;
-      v[k] = *(const float2 *)(mz + (size_t)c * heads * 2);
-    }
-#pragma unroll
-    for (int k = 0; k < 8; k++) mm = v[k].x > mm ? v[k].x : mm;
-  }
-  float zz = 0.0f, acc = 0.0f;
-  for (uint32_t c0 = 0; c0 < nchunk; c0 += 8) {
-    float2 v[8];
-    float x[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const uint32_t c = c0 + k < nchunk ? c0 + k : nchunk - 1;
-      v[k] = *(const float2 *)(mz + (size_t)c * heads * 2);
-      x[k] = cx[(size_t)c * nh];
-    }
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const float sc = c0 + k < nchunk ? expf(v[k].x - mm) : 0.0f;
-      zz = fmaf(v[k].y, sc, zz);
-      acc = fmaf(x[k], sc, acc);
-    }
-  }
-  out[i] = acc / zz;
-}
-
-extern "C" size_t nlg_decode_attn_f16_workspace(uint32_t batch, uint32_t heads, uint32_t kvheads,
-                                                uint32_t head_dim, uint32_t max_seq) {
-  if (!kvheads || (head_dim != 64 && head_dim != 128) || !max_seq) return 0;
-  const size_t nchunk = attn_chunks(head_dim, max_seq);
-  const size_t ctx = (size_t)batch * nchunk * heads * head_dim * 4;
-  return (ctx + 255) / 256 * 256 + (size_t)batch * nchunk * heads * 2 * 4;
-}
-
-// Validate and lay out the workspace; fills everything but q/kc/vc/pos.
-static int attn_setup(AttnArgs &a, uint32_t batch, uint32_t heads, uint32_t kvheads, uint32_t head_dim,
-                      uint32_t max_seq, void *workspace, size_t workspace_bytes) {
-  if (!kvheads || !heads || heads % kvheads) return nlg_fail("decode attn: heads must be a multiple of kvheads");
-  const uint32_t G = heads / kvheads;
-  if (head_dim != 64 && head_dim != 128) return nlg_fail("decode attn: head_dim must be 64 or 128");
-  if (G != 1 && G != 2 && G != 4 && G != 8) return nlg_fail("decode attn: heads/kvheads must be 1, 2, 4 or 8");
-  if (!max_seq || batch > 65535 || kvheads > 65535) return nlg_fail("decode attn: bad max_seq/batch/kvheads");
-  const size_t need = nlg_decode_attn_f16_workspace(batch, heads, kvheads, head_dim, max_seq);
-  if (!workspace || workspace_bytes < need) return nlg_fail("decode attn: needs a %zu-byte workspace", need);
-  a.nchunk = attn_chunks(head_dim, max_seq);
-  const size_t ctx = (size_t)batch * a.nchunk * heads * head_dim * 4;
-  a.pctx = (float *)workspace;
-  a.pmz = (float *)((char *)workspace + (ctx + 255) / 256 * 256);
-  a.heads = heads; a.kvheads = kvheads; a.max_seq = max_seq;
-  a.coef = 1.0f / sqrtf((float)head_dim);  // (/ 1.0 (sqrt (float hd)))
-  return NLG_OK;
-}
-
-int nlg_attn_chunks(const float *q, const uint16_t *kcache, const uint16_t *vcache, const int32_t *pos,
-                    uint32_t rows, uint32_t qper, uint32_t heads, uint32_t kvheads, uint32_t head_dim,
-                    uint32_t max_seq, void *workspace, size_t workspace_bytes, hipStream_t st) {
-  if (!rows) return NLG_OK;
-  AttnArgs a;
-  if (attn_setup(a, rows, heads, kvheads, head_dim, max_seq, workspace, workspace_bytes)) return NLG_ERR;
-  if (((uintptr_t)q & 15) || ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15))
-    return nlg_fail("decode attn: q and caches must be 16-byte aligned");
-  a.q = q; a.kc = kcache; a.vc = vcache; a.pos = pos; a.qper = qper; a.grp = heads / kvheads;
-  // A workgroup scores every query head of its kv head (K and V read once)
-  // unless there are too few workgroups to spread over the CUs: then one
-  // head each (K and V come from L2 for the others).
-  const uint32_t ni = attn_ni(head_dim, max_seq);
-  const uint32_t G = (uint64_t)rows * kvheads * a.nchunk >= 128 ? a.grp : 1;
-  const dim3 grid(a.nchunk, heads / G, rows), blk(ATTN_WAVES * 64);
-#define AT(HD, GG)                                                                     \
-  do {                                                                                 \
-    if (ni == 8) hipLaunchKernelGGL((k_attn_part<HD, GG, 8>), grid, blk, 0, st, a);   \
-    else hipLaunchKernelGGL((k_attn_part<HD, GG, 4>), grid, blk, 0, st, a);           \
-  } while (0)
-  if (head_dim == 128) {
-    if (G == 1) AT(128, 1); else if (G == 2) AT(128, 2); else if (G == 4) AT(128, 4); else AT(128, 8);
-  } else {
-    if (G == 1) AT(64, 1); else if (G == 2) AT(64, 2); else if (G == 4) AT(64, 4); else AT(64, 8);
-  }
-#undef AT
-  NLG_LAUNCHED("decode attention (fp16 KV)");
-  return NLG_OK;
-}
-
-extern "C" int nlg_decode_attn_f16_chunks(const float *q, const uint16_t *kcache, const uint16_t *vcache,
-                                          const int32_t *pos, uint32_t batch, uint32_t heads,
-                                          uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
-                                          void *workspace, size_t workspace_bytes, void *stream) {
-  if (nlg_ensure_init()) return NLG_ERR;
-  return nlg_attn_chunks(q, kcache, vcache, pos, batch, 0, heads, kvheads, head_dim, max_seq, workspace,
-                         workspace_bytes, nlg_stream(stream));
-}
-
-extern "C" int nlg_attn_ternary_linear_residual(const void *workspace, size_t workspace_bytes, uint32_t batch,
-                                                uint32_t heads, uint32_t kvheads, uint32_t head_dim,
-                                                uint32_t max_seq, const uint32_t *w2, const float *bias,
-                                                const float *beta, int beta_per_row, const float *res,
-                                                float *y, uint32_t out, void *stream) {
-  if (nlg_ensure_init()) return NLG_ERR;
-  if (!batch) return NLG_OK;
-  AttnArgs t;
-  if (attn_setup(t, batch, heads, kvheads, head_dim, max_seq, (void *)workspace, workspace_bytes)) return NLG_ERR;
-  if (t.nchunk > NLG_ATTN_MAX_CHUNKS)
-    return nlg_fail("attention + linear: %u chunks (max_seq %u) exceed the %d the fused merge takes; "
-                    "use nlg_decode_attn_f16 and nlg_ternary_linear_residual", t.nchunk, max_seq,
-                    NLG_ATTN_MAX_CHUNKS);
-  if (!res) return nlg_fail("attention + linear: res is null");
-  FusedArgs a{};
-  a.x = t.pctx; a.attn_mz = t.pmz; a.attn_nc = t.nchunk; a.hd = head_dim;
-  a.w2 = w2; a.bias = bias; a.beta = beta; a.beta_per_row = beta_per_row;
-  a.seq = batch; a.out = out; a.cols = heads * head_dim; a.y = y; a.ystride = out; a.res = res; a.rstride = out;
-  return nlg_fused_launch(a, NLG_PRO_ATTN, NLG_EPI_RESID, 0, nlg_stream(stream));
-}
-
-extern "C" int nlg_decode_attn_f16(const float *q, const uint16_t *kcache, const uint16_t *vcache,
-                                   const int32_t *pos, float *out, uint32_t batch, uint32_t heads,
-                                   uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
-                                   void *workspace, size_t workspace_bytes, void *stream) {
-  if (nlg_ensure_init()) return NLG_ERR;
-  if (!batch) return NLG_OK;
-  if (nlg_decode_attn_f16_chunks(q, kcache, vcache, pos, batch, heads, kvheads, head_dim, max_seq, workspace,
-                                 workspace_bytes, stream))
-    return NLG_ERR;
-  AttnArgs a;
-  attn_setup(a, batch, heads, kvheads, head_dim, max_seq, workspace, workspace_bytes);
-  hipStream_t st = nlg_stream(stream);
-  const uint64_t n = (uint64_t)batch * heads * head_dim;
-  hipLaunchKernelGGL(k_attn_merge, dim3(nlg_blocks(n, 256)), dim3(256), 0, st, a.pctx, a.pmz, out, batch,
-                     heads, head_dim, a.nchunk);
-  NLG_LAUNCHED("decode attention merge");
-  return NLG_OK;
-}

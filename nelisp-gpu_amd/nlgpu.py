@@ -105,6 +105,10 @@ def lib() -> C.CDLL:
                                                    vp, u32, vp]),
         "nlg_prefill_attn_f16": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp, vp]),
         "nlg_repack_i8_to_2bit": (i32, [vp, u32, u32, vp, vp, vp]),
+        "nlg_decode_attn_paged_f16": (i32, [vp, vp, vp, vp, vp, u32, vp, u32, u32, u32, u32, u32, u32, vp, sz,
+                                            vp]),
+        "nlg_decode_attn_paged_f16_workspace": (sz, [u32, u32, u32, u32, u32, u32]),
+        "nlg_cache_append_paged_f16": (i32, [vp, vp, vp, u32, vp, u32, u32, u32, u32, vp]),
         "nlg_repack_packed_to_2bit": (i32, [vp, u32, u32, u32, u32, vp, vp, vp]),
         "nlg_fill_normal": (i32, [vp, C.c_uint64, C.c_uint64, C.c_float, u32, vp]),
         "nlg_stack_create": (i32, [C.POINTER(StackConfig), C.POINTER(vp)]),
@@ -343,6 +347,22 @@ def prefill_attn_f16(q, kc, vc, pos, rows, qper, heads, kvheads, head_dim, max_s
     position pos[0] + r % qper) over fp16 caches; ctx [rows][heads*head_dim]."""
     _check(lib().nlg_prefill_attn_f16(q.ptr, kc.ptr, vc.ptr, pos.ptr, rows, qper, heads, kvheads, head_dim,
                                       max_seq, ctx.ptr, stream), "prefill_attn_f16")
+
+
+def decode_attn_paged_f16_workspace(batch, heads, kvheads, head_dim, bs, mbps) -> int:
+    return int(lib().nlg_decode_attn_paged_f16_workspace(batch, heads, kvheads, head_dim, bs, mbps))
+
+
+def decode_attn_paged_f16(q, kpool, vpool, lens, table, npool, out, batch, heads, kvheads, head_dim, bs, mbps,
+                          workspace, stream=None) -> None:
+    _check(lib().nlg_decode_attn_paged_f16(q.ptr, kpool.ptr, vpool.ptr, lens.ptr, table.ptr, npool, out.ptr, batch,
+                                           heads, kvheads, head_dim, bs, mbps, workspace.ptr, workspace.nbytes,
+                                           stream), "decode_attn_paged_f16")
+
+
+def cache_append_paged_f16(src, lens, table, npool, pool, batch, kvdim, bs, mbps, stream=None) -> None:
+    _check(lib().nlg_cache_append_paged_f16(src.ptr, lens.ptr, table.ptr, npool, pool.ptr, batch, kvdim, bs, mbps,
+                                            stream), "cache_append_paged_f16")
 
 
 def repack_i8_to_2bit(wp, out, cols, w2, nbad=None, stream=None) -> None:

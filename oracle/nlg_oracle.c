@@ -1084,3 +1084,48 @@ uint32_t or_repack_packed_2bit(const float *wpk, uint32_t out, uint32_t cols, ui
     }
   return bad;
 }
+
+/* decode-attn-paged-v (kernels.el:1222-1246) with K and V read from fp16
+ * pools [block][bs][kvheads][hd]: sequence s attends positions 0..lens[s]
+ * through table[s*mbps + j/bs] (offset j%bs); blocks outside [0, npool)
+ * read as zero rows (the pools' bounds). */
+void or_decode_attn_paged_f16(const float *q, const uint16_t *kp, const uint16_t *vp, const int32_t *lens,
+                              const int32_t *table, uint32_t npool, float *out, uint32_t B, uint32_t heads,
+                              uint32_t kvheads, uint32_t hd, uint32_t bs, uint32_t mbps) {
+  const uint32_t dim = heads * hd, grp = heads / kvheads, kvdim = kvheads * hd;
+  const float coef = 1.0f / sqrtf((float)hd);
+#pragma omp parallel for schedule(static)
+  for (int64_t idx = 0; idx < (int64_t)B * dim; idx++) {
+    uint32_t s = (uint32_t)(idx / dim), c = (uint32_t)(idx % dim);
+    uint32_t h = c / hd, t = c % hd, kvh = h / grp;
+    const float *qh = q + (size_t)s * dim + (size_t)h * hd;
+    int32_t pos = lens[s];
+    uint32_t len = pos < 0 ? 1u : (uint32_t)pos + 1u;
+    if (len > bs * mbps) len = bs * mbps;
+    float mx = NEG_BIG;
+    for (uint32_t j = 0; j < len; j++) {
+      int32_t ph = table[(size_t)s * mbps + j / bs];
+      float acc = 0.0f;
+      if (ph >= 0 && (uint32_t)ph < npool) {
+        size_t kb = (((size_t)ph * bs + j % bs) * kvdim) + (size_t)kvh * hd;
+        for (uint32_t tt = 0; tt < hd; tt++) acc = acc + qh[tt] * f16_to_f32(kp[kb + tt]);
+      }
+      float sc = acc * coef;
+      if (sc > mx) mx = sc;
+    }
+    float z = 0.0f, ctx = 0.0f;
+    for (uint32_t j = 0; j < len; j++) {
+      int32_t ph = table[(size_t)s * mbps + j / bs];
+      float acc = 0.0f, v = 0.0f;
+      if (ph >= 0 && (uint32_t)ph < npool) {
+        size_t kb = (((size_t)ph * bs + j % bs) * kvdim) + (size_t)kvh * hd;
+        for (uint32_t tt = 0; tt < hd; tt++) acc = acc + qh[tt] * f16_to_f32(kp[kb + tt]);
+        v = f16_to_f32(vp[kb + t]);
+      }
+      float e = expf(acc * coef - mx);
+      z = z + e;
+      ctx = ctx + e * v;
+    }
+    out[idx] = ctx / z;
+  }
+}

@@ -57,6 +57,13 @@ void or_decode_attn_f16(const float *q, const uint16_t *kc, const uint16_t *vc, 
                         float *out, uint32_t B, uint32_t heads, uint32_t kvheads, uint32_t hd,
                         uint32_t max_seq);
 
+/* decode-attn-paged-v (kernels.el:1222-1246) over fp16 pools
+ * [block][bs][kvheads][hd]; sequence s at position lens[s] (negative: 0);
+ * table [B x mbps]; blocks outside [0, npool) read as zero rows. */
+void or_decode_attn_paged_f16(const float *q, const uint16_t *kp, const uint16_t *vp, const int32_t *lens,
+                              const int32_t *table, uint32_t npool, float *out, uint32_t B, uint32_t heads,
+                              uint32_t kvheads, uint32_t hd, uint32_t bs, uint32_t mbps);
+
 /* Weight ingest into the 2-bit layout of ternary-rows (kernels.el:700-746:
  * field f of word w = column 16w+f, bits 2f..2f+1, sign-extended).
  * From int8 lanes (bitlinear-dp4a-1f/-rows WP, kernels.el:619-653: lane l of

@@ -47,6 +47,8 @@ def lib() -> C.CDLL:
         L.or_rmsnorm_rows.argtypes = [vp, vp, C.c_float, vp, u32, u32]
         L.or_decode_attn_f16.restype = None
         L.or_decode_attn_f16.argtypes = [vp, vp, vp, u32, vp, u32, u32, u32, u32, u32]
+        L.or_decode_attn_paged_f16.restype = None
+        L.or_decode_attn_paged_f16.argtypes = [vp, vp, vp, vp, vp, u32, vp, u32, u32, u32, u32, u32, u32]
         L.or_repack_i8_2bit.restype = u32
         L.or_repack_i8_2bit.argtypes = [vp, u32, u32, vp]
         L.or_repack_packed_2bit.restype = u32
@@ -138,6 +140,16 @@ def decode_attn_f16(q, kc, vc, pos, B, heads, kvheads, hd, max_seq) -> np.ndarra
                              _p(np.ascontiguousarray(kc, np.uint16)),
                              _p(np.ascontiguousarray(vc, np.uint16)), int(pos), _p(out), B, heads,
                              kvheads, hd, max_seq)
+    return out
+
+
+def decode_attn_paged_f16(q, kp, vp, lens, table, npool, B, heads, kvheads, hd, bs, mbps) -> np.ndarray:
+    """kp, vp: uint16 fp16 pools [block][bs][kvheads][hd]; lens int32 [B]; table int32 [B x mbps]."""
+    out = np.empty(B * heads * hd, np.float32)
+    lib().or_decode_attn_paged_f16(_p(np.ascontiguousarray(q, np.float32)), _p(np.ascontiguousarray(kp, np.uint16)),
+                                   _p(np.ascontiguousarray(vp, np.uint16)), _p(np.ascontiguousarray(lens, np.int32)),
+                                   _p(np.ascontiguousarray(table, np.int32)), npool, _p(out), B, heads, kvheads, hd,
+                                   bs, mbps)
     return out
 
 

@@ -256,6 +256,55 @@ def test_prefill_attention_fp16(B, heads, kvh, hd, max_seq, P, pos0):
     assert worst <= 1e-4
 
 
+@pytest.mark.parametrize("B,heads,kvh,hd,bs,mbps,npool", [(3, 20, 5, 128, 16, 48, 160), (4, 8, 2, 64, 7, 10, 30),
+                                                       (32, 20, 5, 128, 16, 48, 1600)])
+def test_paged_f16_attention(B, heads, kvh, hd, bs, mbps, npool):
+    """PagedAttention over fp16 pools: per-sequence lengths, shared prefix
+    blocks and a block outside the pool, against the CPU restatement."""
+    print(f"[gpu] paged attention B={B} heads={heads}/{kvh} hd={hd} bs={bs} mbps={mbps} npool={npool}", flush=True)
+    rng = np.random.default_rng(B * 100 + hd)
+    kvdim = kvh * hd
+    kp = nlgpu.normal(B + 1, npool * bs * kvdim).astype(np.float16).view(np.uint16)
+    vp = nlgpu.normal(B + 2, npool * bs * kvdim).astype(np.float16).view(np.uint16)
+    table = rng.permutation(npool)[:B * mbps].reshape(B, mbps).astype(np.int32) if npool >= B * mbps else \
+        rng.integers(0, npool, (B, mbps)).astype(np.int32)
+    table[1, :3] = table[0, :3]  # sequences 0 and 1 share a prefix
+    table[B - 1, 1] = npool + 3  # outside the pool: zero rows
+    lens = rng.integers(0, bs * mbps, B).astype(np.int32)
+    lens[0] = bs * mbps - 1
+    q = (nlgpu.normal(B + 3, B * heads * hd) * f32(2.0)).astype(f32)
+    out = nlgpu.DeviceArray(B * heads * hd * 4)
+    ws = nlgpu.DeviceArray(nlgpu.decode_attn_paged_f16_workspace(B, heads, kvh, hd, bs, mbps))
+    nlgpu.decode_attn_paged_f16(nlgpu.to_device(q), nlgpu.to_device(kp), nlgpu.to_device(vp), nlgpu.to_device(lens),
+                                nlgpu.to_device(table), npool, out, B, heads, kvh, hd, bs, mbps, ws)
+    got = out.download(f32, B * heads * hd)
+    want = orc.decode_attn_paged_f16(q, kp, vp, lens, table, npool, B, heads, kvh, hd, bs, mbps)
+    err = np.abs(got - want).max() / np.abs(want).max()
+    print(f"  max err / max|out| = {err:.2e}", flush=True)
+    assert err <= 1e-4
+
+
+def test_paged_f16_append():
+    B, kvdim, bs, mbps, npool = 5, 640, 16, 8, 50
+    rng = np.random.default_rng(5)
+    table = rng.permutation(npool)[:B * mbps].reshape(B, mbps).astype(np.int32)
+    table[4, 2] = -1  # skipped
+    lens = np.array([0, 17, 127, 200, 40], np.int32)  # 200: past the table, skipped
+    src = nlgpu.normal(9, B * kvdim)
+    pool0 = nlgpu.normal(10, npool * bs * kvdim).astype(np.float16).view(np.uint16)
+    dpool = nlgpu.to_device(pool0)
+    nlgpu.cache_append_paged_f16(nlgpu.to_device(src), nlgpu.to_device(lens), nlgpu.to_device(table), npool, dpool,
+                                 B, kvdim, bs, mbps)
+    got = dpool.download(np.uint16, pool0.size)
+    want = pool0.copy().reshape(npool * bs, kvdim)
+    for s_ in range(B):
+        p = int(lens[s_])
+        if p >= bs * mbps or table[s_, p // bs] < 0:
+            continue
+        want[table[s_, p // bs] * bs + p % bs] = src[s_ * kvdim:(s_ + 1) * kvdim].astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want.ravel())
+
+
 def test_prefill_attention_rejects_bad_shapes():
     d = nlgpu.DeviceArray(4096)
     pos = nlgpu.to_device(np.array([0], np.int32))

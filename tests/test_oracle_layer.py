@@ -143,3 +143,35 @@ def test_one_lane_flip_moves_logits_by_percent(monkeypatch):
     assert errs.max() < 5e-2
     first = int(np.argmax(errs > 1e-5)) if (errs > 1e-5).any() else len(errs)
     assert np.all(errs[:first] < 1e-6)  # before the first flip: rounding-level agreement
+
+
+def test_paged_f16_attention_against_float64():
+    """or_decode_attn_paged_f16 (decode-attn-paged-v over fp16 pools) against
+    a float64 gather through the block table: shared blocks, a block
+    outside the pool (zero rows), a non-power-of-two block size."""
+    rng = np.random.default_rng(7)
+    B, heads, kvh, hd, bs, mbps, npool = 3, 4, 2, 64, 7, 5, 12
+    kvdim = kvh * hd
+    kp = rng.standard_normal(npool * bs * kvdim).astype(np.float16)
+    vp = rng.standard_normal(npool * bs * kvdim).astype(np.float16)
+    table = rng.integers(0, npool, (B, mbps)).astype(np.int32)
+    table[1, :2] = table[0, :2]  # a shared prefix
+    table[2, 3] = npool + 5      # outside the pool
+    lens = np.array([4, 30, 34], np.int32)
+    q = rng.standard_normal(B * heads * hd).astype(np.float32)
+    got = orc.decode_attn_paged_f16(q, kp.view(np.uint16), vp.view(np.uint16), lens, table, npool, B, heads, kvh,
+                                    hd, bs, mbps).reshape(B, heads, hd)
+    K = kp.astype(np.float64).reshape(npool, bs, kvh, hd)
+    V = vp.astype(np.float64).reshape(npool, bs, kvh, hd)
+    for s in range(B):
+        n = lens[s] + 1
+        for h in range(heads):
+            kk, vv = np.zeros((n, hd)), np.zeros((n, hd))
+            for j in range(n):
+                ph = table[s, j // bs]
+                if 0 <= ph < npool:
+                    kk[j], vv[j] = K[ph, j % bs, h // (heads // kvh)], V[ph, j % bs, h // (heads // kvh)]
+            sc = kk @ q.reshape(B, heads, hd)[s, h].astype(np.float64) / np.sqrt(hd)
+            e = np.exp(sc - sc.max())
+            want = (e[:, None] * vv).sum(axis=0) / e.sum()
+            assert np.abs(got[s, h] - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
