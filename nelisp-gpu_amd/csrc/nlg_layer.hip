@@ -294,22 +294,17 @@ int nlg_fused_rows_per_wave(uint32_t out, int epi) {
   return out >= 8192 ? 8 : (out >= 2048 ? 4 : (out >= 1024 ? 2 : 1));
 }
 
+// The row length picks the chunks per lane and the activation float4s per
+// thread together (cols = 64 x chunks x CPL; cols <= 1024 x F4), so only the
+// five pairs a row length can give are instantiated.
 template <int PRO, int EPI, int R>
 static void fused_go(const FusedArgs &a, dim3 grid, size_t lds, hipStream_t st) {
-  const uint32_t nchunk = a.wng / 4;
   const dim3 blk(256);
-#define FZ(CC)                                                                                  \
-  do {                                                                                          \
-    if (a.cols <= 2048) hipLaunchKernelGGL((k_tern_fused<R, CC, 2, PRO, EPI>), grid, blk, lds, st, a); \
-    else if (a.cols <= 3072) hipLaunchKernelGGL((k_tern_fused<R, CC, 3, PRO, EPI>), grid, blk, lds, st, a); \
-    else if (a.cols <= 4096) hipLaunchKernelGGL((k_tern_fused<R, CC, 4, PRO, EPI>), grid, blk, lds, st, a); \
-    else if (a.cols <= 8192) hipLaunchKernelGGL((k_tern_fused<R, CC, 8, PRO, EPI>), grid, blk, lds, st, a); \
-    else hipLaunchKernelGGL((k_tern_fused<R, CC, 16, PRO, EPI>), grid, blk, lds, st, a);       \
-  } while (0)
-  if (nchunk <= 64) FZ(1);
-  else if (nchunk <= 128) FZ(2);
-  else FZ(4);
-#undef FZ
+  if (a.cols <= 2048) hipLaunchKernelGGL((k_tern_fused<R, 1, 2, PRO, EPI>), grid, blk, lds, st, a);
+  else if (a.cols <= 3072) hipLaunchKernelGGL((k_tern_fused<R, 1, 3, PRO, EPI>), grid, blk, lds, st, a);
+  else if (a.cols <= 4096) hipLaunchKernelGGL((k_tern_fused<R, 1, 4, PRO, EPI>), grid, blk, lds, st, a);
+  else if (a.cols <= 8192) hipLaunchKernelGGL((k_tern_fused<R, 2, 8, PRO, EPI>), grid, blk, lds, st, a);
+  else hipLaunchKernelGGL((k_tern_fused<R, 4, 16, PRO, EPI>), grid, blk, lds, st, a);
 }
 
 uint32_t nlg_argmax_parts(uint32_t seq, uint32_t cols, uint32_t out) {
