@@ -503,11 +503,15 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   const uint32_t rbase = blockIdx.x * (32 * NB * WR) + wn * (32 * NB);
   const uint32_t tok0 = blockIdx.y * 128;
   const uint32_t nchunks = a.cols / TG_KC;
-  // weight rows of this lane: rbase + 32 nt + li
-  const uint32_t rw0 = rbase + li, rw1 = rbase + 32 + li;
-  const uint32_t rc0 = rw0 < a.out ? rw0 : a.out - 1, rc1 = rw1 < a.out ? rw1 : a.out - 1;
-  const uint4 *w0 = (const uint4 *)(a.w2 + (size_t)rc0 * a.wng) + 2 * lg;
-  const uint4 *w1 = (const uint4 *)(a.w2 + (size_t)rc1 * a.wng) + 2 * lg;
+  // weight rows of this lane: rbase + 32 nt + li (clamped; dead rows masked at the store)
+  uint32_t rw[NB], rc[NB];
+  const uint4 *wp[NB];
+#pragma unroll
+  for (int nt = 0; nt < NB; nt++) {
+    rw[nt] = rbase + 32 * nt + li;
+    rc[nt] = rw[nt] < a.out ? rw[nt] : a.out - 1;
+    wp[nt] = (const uint4 *)(a.w2 + (size_t)rc[nt] * a.wng) + 2 * lg;
+  }
   // activation staging: thread t copies token t/16 + 8 WR i (i < AI), slot t % 16
   const uint32_t slot = threadIdx.x % 16u, tsub = threadIdx.x / 16u;
   const uint8_t *xb[AI];
@@ -518,14 +522,11 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   }
 #define TL_LOADW(c, dst)                                                                   \
   do {                                                                                     \
-    const uint4 u0 = w0[4 * (c)], u1 = w0[4 * (c) + 1];                                    \
-    dst[0] = u0.x; dst[1] = u0.y; dst[2] = u0.z; dst[3] = u0.w;                             \
-    dst[4] = u1.x; dst[5] = u1.y; dst[6] = u1.z; dst[7] = u1.w;                             \
-    if (NB == 2) {                                                                         \
-      const uint4 u2 = w1[4 * (c)], u3 = w1[4 * (c) + 1];                                  \
-      dst[8 % (8 * NB)] = u2.x; dst[9 % (8 * NB)] = u2.y; dst[10 % (8 * NB)] = u2.z;       \
-      dst[11 % (8 * NB)] = u2.w; dst[12 % (8 * NB)] = u3.x; dst[13 % (8 * NB)] = u3.y;     \
-      dst[14 % (8 * NB)] = u3.z; dst[15 % (8 * NB)] = u3.w;                                \
+    _Pragma("unroll") for (int nt = 0; nt < NB; nt++) {                                    \
+      const uint4 u0 = wp[nt][4 * (c)], u1 = wp[nt][4 * (c) + 1];                          \
+      dst[8 * nt + 0] = u0.x; dst[8 * nt + 1] = u0.y; dst[8 * nt + 2] = u0.z;               \
+      dst[8 * nt + 3] = u0.w; dst[8 * nt + 4] = u1.x; dst[8 * nt + 5] = u1.y;               \
+      dst[8 * nt + 6] = u1.z; dst[8 * nt + 7] = u1.w;                                       \
     }                                                                                      \
   } while (0)
 #define TL_LOADA(c, dst)                                                                   \
@@ -550,30 +551,33 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   TL_LOADW(0, wA);
   TL_LOADA(0, aX);
   TL_LOADW(c1, wB);
-  const float *bsrc = a.bias ? a.bias : a.beta;
-  const float bo0 = a.bias ? bsrc[rc0] : 0.0f, bo1 = a.bias ? bsrc[rc1] : 0.0f;
-  const float be0 = a.beta[a.beta_per_row ? rc0 : 0], be1 = a.beta[a.beta_per_row ? rc1 : 0];
+  float bo[NB], be[NB];
+#pragma unroll
+  for (int nt = 0; nt < NB; nt++) {
+    bo[nt] = a.bias ? a.bias[rc[nt]] : 0.0f;
+    be[nt] = a.beta[a.beta_per_row ? rc[nt] : 0];
+  }
   TL_STOREA(0, aX);
-  v16i acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};  // [token block][row block]
+  v16i acc[2][NB];  // [token block][row block]
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int nt = 0; nt < NB; nt++) acc[mt][nt] = (v16i){};
   const uint8_t *sa0 = s_a + (size_t)(wm * 64 + li) * TL_PITCH + 16 * (8 * lg);
   const uint8_t *sa1 = sa0 + 32 * TL_PITCH;
+  // each A fragment (a0, a1) feeds NB matrix-core steps, each decoded B operand two
 #define TL_MMA(buf, WCUR)                                                                    \
   _Pragma("unroll") for (int t = 0; t < 8; t++) {                                             \
-    const uint32_t x0 = WCUR[t];                                                              \
-    const v4i b0 = {(int)((x0 << 6) & 0xC0C0C0C0u), (int)((x0 << 4) & 0xC0C0C0C0u),           \
-                    (int)((x0 << 2) & 0xC0C0C0C0u), (int)(x0 & 0xC0C0C0C0u)};                  \
     const uint4 av0 = *(const uint4 *)(sa0 + (buf) * 128 * TL_PITCH + 16 * t);                \
     const uint4 av1 = *(const uint4 *)(sa1 + (buf) * 128 * TL_PITCH + 16 * t);                \
     const v4i a0 = {(int)av0.x, (int)av0.y, (int)av0.z, (int)av0.w};                          \
     const v4i a1 = {(int)av1.x, (int)av1.y, (int)av1.z, (int)av1.w};                          \
-    acc00 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc00, 0, 0, 0);                    \
-    acc10 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc10, 0, 0, 0);                    \
-    if (NB == 2) {                                                                            \
-      const uint32_t x1 = WCUR[(8 + t) % (8 * NB)];                                           \
-      const v4i b1 = {(int)((x1 << 6) & 0xC0C0C0C0u), (int)((x1 << 4) & 0xC0C0C0C0u),         \
-                      (int)((x1 << 2) & 0xC0C0C0C0u), (int)(x1 & 0xC0C0C0C0u)};                \
-      acc01 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, acc01, 0, 0, 0);                  \
-      acc11 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc11, 0, 0, 0);                  \
+    _Pragma("unroll") for (int nt = 0; nt < NB; nt++) {                                       \
+      const uint32_t x0 = WCUR[8 * nt + t];                                                   \
+      const v4i b0 = {(int)((x0 << 6) & 0xC0C0C0C0u), (int)((x0 << 4) & 0xC0C0C0C0u),         \
+                      (int)((x0 << 2) & 0xC0C0C0C0u), (int)(x0 & 0xC0C0C0C0u)};                \
+      acc[0][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc[0][nt], 0, 0, 0);        \
+      acc[1][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc[1][nt], 0, 0, 0);        \
     }                                                                                         \
   }
   // chunk c: fetch chunk c + 1's activations, then chunk c + 2's weights
@@ -605,7 +609,6 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
 #undef TL_STOREA
   // epilogue: acc[mt][nt] register r is token tok0 + 64 wm + 32 mt + (r%4) + 8 (r/4) + 4 lg,
   // row rbase + 32 nt + li
-  const bool l0 = rw0 < a.out, l1 = NB == 2 && rw1 < a.out;
   if (EPI == NLG_EPI_SWIGLU) {
     // Gate row 2j and up row 2j+1 sit in lanes l, l^1.  Each lane of a pair
     // finishes half of the pair's tokens: the even lane registers 0..7, the
@@ -615,10 +618,8 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
     for (int mt = 0; mt < 2; mt++) {
 #pragma unroll
       for (int nt = 0; nt < NB; nt++) {
-        const v16i q = mt ? (nt ? acc11 : acc10) : (nt ? acc01 : acc00);
-        const float bo = nt ? bo1 : bo0, be = nt ? be1 : be0;
-        const uint32_t row = nt ? rw1 : rw0;
-        const bool lr = nt ? l1 : l0;
+        const v16i q = acc[mt][nt];
+        const bool lr = rw[nt] < a.out;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
           const uint32_t tlo = tok0 + 64 * wm + 32 * mt + (k % 4) + 8 * (k / 4) + 4 * lg;
@@ -626,15 +627,15 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
           const float glo = a.gamma[tlo < a.seq ? tlo : a.seq - 1];
           const float ghi = a.gamma[thi < a.seq ? thi : a.seq - 1];
           // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
-          const float vlo = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, glo), (float)(q[k] >> 6)));
-          const float vhi = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, ghi), (float)(q[k + 8] >> 6)));
+          const float vlo = __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], glo), (float)(q[k] >> 6)));
+          const float vhi = __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], ghi), (float)(q[k + 8] >> 6)));
           const float keep = odd ? vhi : vlo, give = odd ? vlo : vhi;
           const float got = __int_as_float(nlg_dpp<0xB1>(__float_as_int(give)));  // from lane ^ 1
           const float g = odd ? got : keep, u = odd ? keep : got;
           const uint32_t tk = odd ? thi : tlo;
           if (lr && tk < a.seq) {
             const float sg = 1.0f / (1.0f + expf(0.0f - g));
-            a.y[(size_t)tk * a.ystride + (row >> 1)] = (g * sg) * u;
+            a.y[(size_t)tk * a.ystride + (rw[nt] >> 1)] = (g * sg) * u;
           }
         }
       }
@@ -648,14 +649,11 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
       const uint32_t tk = tok0 + 64 * wm + 32 * mt + (r % 4) + 8 * (r / 4) + 4 * lg;
       const uint32_t tkc = tk < a.seq ? tk : a.seq - 1;
       const float gm = a.gamma[tkc];
-      const int q0 = mt ? acc10[r] : acc00[r];
-      // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
-      const float v0 = __fadd_rn(bo0, __fmul_rn(__fmul_rn(be0, gm), (float)(q0 >> 6)));
-      tg_store<EPI>(a, lane, rw0, tk, l0 && tk < a.seq, v0);
-      if (NB == 2) {
-        const int q1 = mt ? acc11[r] : acc01[r];
-        const float v1 = __fadd_rn(bo1, __fmul_rn(__fmul_rn(be1, gm), (float)(q1 >> 6)));
-        tg_store<EPI>(a, lane, rw1, tk, l1 && tk < a.seq, v1);
+#pragma unroll
+      for (int nt = 0; nt < NB; nt++) {
+        // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
+        const float v = __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], gm), (float)(acc[mt][nt][r] >> 6)));
+        tg_store<EPI>(a, lane, rw[nt], tk, rw[nt] < a.out && tk < a.seq, v);
       }
     }
   }
