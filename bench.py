@@ -479,6 +479,41 @@ def paged_bench(stream):
     return res
 
 
+def ring_bench(stream):
+    """StreamingLLM decode attention over fp16 ring caches at the config-5
+    decode shape (20/5 heads x 128), 4 sink slots + a 2044-slot window, every
+    sequence wrapped (stream positions 10000 + b), B = 1 and 32, 8 rotated
+    cache copies; bytes = K and V of the 2048 attended slots + q + out + the
+    two rotation tables (2048 rows x 64 floats each)."""
+    import nlgpu
+    heads, kvh, hd, nsink, win, ncp = 20, 5, 128, 4, 2044, 8
+    cap = nsink + win
+    ang = np.outer(np.arange(cap), 1.0 / 500000.0 ** (np.arange(hd // 2) * 2.0 / hd))
+    co, si = nlgpu.to_device(np.cos(ang).astype(np.float32)), nlgpu.to_device(np.sin(ang).astype(np.float32))
+    res = {}
+    for B in (1, 32):
+        cache_bytes = B * kvh * cap * hd * 2
+        kc, vc = nlgpu.DeviceArray(cache_bytes * ncp), nlgpu.DeviceArray(cache_bytes * ncp)
+        nlgpu.lib().nlg_fill_normal(C.c_void_p(kc.ptr), cache_bytes * ncp // 4, 1, C.c_float(1.0), 0, stream)
+        nlgpu.lib().nlg_fill_normal(C.c_void_p(vc.ptr), cache_bytes * ncp // 4, 2, C.c_float(1.0), 0, stream)
+        q = nlgpu.to_device(nlgpu.normal(3, B * heads * hd))
+        out = nlgpu.DeviceArray(B * heads * hd * 4)
+        ws = nlgpu.DeviceArray(nlgpu.decode_attn_stream_f16_workspace(B, heads, kvh, hd, nsink, win))
+        dpos = nlgpu.to_device(10000 + np.arange(B, dtype=np.int32))
+
+        def fn(i):
+            c = i % ncp
+            nlgpu.decode_attn_stream_f16(q, _Ptr(kc.ptr + c * cache_bytes, cache_bytes),
+                                         _Ptr(vc.ptr + c * cache_bytes, cache_bytes), dpos, co, si, out, B, heads,
+                                         kvh, hd, nsink, win, ws, stream=stream)
+        us = _per_launch_us(fn, 4 * ncp, stream)
+        nbytes = 2 * cache_bytes + B * heads * hd * 8 + 2 * cap * (hd // 2) * 4
+        res[f"B{B}"] = {"us": round(us, 3), "bytes": int(nbytes), "gbs": round(nbytes / us / 1e3, 1),
+                        "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "launches": 2}
+        kc.free(); vc.free()
+    return res
+
+
 def cpu_baseline(x, w_one, seconds: float):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import nlg_oracle as orc
@@ -597,6 +632,7 @@ def main():
         extra["weight_ingest_repack"] = repack_bench(stream)
         extra["transposed_linear"] = tlinear_bench(stream)
         extra["paged_attention_f16"] = paged_bench(stream)
+        extra["ring_attention_f16"] = ring_bench(stream)
     value = STEP_BYTES / (r["step_ms"] * 1e-3) / 1e9
     gemv_gbs = GEMV_BYTES / (r["gemv_ms"] * 1e-3) / 1e9
     stacked_gbs = GEMV_BYTES * COPIES / (r["stacked_ms"] * 1e-3) / 1e9

@@ -270,6 +270,32 @@ int nlg_cache_append_paged_f16(const float *src, const int32_t *lens, const int3
                                uint16_t *pool, uint32_t batch, uint32_t kvdim, uint32_t bs, uint32_t mbps,
                                void *stream);
 
+/* StreamingLLM fp16 ring caches: decode-attn-stream's arithmetic
+ * (kernels.el:404-451) over caches [batch][kvheads][nsink + win][head_dim]
+ * fp16 holding RAW (un-rotated) keys: nsink permanent sink slots, then a
+ * win-slot ring.  Sequence b at stream position pos[b] (negative: 0) attends
+ * len = min(pos + 1, nsink + win) cache-relative ranks: ranks below nsink
+ * are the sink slots, later ones walk the ring from its oldest slot.  K of
+ * rank r is rotated by rows r of co/si and q by row min(pos, nsink + win - 1)
+ * (pairs (2m, 2m+1)); co/si hold >= nsink + win rows of head_dim/2 floats.
+ * q, caches and tables 16-byte aligned; win > 0.  Same chunk pass and merge
+ * as nlg_decode_attn_f16; workspace from nlg_decode_attn_stream_f16_workspace
+ * (0 for invalid sizes). */
+int nlg_decode_attn_stream_f16(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                               const int32_t *pos, const float *co, const float *si, float *out,
+                               uint32_t batch, uint32_t heads, uint32_t kvheads, uint32_t head_dim,
+                               uint32_t nsink, uint32_t win, void *workspace, size_t workspace_bytes,
+                               void *stream);
+size_t nlg_decode_attn_stream_f16_workspace(uint32_t batch, uint32_t heads, uint32_t kvheads,
+                                           uint32_t head_dim, uint32_t nsink, uint32_t win);
+/* cache-append-ring (kernels.el:396-403) into fp16 ring caches: row b of src
+ * [batch x kvheads*head_dim] f32 (raw K or V) goes to the slot of stream
+ * position pos[b] (pos < nsink: slot pos; else nsink + (pos - nsink) mod
+ * win), rounded to nearest even; negative positions write nothing. */
+int nlg_cache_append_ring_f16(const float *src, const int32_t *pos, uint16_t *cache, uint32_t batch,
+                              uint32_t kvheads, uint32_t head_dim, uint32_t nsink, uint32_t win,
+                              void *stream);
+
 /* The first of those launches alone: per chunk of positions and head, the
  * chunk's max score, sum of exp and exp-weighted sum of V, left in
  * `workspace` for nlg_attn_ternary_linear_residual. */

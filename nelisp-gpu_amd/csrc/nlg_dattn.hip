@@ -6,8 +6,11 @@
 // Each workgroup of the first pass handles one (chunk, kv head, sequence)
 // for all the query heads of that kv head, so K and V are read from HBM once;
 // a second launch merges the chunks (max-rescaled sums).  The same chunk pass
-// serves contiguous caches [seq][kvheads][max_seq][hd] and paged pools
-// (decode-attn-paged-v, kernels.el:1222-1246) through a block table.
+// serves contiguous caches [seq][kvheads][max_seq][hd], paged pools
+// (decode-attn-paged-v, kernels.el:1222-1246) through a block table, and
+// StreamingLLM ring caches (decode-attn-stream, kernels.el:409-451): nsink
+// sink slots + a win-slot ring, keys and the query rotated by their
+// cache-relative positions.
 #include <math.h>
 
 #include "nlg_internal.h"
@@ -35,7 +38,18 @@ struct AttnArgs {
   // lens[b] (or pos[0] when lens is null); blocks >= npool read as zeros
   const int32_t *table, *lens;
   uint32_t bs, mbps, npool;
+  // ring caches (AM_RING): [B][kvheads][nsink + win][hd], sequence b at
+  // stream position pos[b]; co/si: [>= nsink + win][hd/2] rotation tables
+  const float *co, *si;
+  uint32_t nsink, win;
 };
+
+// how k_attn_part finds position p's K/V row
+enum { AM_CONTIG = 0, AM_PAGED = 1, AM_RING = 2 };
+
+__device__ __forceinline__ float f4_at(const float4 &v, int j) {
+  return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
+}
 
 // Sum over aligned groups of L lanes (L = 8 or 16); every lane gets its
 // group's sum.
@@ -68,8 +82,14 @@ uint32_t nlg_attn_chunk_count(uint32_t head_dim, uint32_t max_seq) { return attn
 // Lanes hold 8 dimensions of one position: LPP = HD/8 lanes per position,
 // PPI = 64/LPP positions per wave instruction.  Every K and V load of the
 // workgroup is issued before the first score is computed.
-template <int HD, int G, int NI, bool PG>
+//
+// In a ring cache (AM_RING) chunk positions are cache-relative ranks r:
+// rank r < nsink is sink slot r, later ranks walk the ring from its oldest
+// entry; K is rotated by r and q by the query's rank (CO/SI tables, pairs
+// (2m, 2m+1)) before the product, as decode-attn-stream does.
+template <int HD, int G, int NI, int MODE>
 __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
+  constexpr bool PG = MODE == AM_PAGED, RG = MODE == AM_RING;
   constexpr int LPP = HD / 8, PPI = 64 / LPP, PW = NI * PPI, NW = ATTN_WAVES, CS = NW * PW;
   __shared__ float s_m[NW][G], s_z[NW][G];
   __shared__ float s_ctx[NW][G][HD];
@@ -91,8 +111,32 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   const uint16_t *kb = a.kc + slot * a.max_seq * HD + d0;
   const uint16_t *vb = a.vc + slot * a.max_seq * HD + d0;
   uint4 kr[NI], vr[NI];
+  float4 rc[NI], rs[NI];  // ring: the ranks' rotation pairs (cos, sin)
   uint32_t pp[NI];
-  if (PG) {
+  uint32_t len = 0, qrank = 0;
+  if (RG) {
+    // the stream position first: it fixes the ring's oldest slot
+    const int32_t ps = a.pos[b];
+    const uint32_t pos = ps < 0 ? 0u : (uint32_t)ps, cap = a.max_seq;
+    len = pos + 1 < cap ? pos + 1 : cap;  // pos + 1 > 0: pos < 2^31
+    const uint32_t start = pos >= cap ? pos - a.win + 1 : a.nsink;
+    const uint32_t woff = (start - a.nsink) % a.win;
+    qrank = pos < cap ? pos : cap - 1;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      pp[i] = p0 + w * PW + i * PPI + grp;
+      const uint32_t pc = pp[i] < cap ? pp[i] : cap - 1;
+      uint32_t sl = pc;
+      if (pc >= a.nsink) {
+        const uint32_t t = woff + (pc - a.nsink);  // < 2 win
+        sl = a.nsink + (t >= a.win ? t - a.win : t);
+      }
+      kr[i] = *(const uint4 *)(kb + (size_t)sl * HD);
+      vr[i] = *(const uint4 *)(vb + (size_t)sl * HD);
+      rc[i] = *(const float4 *)(a.co + (size_t)pc * (HD / 2) + d0 / 2);
+      rs[i] = *(const float4 *)(a.si + (size_t)pc * (HD / 2) + d0 / 2);
+    }
+  } else if (PG) {
     // the block-table entry first, then K and V of that block's row
     const int32_t *trow = a.table + (size_t)b * a.mbps;
     int32_t ph[NI];
@@ -129,8 +173,22 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
     q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
     q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
   }
-  const int32_t pr = PG ? (a.lens ? a.lens[b] : a.pos[0]) : a.pos[0] + (a.qper ? (int32_t)(qr % a.qper) : 0);
-  const uint32_t len = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
+  if (RG) {  // q rotated by the query's rank
+    const float4 qc = *(const float4 *)(a.co + (size_t)qrank * (HD / 2) + d0 / 2);
+    const float4 qs = *(const float4 *)(a.si + (size_t)qrank * (HD / 2) + d0 / 2);
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float x0 = q[h][2 * j], x1 = q[h][2 * j + 1], c = f4_at(qc, j), sn = f4_at(qs, j);
+        q[h][2 * j] = x0 * c - x1 * sn;
+        q[h][2 * j + 1] = x0 * sn + x1 * c;
+      }
+    }
+  } else {
+    const int32_t pr = PG ? (a.lens ? a.lens[b] : a.pos[0]) : a.pos[0] + (a.qper ? (int32_t)(qr % a.qper) : 0);
+    len = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
+  }
   if (p0 >= len) {  // block-uniform: a chunk past the position adds nothing
     for (int i = threadIdx.x; i < G * HD; i += NW * 64) pctx[i] = 0.0f;
     if (threadIdx.x < G) {
@@ -142,11 +200,22 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   float s[NI][G];
 #pragma unroll
   for (int i = 0; i < NI; i++) {
+    float kf[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) kf[j] = f16x8_at(kr[i], j);
+    if (RG) {  // K rotated by its rank
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float k0 = kf[2 * j], k1 = kf[2 * j + 1], c = f4_at(rc[i], j), sn = f4_at(rs[i], j);
+        kf[2 * j] = k0 * c - k1 * sn;
+        kf[2 * j + 1] = k0 * sn + k1 * c;
+      }
+    }
 #pragma unroll
     for (int h = 0; h < G; h++) {
       float d = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; j++) d = fmaf(q[h][j], f16x8_at(kr[i], j), d);
+      for (int j = 0; j < 8; j++) d = fmaf(q[h][j], kf[j], d);
       d = group_sum<LPP>(d);
       s[i][h] = pp[i] < len ? d * a.coef : -INFINITY;
     }
@@ -283,6 +352,7 @@ static int attn_setup(AttnArgs &a, uint32_t batch, uint32_t heads, uint32_t kvhe
   a.heads = heads; a.kvheads = kvheads; a.max_seq = max_seq;
   a.coef = 1.0f / sqrtf((float)head_dim);  // (/ 1.0 (sqrt (float hd)))
   a.table = nullptr; a.lens = nullptr; a.bs = a.mbps = a.npool = 0;
+  a.co = a.si = nullptr; a.nsink = a.win = 0;
   return NLG_OK;
 }
 
@@ -290,7 +360,7 @@ static int attn_setup(AttnArgs &a, uint32_t batch, uint32_t heads, uint32_t kvhe
 // workgroup scores every query head of its kv head (K and V read once)
 // unless there are too few workgroups to spread over the CUs: then one head
 // each (K and V come from L2 for the others).
-static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, bool paged, hipStream_t st) {
+static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, int mode, hipStream_t st) {
   const uint32_t ni = attn_ni(head_dim, a.max_seq);
   const uint32_t G = (uint64_t)rows * a.kvheads * a.nchunk >= 128 ? a.grp : 1;
   const dim3 grid(a.nchunk, a.heads / G, rows), blk(ATTN_WAVES * 64);
@@ -301,8 +371,9 @@ static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, boo
   } while (0)
 #define AT(HD, GG)                                                                         \
   do {                                                                                     \
-    if (paged) AT1(HD, GG, true);                                                          \
-    else AT1(HD, GG, false);                                                               \
+    if (mode == AM_PAGED) AT1(HD, GG, AM_PAGED);                                           \
+    else if (mode == AM_RING) AT1(HD, GG, AM_RING);                                        \
+    else AT1(HD, GG, AM_CONTIG);                                                           \
   } while (0)
   if (head_dim == 128) {
     if (G == 1) AT(128, 1); else if (G == 2) AT(128, 2); else if (G == 4) AT(128, 4); else AT(128, 8);
@@ -311,7 +382,9 @@ static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, boo
   }
 #undef AT
 #undef AT1
-  NLG_LAUNCHED(paged ? "decode attention (paged fp16 KV)" : "decode attention (fp16 KV)");
+  NLG_LAUNCHED(mode == AM_PAGED  ? "decode attention (paged fp16 KV)"
+               : mode == AM_RING ? "decode attention (ring fp16 KV)"
+                                 : "decode attention (fp16 KV)");
   return NLG_OK;
 }
 
@@ -324,7 +397,7 @@ int nlg_attn_chunks(const float *q, const uint16_t *kcache, const uint16_t *vcac
   if (((uintptr_t)q & 15) || ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15))
     return nlg_fail("decode attn: q and caches must be 16-byte aligned");
   a.q = q; a.kc = kcache; a.vc = vcache; a.pos = pos; a.qper = qper; a.grp = heads / kvheads;
-  return attn_chunks_launch(a, rows, head_dim, false, st);
+  return attn_chunks_launch(a, rows, head_dim, AM_CONTIG, st);
 }
 
 extern "C" int nlg_decode_attn_f16_chunks(const float *q, const uint16_t *kcache, const uint16_t *vcache,
@@ -384,7 +457,7 @@ extern "C" int nlg_decode_attn_paged_f16(const float *q, const uint16_t *kpool, 
   a.q = q; a.kc = kpool; a.vc = vpool; a.pos = lens; a.qper = 0; a.grp = heads / kvheads;
   a.table = table; a.lens = lens; a.bs = bs; a.mbps = mbps; a.npool = npool;
   hipStream_t st = nlg_stream(stream);
-  if (attn_chunks_launch(a, batch, head_dim, true, st)) return NLG_ERR;
+  if (attn_chunks_launch(a, batch, head_dim, AM_PAGED, st)) return NLG_ERR;
   const uint64_t n = (uint64_t)batch * heads * head_dim;
   hipLaunchKernelGGL(k_attn_merge, dim3(nlg_blocks(n, 256)), dim3(256), 0, st, a.pctx, a.pmz, out, batch,
                      heads, head_dim, a.nchunk);
@@ -419,6 +492,75 @@ extern "C" int nlg_cache_append_paged_f16(const float *src, const int32_t *lens,
   hipLaunchKernelGGL(k_append_paged_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, nlg_stream(stream), src,
                      lens, table, npool, pool, batch, kvdim, bs, mbps);
   NLG_LAUNCHED("paged fp16 append");
+  return NLG_OK;
+}
+
+// StreamingLLM ring caches: decode-attn-stream (kernels.el:409-451) over
+// fp16 caches [batch][kvheads][nsink + win][head_dim], each sequence at its
+// own stream position pos[b]; the same chunk pass and merge as above.
+extern "C" size_t nlg_decode_attn_stream_f16_workspace(uint32_t batch, uint32_t heads, uint32_t kvheads,
+                                                      uint32_t head_dim, uint32_t nsink, uint32_t win) {
+  const uint64_t cap = (uint64_t)nsink + win;
+  if (!win || cap > 0x7fffffffull) return 0;
+  return nlg_decode_attn_f16_workspace(batch, heads, kvheads, head_dim, (uint32_t)cap);
+}
+
+extern "C" int nlg_decode_attn_stream_f16(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                                          const int32_t *pos, const float *co, const float *si, float *out,
+                                          uint32_t batch, uint32_t heads, uint32_t kvheads, uint32_t head_dim,
+                                          uint32_t nsink, uint32_t win, void *workspace, size_t workspace_bytes,
+                                          void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!batch) return NLG_OK;
+  if (!q || !kcache || !vcache || !pos || !co || !si || !out) return nlg_fail("stream attn: null pointer");
+  if (!win || (uint64_t)nsink + win > 0x7fffffffull)
+    return nlg_fail("stream attn: win must be nonzero and nsink + win < 2^31 (nsink %u, win %u)", nsink, win);
+  AttnArgs a;
+  if (attn_setup(a, batch, heads, kvheads, head_dim, nsink + win, workspace, workspace_bytes)) return NLG_ERR;
+  if (((uintptr_t)q & 15) || ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15) || ((uintptr_t)co & 15) ||
+      ((uintptr_t)si & 15))
+    return nlg_fail("stream attn: q, caches and rotation tables must be 16-byte aligned");
+  a.q = q; a.kc = kcache; a.vc = vcache; a.pos = pos; a.qper = 0; a.grp = heads / kvheads;
+  a.co = co; a.si = si; a.nsink = nsink; a.win = win;
+  hipStream_t st = nlg_stream(stream);
+  if (attn_chunks_launch(a, batch, head_dim, AM_RING, st)) return NLG_ERR;
+  const uint64_t n = (uint64_t)batch * heads * head_dim;
+  hipLaunchKernelGGL(k_attn_merge, dim3(nlg_blocks(n, 256)), dim3(256), 0, st, a.pctx, a.pmz, out, batch,
+                     heads, head_dim, a.nchunk);
+  NLG_LAUNCHED("ring decode attention merge");
+  return NLG_OK;
+}
+
+// Append B raw (un-rotated) rows of K or V into fp16 ring caches, row s at
+// the slot of stream position pos[s] (cache-append-ring, kernels.el:396-407:
+// slot = pos < nsink ? pos : nsink + (pos - nsink) mod win; fp16 round to
+// nearest even).  Negative positions write nothing.
+__global__ __launch_bounds__(256) void k_append_ring_f16(const float *src, const int32_t *pos, uint16_t *cache,
+                                                         uint32_t batch, uint32_t kvheads, uint32_t hd,
+                                                         uint32_t nsink, uint32_t win) {
+  const uint32_t kvdim = kvheads * hd;
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (uint64_t)batch * kvdim) return;
+  const uint32_t s = (uint32_t)(i / kvdim), t = (uint32_t)(i % kvdim);
+  const int32_t p = pos[s];
+  if (p < 0) return;
+  const uint32_t slot = (uint32_t)p < nsink ? (uint32_t)p : nsink + ((uint32_t)p - nsink) % win;
+  const size_t row = (size_t)s * kvheads + t / hd;
+  cache[(row * (nsink + win) + slot) * hd + t % hd] = __builtin_bit_cast(uint16_t, (_Float16)src[i]);
+}
+
+extern "C" int nlg_cache_append_ring_f16(const float *src, const int32_t *pos, uint16_t *cache, uint32_t batch,
+                                         uint32_t kvheads, uint32_t head_dim, uint32_t nsink, uint32_t win,
+                                         void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!batch || !kvheads || !head_dim) return NLG_OK;
+  if (!src || !pos || !cache) return nlg_fail("ring append: null pointer");
+  if (!win || (uint64_t)nsink + win > 0x7fffffffull)
+    return nlg_fail("ring append: win must be nonzero and nsink + win < 2^31 (nsink %u, win %u)", nsink, win);
+  const uint64_t n = (uint64_t)batch * kvheads * head_dim;
+  hipLaunchKernelGGL(k_append_ring_f16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, nlg_stream(stream), src,
+                     pos, cache, batch, kvheads, head_dim, nsink, win);
+  NLG_LAUNCHED("ring fp16 append");
   return NLG_OK;
 }
 

@@ -109,6 +109,10 @@ def lib() -> C.CDLL:
                                             vp]),
         "nlg_decode_attn_paged_f16_workspace": (sz, [u32, u32, u32, u32, u32, u32]),
         "nlg_cache_append_paged_f16": (i32, [vp, vp, vp, u32, vp, u32, u32, u32, u32, vp]),
+        "nlg_decode_attn_stream_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp, sz,
+                                             vp]),
+        "nlg_decode_attn_stream_f16_workspace": (sz, [u32, u32, u32, u32, u32, u32]),
+        "nlg_cache_append_ring_f16": (i32, [vp, vp, vp, u32, u32, u32, u32, u32, vp]),
         "nlg_repack_packed_to_2bit": (i32, [vp, u32, u32, u32, u32, vp, vp, vp]),
         "nlg_fill_normal": (i32, [vp, C.c_uint64, C.c_uint64, C.c_float, u32, vp]),
         "nlg_stack_create": (i32, [C.POINTER(StackConfig), C.POINTER(vp)]),
@@ -363,6 +367,23 @@ def decode_attn_paged_f16(q, kpool, vpool, lens, table, npool, out, batch, heads
 def cache_append_paged_f16(src, lens, table, npool, pool, batch, kvdim, bs, mbps, stream=None) -> None:
     _check(lib().nlg_cache_append_paged_f16(src.ptr, lens.ptr, table.ptr, npool, pool.ptr, batch, kvdim, bs, mbps,
                                             stream), "cache_append_paged_f16")
+
+
+def decode_attn_stream_f16_workspace(batch, heads, kvheads, head_dim, nsink, win) -> int:
+    return int(lib().nlg_decode_attn_stream_f16_workspace(batch, heads, kvheads, head_dim, nsink, win))
+
+
+def decode_attn_stream_f16(q, kc, vc, pos, co, si, out, batch, heads, kvheads, head_dim, nsink, win, workspace,
+                           stream=None) -> None:
+    """StreamingLLM decode attention over fp16 ring caches [batch][kvheads][nsink+win][head_dim]."""
+    _check(lib().nlg_decode_attn_stream_f16(q.ptr, kc.ptr, vc.ptr, pos.ptr, co.ptr, si.ptr, out.ptr, batch, heads,
+                                            kvheads, head_dim, nsink, win, workspace.ptr, workspace.nbytes, stream),
+           "decode_attn_stream_f16")
+
+
+def cache_append_ring_f16(src, pos, cache, batch, kvheads, head_dim, nsink, win, stream=None) -> None:
+    _check(lib().nlg_cache_append_ring_f16(src.ptr, pos.ptr, cache.ptr, batch, kvheads, head_dim, nsink, win,
+                                           stream), "cache_append_ring_f16")
 
 
 def repack_i8_to_2bit(wp, out, cols, w2, nbad=None, stream=None) -> None:

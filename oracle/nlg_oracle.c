@@ -1129,3 +1129,57 @@ void or_decode_attn_paged_f16(const float *q, const uint16_t *kp, const uint16_t
     out[idx] = ctx / z;
   }
 }
+
+/* decode-attn-stream (kernels.el:404-451) over fp16 ring caches
+ * [B][kvheads][nsink + win][hd], sequence s at stream position pos[s]
+ * (negative: 0): ranks r < len = min(pos + 1, cap) walk sink slots then the
+ * ring from its oldest slot; K is rotated by r and q by qcrel = min(pos,
+ * cap - 1) with the CO/SI tables, pairs (2m, 2m+1); per output element a
+ * serial q.k, mx seeded at -1e30, e = exp(s - mx), C = sum(e*v)/sum(e). */
+static float ring_dot(const float *qh, const uint16_t *kr, const float *co, const float *si, uint32_t r,
+                      uint32_t qcrel, uint32_t half) {
+  float acc = 0.0f;
+  for (uint32_t m = 0; m < half; m++) {
+    float cc = co[(size_t)r * half + m], ss = si[(size_t)r * half + m];
+    float k0 = f16_to_f32(kr[2 * m]), k1 = f16_to_f32(kr[2 * m + 1]);
+    float kr0 = (k0 * cc) - (k1 * ss), kr1 = (k0 * ss) + (k1 * cc);
+    float qcc = co[(size_t)qcrel * half + m], qss = si[(size_t)qcrel * half + m];
+    float q0 = qh[2 * m], q1 = qh[2 * m + 1];
+    float qr0 = (q0 * qcc) - (q1 * qss), qr1 = (q0 * qss) + (q1 * qcc);
+    acc = acc + ((qr0 * kr0) + (qr1 * kr1));
+  }
+  return acc;
+}
+void or_decode_attn_stream_f16(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *pos,
+                               const float *co, const float *si, float *out, uint32_t B, uint32_t heads,
+                               uint32_t kvheads, uint32_t hd, uint32_t nsink, uint32_t win) {
+  const uint32_t dim = heads * hd, grp = heads / kvheads, half = hd / 2, cap = nsink + win;
+  const float coef = 1.0f / sqrtf((float)hd);
+#pragma omp parallel for schedule(static)
+  for (int64_t idx = 0; idx < (int64_t)B * dim; idx++) {
+    uint32_t s = (uint32_t)(idx / dim), c = (uint32_t)(idx % dim);
+    uint32_t h = c / hd, t = c % hd, kvh = h / grp;
+    const float *qh = q + (size_t)s * dim + (size_t)h * hd;
+    const uint16_t *kb = kc + ((size_t)s * kvheads + kvh) * cap * hd;
+    const uint16_t *vb = vc + ((size_t)s * kvheads + kvh) * cap * hd;
+    uint32_t p = pos[s] < 0 ? 0u : (uint32_t)pos[s];
+    uint32_t len = p + 1 < cap ? p + 1 : cap;
+    uint32_t start = nsink;
+    if (p >= cap) start = (p - win) + 1;
+    uint32_t woff = (start - nsink) % win, qcrel = p < cap ? p : cap - 1;
+    float mx = NEG_BIG;
+    for (uint32_t r = 0; r < len; r++) {
+      uint32_t slot = r < nsink ? r : nsink + (woff + (r - nsink)) % win;
+      float sc = ring_dot(qh, kb + (size_t)slot * hd, co, si, r, qcrel, half) * coef;
+      if (sc > mx) mx = sc;
+    }
+    float z = 0.0f, ctx = 0.0f;
+    for (uint32_t r = 0; r < len; r++) {
+      uint32_t slot = r < nsink ? r : nsink + (woff + (r - nsink)) % win;
+      float e = expf(ring_dot(qh, kb + (size_t)slot * hd, co, si, r, qcrel, half) * coef - mx);
+      z = z + e;
+      ctx = ctx + e * f16_to_f32(vb[(size_t)slot * hd + t]);
+    }
+    out[idx] = ctx / z;
+  }
+}

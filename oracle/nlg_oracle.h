@@ -64,6 +64,13 @@ void or_decode_attn_paged_f16(const float *q, const uint16_t *kp, const uint16_t
                               const int32_t *table, uint32_t npool, float *out, uint32_t B, uint32_t heads,
                               uint32_t kvheads, uint32_t hd, uint32_t bs, uint32_t mbps);
 
+/* decode-attn-stream (kernels.el:404-451) over fp16 ring caches
+ * [B][kvheads][nsink + win][hd]; sequence s at stream position pos[s]
+ * (negative: 0); co/si: [>= nsink + win][hd/2] rotation tables. */
+void or_decode_attn_stream_f16(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *pos,
+                               const float *co, const float *si, float *out, uint32_t B, uint32_t heads,
+                               uint32_t kvheads, uint32_t hd, uint32_t nsink, uint32_t win);
+
 /* Weight ingest into the 2-bit layout of ternary-rows (kernels.el:700-746:
  * field f of word w = column 16w+f, bits 2f..2f+1, sign-extended).
  * From int8 lanes (bitlinear-dp4a-1f/-rows WP, kernels.el:619-653: lane l of

@@ -49,6 +49,8 @@ def lib() -> C.CDLL:
         L.or_decode_attn_f16.argtypes = [vp, vp, vp, u32, vp, u32, u32, u32, u32, u32]
         L.or_decode_attn_paged_f16.restype = None
         L.or_decode_attn_paged_f16.argtypes = [vp, vp, vp, vp, vp, u32, vp, u32, u32, u32, u32, u32, u32]
+        L.or_decode_attn_stream_f16.restype = None
+        L.or_decode_attn_stream_f16.argtypes = [vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32]
         L.or_repack_i8_2bit.restype = u32
         L.or_repack_i8_2bit.argtypes = [vp, u32, u32, vp]
         L.or_repack_packed_2bit.restype = u32
@@ -151,6 +153,29 @@ def decode_attn_paged_f16(q, kp, vp, lens, table, npool, B, heads, kvheads, hd, 
                                    _p(np.ascontiguousarray(table, np.int32)), npool, _p(out), B, heads, kvheads, hd,
                                    bs, mbps)
     return out
+
+
+def decode_attn_stream_f16(q, kc, vc, pos, co, si, B, heads, kvheads, hd, nsink, win) -> np.ndarray:
+    """kc, vc: uint16 fp16 ring caches [B][kvheads][nsink+win][hd]; pos int32 [B]; co, si f32 [>= cap][hd/2]."""
+    out = np.empty(B * heads * hd, np.float32)
+    lib().or_decode_attn_stream_f16(_p(np.ascontiguousarray(q, np.float32)), _p(np.ascontiguousarray(kc, np.uint16)),
+                                    _p(np.ascontiguousarray(vc, np.uint16)), _p(np.ascontiguousarray(pos, np.int32)),
+                                    _p(np.ascontiguousarray(co, np.float32)), _p(np.ascontiguousarray(si, np.float32)),
+                                    _p(out), B, heads, kvheads, hd, nsink, win)
+    return out
+
+
+def cache_append_ring_f16(cache, src, pos, B, kvheads, hd, nsink, win) -> None:
+    """cache-append-ring (kernels.el:396-403) into fp16 ring caches [B][kvheads][nsink+win][hd], in place:
+    row s of src [B x kvheads*hd] (rounded to fp16, nearest even) at the slot of pos[s]; negative pos skipped."""
+    cap = nsink + win
+    c = cache.reshape(B, kvheads, cap, hd)
+    for s in range(B):
+        p = int(pos[s])
+        if p < 0:
+            continue
+        slot = p if p < nsink else nsink + (p - nsink) % win
+        c[s, :, slot, :] = np.asarray(src, np.float32).reshape(B, kvheads, hd)[s].astype(np.float16).view(np.uint16)
 
 
 def repack_i8_2bit(wp, out, cols):

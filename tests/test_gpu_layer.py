@@ -305,6 +305,92 @@ def test_paged_f16_append():
     assert np.array_equal(got, want.ravel())
 
 
+def _rope_tables(rows, hd, theta=500000.0):
+    ang = np.outer(np.arange(rows), 1.0 / theta ** (np.arange(hd // 2) * 2.0 / hd))
+    return np.cos(ang).astype(f32), np.sin(ang).astype(f32)
+
+
+@pytest.mark.parametrize("B,heads,kvh,hd,nsink,win", [(1, 4, 2, 64, 2, 6), (3, 8, 1, 64, 0, 37),
+                                                      (4, 4, 4, 128, 4, 250), (2, 16, 2, 128, 4, 1020),
+                                                      (32, 20, 5, 128, 4, 508)])
+def test_ring_f16_attention(B, heads, kvh, hd, nsink, win):
+    """StreamingLLM decode attention over fp16 ring caches: sequences before
+    the ring fills, exactly at capacity and wrapped many times, against the
+    CPU restatement."""
+    print(f"[gpu] ring attention B={B} heads={heads}/{kvh} hd={hd} nsink={nsink} win={win}", flush=True)
+    cap = nsink + win
+    rng = np.random.default_rng(B * 7 + win)
+    kc = nlgpu.normal(B + 11, B * kvh * cap * hd).astype(np.float16).view(np.uint16)
+    vc = nlgpu.normal(B + 12, B * kvh * cap * hd).astype(np.float16).view(np.uint16)
+    pos = rng.integers(0, 5 * cap, B).astype(np.int32)
+    pos[0] = min(3, cap - 1)
+    if B > 1:
+        pos[1] = cap - 1
+    if B > 2:
+        pos[2] = cap
+    if B > 3:
+        pos[3] = 40 * cap + 7
+    co, si = _rope_tables(cap, hd)
+    q = (nlgpu.normal(B + 13, B * heads * hd) * f32(2.0)).astype(f32)
+    out = nlgpu.DeviceArray(B * heads * hd * 4)
+    ws = nlgpu.DeviceArray(nlgpu.decode_attn_stream_f16_workspace(B, heads, kvh, hd, nsink, win))
+    nlgpu.decode_attn_stream_f16(nlgpu.to_device(q), nlgpu.to_device(kc), nlgpu.to_device(vc), nlgpu.to_device(pos),
+                                 nlgpu.to_device(co), nlgpu.to_device(si), out, B, heads, kvh, hd, nsink, win, ws)
+    got = out.download(f32, B * heads * hd)
+    want = orc.decode_attn_stream_f16(q, kc, vc, pos, co, si, B, heads, kvh, hd, nsink, win)
+    err = np.abs(got - want).max() / np.abs(want).max()
+    print(f"  max err / max|out| = {err:.2e}", flush=True)
+    assert err <= 1e-4
+
+
+def test_ring_f16_append_then_attend_over_a_stream():
+    """Appends of raw K/V rows and attention, step by step past several ring
+    wraps (sequences at different stream positions, one idle at -1): the
+    caches stay bit-identical to the restatement's and every step's output
+    matches it."""
+    B, heads, kvh, hd, nsink, win = 3, 4, 2, 64, 2, 5
+    cap = nsink + win
+    print(f"[gpu] ring append + attention stream B={B} cap={cap}", flush=True)
+    kc = np.zeros(B * kvh * cap * hd, np.uint16)
+    vc = np.zeros_like(kc)
+    dkc, dvc = nlgpu.to_device(kc), nlgpu.to_device(vc)
+    co, si = _rope_tables(cap, hd)
+    dco, dsi = nlgpu.to_device(co), nlgpu.to_device(si)
+    ws = nlgpu.DeviceArray(nlgpu.decode_attn_stream_f16_workspace(B, heads, kvh, hd, nsink, win))
+    out = nlgpu.DeviceArray(B * heads * hd * 4)
+    start = np.array([0, 4, -1000], np.int32)
+    for step in range(24):
+        pos = start + step
+        pos[2] = -1 if step < 10 else step - 10
+        k = nlgpu.normal(100 + step, B * kvh * hd)
+        v = nlgpu.normal(200 + step, B * kvh * hd)
+        dpos = nlgpu.to_device(pos.astype(np.int32))
+        nlgpu.cache_append_ring_f16(nlgpu.to_device(k), dpos, dkc, B, kvh, hd, nsink, win)
+        nlgpu.cache_append_ring_f16(nlgpu.to_device(v), dpos, dvc, B, kvh, hd, nsink, win)
+        orc.cache_append_ring_f16(kc, k, pos, B, kvh, hd, nsink, win)
+        orc.cache_append_ring_f16(vc, v, pos, B, kvh, hd, nsink, win)
+        q = nlgpu.normal(300 + step, B * heads * hd)
+        nlgpu.decode_attn_stream_f16(nlgpu.to_device(q), dkc, dvc, dpos, dco, dsi, out, B, heads, kvh, hd, nsink,
+                                     win, ws)
+        assert np.array_equal(dkc.download(np.uint16, kc.size), kc), step
+        assert np.array_equal(dvc.download(np.uint16, vc.size), vc), step
+        got = out.download(f32, B * heads * hd)
+        want = orc.decode_attn_stream_f16(q, kc, vc, pos, co, si, B, heads, kvh, hd, nsink, win)
+        assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max(), step
+
+
+def test_ring_f16_rejects_bad_shapes():
+    d = nlgpu.DeviceArray(1 << 16)
+    pos = nlgpu.to_device(np.array([0], np.int32))
+    assert nlgpu.decode_attn_stream_f16_workspace(1, 4, 2, 64, 4, 0) == 0
+    with pytest.raises(nlgpu.NlgError, match="win"):
+        nlgpu.decode_attn_stream_f16(d, d, d, pos, d, d, d, 1, 4, 2, 64, 4, 0, d)
+    with pytest.raises(nlgpu.NlgError, match="win"):
+        nlgpu.cache_append_ring_f16(d, pos, d, 1, 2, 64, 4, 0)
+    with pytest.raises(nlgpu.NlgError, match="head_dim"):
+        nlgpu.decode_attn_stream_f16(d, d, d, pos, d, d, d, 1, 4, 2, 96, 4, 8, d)
+
+
 def test_prefill_attention_rejects_bad_shapes():
     d = nlgpu.DeviceArray(4096)
     pos = nlgpu.to_device(np.array([0], np.int32))

@@ -175,3 +175,103 @@ def test_paged_f16_attention_against_float64():
             e = np.exp(sc - sc.max())
             want = (e[:, None] * vv).sum(axis=0) / e.sum()
             assert np.abs(got[s, h] - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+
+
+def _ring_history(rng, B, kvh, hd, nsink, win, pos):
+    """Stream positions 0..pos[s] appended one by one into fp16 ring caches
+    with the reference's slot rule (later positions overwrite ring slots);
+    returns the caches and, per sequence, every appended raw K/V row."""
+    cap = nsink + win
+    kc = np.zeros(B * kvh * cap * hd, np.uint16)
+    vc = np.zeros_like(kc)
+    hist = []
+    for s in range(B):
+        ks = rng.standard_normal((int(pos[s]) + 1, kvh * hd)).astype(f32)
+        vs = rng.standard_normal((int(pos[s]) + 1, kvh * hd)).astype(f32)
+        for p in range(int(pos[s]) + 1):
+            pp = np.full(B, -1, np.int32)
+            pp[s] = p
+            orc.cache_append_ring_f16(kc, np.tile(ks[p], B), pp, B, kvh, hd, nsink, win)
+            orc.cache_append_ring_f16(vc, np.tile(vs[p], B), pp, B, kvh, hd, nsink, win)
+        hist.append((ks, vs))
+    return kc, vc, hist
+
+
+def test_ring_f16_attention_against_float64():
+    """or_decode_attn_stream_f16 (decode-attn-stream over fp16 ring caches)
+    against float64 attention over the positions a StreamingLLM cache keeps
+    (the nsink first ones and the last win), built from the append history
+    rather than from the ring-offset arithmetic; K rotated by its rank in that
+    list and q by min(pos, cap - 1), pairs (2m, 2m+1)."""
+    rng = np.random.default_rng(11)
+    for B, heads, kvh, hd, nsink, win, pos in ((3, 4, 2, 64, 2, 6, [3, 7, 20]), (2, 2, 1, 128, 0, 5, [12, 4]),
+                                               (2, 4, 1, 64, 4, 1, [2, 9])):
+        pos = np.array(pos, np.int32)
+        cap = nsink + win
+        kc, vc, hist = _ring_history(rng, B, kvh, hd, nsink, win, pos)
+        ang = np.outer(np.arange(cap), 1.0 / 10000.0 ** (np.arange(hd // 2) * 2.0 / hd))
+        co, si = np.cos(ang).astype(f32), np.sin(ang).astype(f32)
+        q = rng.standard_normal(B * heads * hd).astype(f32)
+        got = orc.decode_attn_stream_f16(q, kc, vc, pos, co, si, B, heads, kvh, hd, nsink,
+                                         win).reshape(B, heads, hd)
+        for s in range(B):
+            p = int(pos[s])
+            kept = list(range(p + 1)) if p < cap else list(range(nsink)) + list(range(p - win + 1, p + 1))
+            ks, vs = hist[s]
+            qr = min(p, cap - 1)
+            for h in range(heads):
+                kv = h // (heads // kvh)
+                qh = q.reshape(B, heads, hd)[s, h].astype(np.float64)
+                q0, q1 = qh[0::2], qh[1::2]
+                c, sn = co.astype(np.float64), si.astype(np.float64)
+                qrot0, qrot1 = q0 * c[qr] - q1 * sn[qr], q0 * sn[qr] + q1 * c[qr]
+                sc, vv = [], []
+                for r, ap in enumerate(kept):
+                    kk = ks[ap, kv * hd:(kv + 1) * hd].astype(np.float16).astype(np.float64)
+                    k0, k1 = kk[0::2], kk[1::2]
+                    kr0, kr1 = k0 * c[r] - k1 * sn[r], k0 * sn[r] + k1 * c[r]
+                    sc.append((qrot0 @ kr0 + qrot1 @ kr1) / np.sqrt(hd))
+                    vv.append(vs[ap, kv * hd:(kv + 1) * hd].astype(np.float16).astype(np.float64))
+                e = np.exp(np.array(sc) - max(sc))
+                want = (e @ np.array(vv)) / e.sum()
+                assert np.abs(got[s, h] - want).max() <= 1e-5 * max(1.0, np.abs(want).max()), (B, s, h, p)
+
+
+def test_ring_f16_attention_equals_the_dsl_restatement_bit_for_bit():
+    """At one sequence the fp16 ring restatement performs the DSL kernel's
+    operations in its order on the same (fp16-exact) values, so it matches
+    decode-attn-stream's restatement on the reference's f32 [cap][kvdim]
+    layout bit for bit, wrapped or not."""
+    rng = np.random.default_rng(12)
+    heads, kvh, hd, nsink, win = 4, 2, 64, 3, 5
+    cap, kvd = nsink + win, kvh * hd
+    co = rng.uniform(-1, 1, (cap, hd // 2)).astype(f32)
+    si = rng.uniform(-1, 1, (cap, hd // 2)).astype(f32)
+    for p in (0, 2, 6, 7, 8, 19):
+        kc16 = rng.standard_normal(kvh * cap * hd).astype(np.float16)
+        vc16 = rng.standard_normal(kvh * cap * hd).astype(np.float16)
+        q = rng.standard_normal(heads * hd).astype(f32)
+        got = orc.decode_attn_stream_f16(q, kc16.view(np.uint16), vc16.view(np.uint16), np.array([p], np.int32),
+                                         co, si, 1, heads, kvh, hd, nsink, win)
+        # the reference layout: slot-major rows of kvdim
+        kref = kc16.astype(f32).reshape(kvh, cap, hd).transpose(1, 0, 2).reshape(cap * kvd).copy()
+        vref = vc16.astype(f32).reshape(kvh, cap, hd).transpose(1, 0, 2).reshape(cap * kvd).copy()
+        out = np.zeros(heads * hd, f32)
+        orc.dispatch("decode-attn-stream", [q, kref, vref, np.array([p], f32), co.ravel(), si.ravel(), out],
+                     [heads * hd, heads, kvh, nsink, win], (heads * hd + 63) // 64)
+        assert np.array_equal(got.view(np.uint32), out.view(np.uint32)), p
+
+
+def test_ring_f16_identity_rotation_is_plain_decode_attention():
+    """With cos 1 and sin 0 and the ring not yet wrapped, ranks are positions
+    and slots: the ring attention is decode-attn over the same cache."""
+    rng = np.random.default_rng(13)
+    B, heads, kvh, hd, nsink, win, pos = 2, 4, 1, 64, 2, 14, 9
+    cap = nsink + win
+    kc = rng.standard_normal(B * kvh * cap * hd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(B * kvh * cap * hd).astype(np.float16).view(np.uint16)
+    q = rng.standard_normal(B * heads * hd).astype(f32)
+    one, zero = np.ones((cap, hd // 2), f32), np.zeros((cap, hd // 2), f32)
+    got = orc.decode_attn_stream_f16(q, kc, vc, np.full(B, pos, np.int32), one, zero, B, heads, kvh, hd, nsink, win)
+    want = orc.decode_attn_f16(q, kc, vc, pos, B, heads, kvh, hd, cap)
+    assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max()
