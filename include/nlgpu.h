@@ -295,6 +295,26 @@ size_t nlg_decode_attn_stream_f16_workspace(uint32_t batch, uint32_t heads, uint
 int nlg_cache_append_ring_f16(const float *src, const int32_t *pos, uint16_t *cache, uint32_t batch,
                               uint32_t kvheads, uint32_t head_dim, uint32_t nsink, uint32_t win,
                               void *stream);
+/* attn-stream-entries (kernels.el:1052-1090) over fp16 caches
+ * [batch][kvheads][nslots][head_dim]: sequence b attends the ne rows its
+ * entry list names, ent[b] = ne (slot, cache-relative rank) int32 pairs
+ * ([batch][ne][2], 8-byte aligned), K rotated by its rank and q by qrank[b]
+ * through co/si ([trows][head_dim/2]).  Slots outside [0, nslots) read as
+ * zero rows and ranks outside [0, trows) as zero rotations (the reference's
+ * robust reads).  Workspace from nlg_attn_entries_f16_workspace. */
+int nlg_attn_entries_f16(const float *q, const uint16_t *kcache, const uint16_t *vcache, const int32_t *ent,
+                         const int32_t *qrank, const float *co, const float *si, float *out, uint32_t batch,
+                         uint32_t heads, uint32_t kvheads, uint32_t head_dim, uint32_t nslots, uint32_t ne,
+                         uint32_t trows, void *workspace, size_t workspace_bytes, void *stream);
+size_t nlg_attn_entries_f16_workspace(uint32_t batch, uint32_t heads, uint32_t kvheads, uint32_t head_dim,
+                                      uint32_t ne);
+/* block-copy (kernels.el:1184-1193) on a K pool and a V pool of fp16 blocks
+ * [npool][bs][kvdim] at once (copy-on-write of shared prefix blocks): n
+ * copies in one launch, pairs[2i] -> pairs[2i+1]; pairs naming a block
+ * outside [0, npool) are skipped.  Copies of one call run concurrently: no
+ * destination may be another pair's source. */
+int nlg_block_copy_f16(uint16_t *kpool, uint16_t *vpool, const int32_t *pairs, uint32_t n, uint32_t npool,
+                       uint32_t bs, uint32_t kvdim, void *stream);
 
 /* The first of those launches alone: per chunk of positions and head, the
  * chunk's max score, sum of exp and exp-weighted sum of V, left in

@@ -42,10 +42,16 @@ struct AttnArgs {
   // stream position pos[b]; co/si: [>= nsink + win][hd/2] rotation tables
   const float *co, *si;
   uint32_t nsink, win;
+  // entry lists (AM_ENTRIES): sequence b attends ent[b][0..max_seq) = (slot,
+  // rank) int32 pairs over its cache [kvheads][nslots][hd]; the query's rank
+  // is lens[b]; slots outside [0, nslots) read as zero rows, ranks outside
+  // [0, trows) as zero rotations
+  const int32_t *ent;
+  uint32_t nslots, trows;
 };
 
 // how k_attn_part finds position p's K/V row
-enum { AM_CONTIG = 0, AM_PAGED = 1, AM_RING = 2 };
+enum { AM_CONTIG = 0, AM_PAGED = 1, AM_RING = 2, AM_ENTRIES = 3 };
 
 __device__ __forceinline__ float f4_at(const float4 &v, int j) {
   return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
@@ -86,10 +92,12 @@ uint32_t nlg_attn_chunk_count(uint32_t head_dim, uint32_t max_seq) { return attn
 // In a ring cache (AM_RING) chunk positions are cache-relative ranks r:
 // rank r < nsink is sink slot r, later ranks walk the ring from its oldest
 // entry; K is rotated by r and q by the query's rank (CO/SI tables, pairs
-// (2m, 2m+1)) before the product, as decode-attn-stream does.
+// (2m, 2m+1)) before the product, as decode-attn-stream does.  An entry
+// list (AM_ENTRIES, attn-stream-entries) names each attended row's slot and
+// rank explicitly; chunk positions index the list.
 template <int HD, int G, int NI, int MODE>
 __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
-  constexpr bool PG = MODE == AM_PAGED, RG = MODE == AM_RING;
+  constexpr bool PG = MODE == AM_PAGED, RG = MODE == AM_RING || MODE == AM_ENTRIES, EN = MODE == AM_ENTRIES;
   constexpr int LPP = HD / 8, PPI = 64 / LPP, PW = NI * PPI, NW = ATTN_WAVES, CS = NW * PW;
   __shared__ float s_m[NW][G], s_z[NW][G];
   __shared__ float s_ctx[NW][G][HD];
@@ -114,7 +122,35 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   float4 rc[NI], rs[NI];  // ring: the ranks' rotation pairs (cos, sin)
   uint32_t pp[NI];
   uint32_t len = 0, qrank = 0;
-  if (RG) {
+  if (EN) {
+    // the list entries first, then the rows and rotations they name
+    const int2 *eb = (const int2 *)(a.ent + (size_t)b * a.max_seq * 2);
+    const uint16_t *kbe = a.kc + slot * a.nslots * HD + d0, *vbe = a.vc + slot * a.nslots * HD + d0;
+    int2 ev[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      pp[i] = p0 + w * PW + i * PPI + grp;
+      ev[i] = eb[pp[i] < a.max_seq ? pp[i] : a.max_seq - 1];
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const bool sok = ev[i].x >= 0 && (uint32_t)ev[i].x < a.nslots;
+      const bool rok = ev[i].y >= 0 && (uint32_t)ev[i].y < a.trows;
+      const size_t sl = sok ? (uint32_t)ev[i].x : 0u, rk = rok ? (uint32_t)ev[i].y : 0u;
+      const uint4 k4 = *(const uint4 *)(kbe + sl * HD), v4 = *(const uint4 *)(vbe + sl * HD);
+      const float4 c4 = *(const float4 *)(a.co + rk * (HD / 2) + d0 / 2);
+      const float4 s4 = *(const float4 *)(a.si + rk * (HD / 2) + d0 / 2);
+      const uint4 z4 = make_uint4(0, 0, 0, 0);
+      const float4 f0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      kr[i] = sok ? k4 : z4;
+      vr[i] = sok ? v4 : z4;
+      rc[i] = rok ? c4 : f0;
+      rs[i] = rok ? s4 : f0;
+    }
+    len = a.max_seq;
+    const int32_t qk = a.lens[b];
+    qrank = qk >= 0 && (uint32_t)qk < a.trows ? (uint32_t)qk : a.trows;  // trows: a zero rotation
+  } else if (RG) {
     // the stream position first: it fixes the ring's oldest slot
     const int32_t ps = a.pos[b];
     const uint32_t pos = ps < 0 ? 0u : (uint32_t)ps, cap = a.max_seq;
@@ -174,8 +210,11 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
     q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
   }
   if (RG) {  // q rotated by the query's rank
-    const float4 qc = *(const float4 *)(a.co + (size_t)qrank * (HD / 2) + d0 / 2);
-    const float4 qs = *(const float4 *)(a.si + (size_t)qrank * (HD / 2) + d0 / 2);
+    const bool qok = !EN || qrank < a.trows;
+    const size_t qo = (size_t)(qok ? qrank : 0u) * (HD / 2) + d0 / 2;
+    const float4 f0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 qc = qok ? *(const float4 *)(a.co + qo) : f0;
+    const float4 qs = qok ? *(const float4 *)(a.si + qo) : f0;
 #pragma unroll
     for (int h = 0; h < G; h++) {
 #pragma unroll
@@ -353,6 +392,7 @@ static int attn_setup(AttnArgs &a, uint32_t batch, uint32_t heads, uint32_t kvhe
   a.coef = 1.0f / sqrtf((float)head_dim);  // (/ 1.0 (sqrt (float hd)))
   a.table = nullptr; a.lens = nullptr; a.bs = a.mbps = a.npool = 0;
   a.co = a.si = nullptr; a.nsink = a.win = 0;
+  a.ent = nullptr; a.nslots = a.trows = 0;
   return NLG_OK;
 }
 
@@ -373,6 +413,7 @@ static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, int
   do {                                                                                     \
     if (mode == AM_PAGED) AT1(HD, GG, AM_PAGED);                                           \
     else if (mode == AM_RING) AT1(HD, GG, AM_RING);                                        \
+    else if (mode == AM_ENTRIES) AT1(HD, GG, AM_ENTRIES);                                  \
     else AT1(HD, GG, AM_CONTIG);                                                           \
   } while (0)
   if (head_dim == 128) {
@@ -382,9 +423,10 @@ static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, int
   }
 #undef AT
 #undef AT1
-  NLG_LAUNCHED(mode == AM_PAGED  ? "decode attention (paged fp16 KV)"
-               : mode == AM_RING ? "decode attention (ring fp16 KV)"
-                                 : "decode attention (fp16 KV)");
+  NLG_LAUNCHED(mode == AM_PAGED     ? "decode attention (paged fp16 KV)"
+               : mode == AM_RING    ? "decode attention (ring fp16 KV)"
+               : mode == AM_ENTRIES ? "decode attention (fp16 KV entry list)"
+                                    : "decode attention (fp16 KV)");
   return NLG_OK;
 }
 
@@ -528,6 +570,81 @@ extern "C" int nlg_decode_attn_stream_f16(const float *q, const uint16_t *kcache
   hipLaunchKernelGGL(k_attn_merge, dim3(nlg_blocks(n, 256)), dim3(256), 0, st, a.pctx, a.pmz, out, batch,
                      heads, head_dim, a.nchunk);
   NLG_LAUNCHED("ring decode attention merge");
+  return NLG_OK;
+}
+
+// attn-stream-entries (kernels.el:1052-1090) over fp16 caches
+// [batch][kvheads][nslots][head_dim]: sequence b attends the ne rows its
+// entry list ent[b] names, (slot, cache-relative rank) int32 pairs, K rotated
+// by the rank and q by qrank[b]; tables co/si hold trows rows.
+extern "C" size_t nlg_attn_entries_f16_workspace(uint32_t batch, uint32_t heads, uint32_t kvheads,
+                                                 uint32_t head_dim, uint32_t ne) {
+  return nlg_decode_attn_f16_workspace(batch, heads, kvheads, head_dim, ne);
+}
+
+extern "C" int nlg_attn_entries_f16(const float *q, const uint16_t *kcache, const uint16_t *vcache,
+                                    const int32_t *ent, const int32_t *qrank, const float *co, const float *si,
+                                    float *out, uint32_t batch, uint32_t heads, uint32_t kvheads, uint32_t head_dim,
+                                    uint32_t nslots, uint32_t ne, uint32_t trows, void *workspace,
+                                    size_t workspace_bytes, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!batch) return NLG_OK;
+  if (!q || !kcache || !vcache || !ent || !qrank || !co || !si || !out) return nlg_fail("entries attn: null pointer");
+  if (!nslots || !ne || !trows) return nlg_fail("entries attn: nslots, ne and trows must be nonzero");
+  AttnArgs a;
+  if (attn_setup(a, batch, heads, kvheads, head_dim, ne, workspace, workspace_bytes)) return NLG_ERR;
+  if (((uintptr_t)q & 15) || ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15) || ((uintptr_t)co & 15) ||
+      ((uintptr_t)si & 15) || ((uintptr_t)ent & 7))
+    return nlg_fail("entries attn: q, caches and tables must be 16-byte aligned, ent 8-byte aligned");
+  a.q = q; a.kc = kcache; a.vc = vcache; a.pos = qrank; a.lens = qrank; a.qper = 0; a.grp = heads / kvheads;
+  a.co = co; a.si = si; a.ent = ent; a.nslots = nslots; a.trows = trows;
+  hipStream_t st = nlg_stream(stream);
+  if (attn_chunks_launch(a, batch, head_dim, AM_ENTRIES, st)) return NLG_ERR;
+  const uint64_t n = (uint64_t)batch * heads * head_dim;
+  hipLaunchKernelGGL(k_attn_merge, dim3(nlg_blocks(n, 256)), dim3(256), 0, st, a.pctx, a.pmz, out, batch,
+                     heads, head_dim, a.nchunk);
+  NLG_LAUNCHED("entry-list decode attention merge");
+  return NLG_OK;
+}
+
+// block-copy (kernels.el:1184-1193) for both fp16 pools at once, n copies in
+// one launch: pair i = (src block, dst block) of pairs[2i..2i+1]; pairs with
+// a block outside [0, npool) are skipped.  A workgroup copies one block of
+// bs * kvdim halves in 16-byte pieces when kvdim % 8 == 0, else halves.
+template <bool V16>
+__global__ __launch_bounds__(256) void k_block_copy_f16(uint16_t *kpool, uint16_t *vpool, const int32_t *pairs,
+                                                        uint32_t npool, uint32_t bn) {
+  const int32_t src = pairs[2 * blockIdx.x], dst = pairs[2 * blockIdx.x + 1];
+  if (src < 0 || dst < 0 || (uint32_t)src >= npool || (uint32_t)dst >= npool) return;
+  if (V16) {
+    const uint32_t n16 = bn / 8;
+    const uint4 *ks = (const uint4 *)(kpool + (size_t)src * bn), *vs = (const uint4 *)(vpool + (size_t)src * bn);
+    uint4 *kd = (uint4 *)(kpool + (size_t)dst * bn), *vd = (uint4 *)(vpool + (size_t)dst * bn);
+    for (uint32_t i = threadIdx.x; i < n16; i += 256) {
+      kd[i] = ks[i];
+      vd[i] = vs[i];
+    }
+  } else {
+    for (uint32_t i = threadIdx.x; i < bn; i += 256) {
+      kpool[(size_t)dst * bn + i] = kpool[(size_t)src * bn + i];
+      vpool[(size_t)dst * bn + i] = vpool[(size_t)src * bn + i];
+    }
+  }
+}
+
+extern "C" int nlg_block_copy_f16(uint16_t *kpool, uint16_t *vpool, const int32_t *pairs, uint32_t n,
+                                  uint32_t npool, uint32_t bs, uint32_t kvdim, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!n || !bs || !kvdim) return NLG_OK;
+  if (!kpool || !vpool || !pairs) return nlg_fail("block copy: null pointer");
+  if (n > 0x7fffffffu || (uint64_t)bs * kvdim > 0xffffffffull) return nlg_fail("block copy: too many copies or too large a block");
+  const uint32_t bn = bs * kvdim;
+  const bool v16 = kvdim % 8 == 0 && !((uintptr_t)kpool & 15) && !((uintptr_t)vpool & 15);
+  if (v16) hipLaunchKernelGGL(k_block_copy_f16<true>, dim3(n), dim3(256), 0, nlg_stream(stream), kpool, vpool, pairs,
+                              npool, bn);
+  else hipLaunchKernelGGL(k_block_copy_f16<false>, dim3(n), dim3(256), 0, nlg_stream(stream), kpool, vpool, pairs,
+                          npool, bn);
+  NLG_LAUNCHED("fp16 block copy");
   return NLG_OK;
 }
 

@@ -113,6 +113,10 @@ def lib() -> C.CDLL:
                                              vp]),
         "nlg_decode_attn_stream_f16_workspace": (sz, [u32, u32, u32, u32, u32, u32]),
         "nlg_cache_append_ring_f16": (i32, [vp, vp, vp, u32, u32, u32, u32, u32, vp]),
+        "nlg_attn_entries_f16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, vp, sz,
+                                       vp]),
+        "nlg_attn_entries_f16_workspace": (sz, [u32, u32, u32, u32, u32]),
+        "nlg_block_copy_f16": (i32, [vp, vp, vp, u32, u32, u32, u32, vp]),
         "nlg_repack_packed_to_2bit": (i32, [vp, u32, u32, u32, u32, vp, vp, vp]),
         "nlg_fill_normal": (i32, [vp, C.c_uint64, C.c_uint64, C.c_float, u32, vp]),
         "nlg_stack_create": (i32, [C.POINTER(StackConfig), C.POINTER(vp)]),
@@ -379,6 +383,22 @@ def decode_attn_stream_f16(q, kc, vc, pos, co, si, out, batch, heads, kvheads, h
     _check(lib().nlg_decode_attn_stream_f16(q.ptr, kc.ptr, vc.ptr, pos.ptr, co.ptr, si.ptr, out.ptr, batch, heads,
                                             kvheads, head_dim, nsink, win, workspace.ptr, workspace.nbytes, stream),
            "decode_attn_stream_f16")
+
+
+def attn_entries_f16_workspace(batch, heads, kvheads, head_dim, ne) -> int:
+    return int(lib().nlg_attn_entries_f16_workspace(batch, heads, kvheads, head_dim, ne))
+
+
+def attn_entries_f16(q, kc, vc, ent, qrank, co, si, out, batch, heads, kvheads, head_dim, nslots, ne, trows,
+                     workspace, stream=None) -> None:
+    """attn-stream-entries over fp16 caches [batch][kvheads][nslots][head_dim]; ent [batch][ne][2] int32."""
+    _check(lib().nlg_attn_entries_f16(q.ptr, kc.ptr, vc.ptr, ent.ptr, qrank.ptr, co.ptr, si.ptr, out.ptr, batch,
+                                      heads, kvheads, head_dim, nslots, ne, trows, workspace.ptr, workspace.nbytes,
+                                      stream), "attn_entries_f16")
+
+
+def block_copy_f16(kpool, vpool, pairs, n, npool, bs, kvdim, stream=None) -> None:
+    _check(lib().nlg_block_copy_f16(kpool.ptr, vpool.ptr, pairs.ptr, n, npool, bs, kvdim, stream), "block_copy_f16")
 
 
 def cache_append_ring_f16(src, pos, cache, batch, kvheads, head_dim, nsink, win, stream=None) -> None:

@@ -1183,3 +1183,57 @@ void or_decode_attn_stream_f16(const float *q, const uint16_t *kc, const uint16_
     out[idx] = ctx / z;
   }
 }
+
+/* attn-stream-entries (kernels.el:1052-1090) over fp16 caches
+ * [B][kvheads][nslots][hd]: sequence s attends the ne rows of its entry list
+ * ent[s] = (slot, rank) pairs, K rotated by the rank and q by qrank[s], in the
+ * DSL body's operation order.  A slot outside [0, nslots) reads as a zero row
+ * and a rank outside [0, trows) as a zero rotation (robust buffer access). */
+static float ent_dot(const float *qh, const uint16_t *kr, const float *co, const float *si, int32_t rank,
+                     int32_t qrank, uint32_t trows, uint32_t half) {
+  float acc = 0.0f;
+  int rok = rank >= 0 && (uint32_t)rank < trows, qok = qrank >= 0 && (uint32_t)qrank < trows;
+  for (uint32_t m = 0; m < half; m++) {
+    float cc = rok ? co[(size_t)rank * half + m] : 0.0f, ss = rok ? si[(size_t)rank * half + m] : 0.0f;
+    float k0 = kr ? f16_to_f32(kr[2 * m]) : 0.0f, k1 = kr ? f16_to_f32(kr[2 * m + 1]) : 0.0f;
+    float kr0 = (k0 * cc) - (k1 * ss), kr1 = (k0 * ss) + (k1 * cc);
+    float qcc = qok ? co[(size_t)qrank * half + m] : 0.0f, qss = qok ? si[(size_t)qrank * half + m] : 0.0f;
+    float q0 = qh[2 * m], q1 = qh[2 * m + 1];
+    float qr0 = (q0 * qcc) - (q1 * qss), qr1 = (q0 * qss) + (q1 * qcc);
+    acc = acc + ((qr0 * kr0) + (qr1 * kr1));
+  }
+  return acc;
+}
+void or_attn_entries_f16(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *ent,
+                         const int32_t *qrank, const float *co, const float *si, float *out, uint32_t B,
+                         uint32_t heads, uint32_t kvheads, uint32_t hd, uint32_t nslots, uint32_t ne,
+                         uint32_t trows) {
+  const uint32_t dim = heads * hd, grp = heads / kvheads, half = hd / 2;
+  const float coef = 1.0f / sqrtf((float)hd);
+#pragma omp parallel for schedule(static)
+  for (int64_t idx = 0; idx < (int64_t)B * dim; idx++) {
+    uint32_t s = (uint32_t)(idx / dim), c = (uint32_t)(idx % dim);
+    uint32_t h = c / hd, t = c % hd, kvh = h / grp;
+    const float *qh = q + (size_t)s * dim + (size_t)h * hd;
+    const uint16_t *kb = kc + ((size_t)s * kvheads + kvh) * nslots * hd;
+    const uint16_t *vb = vc + ((size_t)s * kvheads + kvh) * nslots * hd;
+    const int32_t *es = ent + (size_t)s * ne * 2;
+    float mx = NEG_BIG;
+    for (uint32_t r = 0; r < ne; r++) {
+      int32_t sl = es[2 * r];
+      const uint16_t *kr = sl >= 0 && (uint32_t)sl < nslots ? kb + (size_t)sl * hd : NULL;
+      float sc = ent_dot(qh, kr, co, si, es[2 * r + 1], qrank[s], trows, half) * coef;
+      if (sc > mx) mx = sc;
+    }
+    float z = 0.0f, ctx = 0.0f;
+    for (uint32_t r = 0; r < ne; r++) {
+      int32_t sl = es[2 * r];
+      int ok = sl >= 0 && (uint32_t)sl < nslots;
+      const uint16_t *kr = ok ? kb + (size_t)sl * hd : NULL;
+      float e = expf(ent_dot(qh, kr, co, si, es[2 * r + 1], qrank[s], trows, half) * coef - mx);
+      z = z + e;
+      ctx = ctx + e * (ok ? f16_to_f32(vb[(size_t)sl * hd + t]) : 0.0f);
+    }
+    out[idx] = ctx / z;
+  }
+}

@@ -70,6 +70,13 @@ void or_decode_attn_paged_f16(const float *q, const uint16_t *kp, const uint16_t
 void or_decode_attn_stream_f16(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *pos,
                                const float *co, const float *si, float *out, uint32_t B, uint32_t heads,
                                uint32_t kvheads, uint32_t hd, uint32_t nsink, uint32_t win);
+/* attn-stream-entries (kernels.el:1052-1090) over fp16 caches
+ * [B][kvheads][nslots][hd]; ent [B][ne][2] int32 (slot, rank); qrank [B];
+ * co/si [trows][hd/2]; bad slots read zero rows, bad ranks zero rotations. */
+void or_attn_entries_f16(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *ent,
+                         const int32_t *qrank, const float *co, const float *si, float *out, uint32_t B,
+                         uint32_t heads, uint32_t kvheads, uint32_t hd, uint32_t nslots, uint32_t ne,
+                         uint32_t trows);
 
 /* Weight ingest into the 2-bit layout of ternary-rows (kernels.el:700-746:
  * field f of word w = column 16w+f, bits 2f..2f+1, sign-extended).

@@ -51,6 +51,8 @@ def lib() -> C.CDLL:
         L.or_decode_attn_paged_f16.argtypes = [vp, vp, vp, vp, vp, u32, vp, u32, u32, u32, u32, u32, u32]
         L.or_decode_attn_stream_f16.restype = None
         L.or_decode_attn_stream_f16.argtypes = [vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32]
+        L.or_attn_entries_f16.restype = None
+        L.or_attn_entries_f16.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32]
         L.or_repack_i8_2bit.restype = u32
         L.or_repack_i8_2bit.argtypes = [vp, u32, u32, vp]
         L.or_repack_packed_2bit.restype = u32
@@ -163,6 +165,28 @@ def decode_attn_stream_f16(q, kc, vc, pos, co, si, B, heads, kvheads, hd, nsink,
                                     _p(np.ascontiguousarray(co, np.float32)), _p(np.ascontiguousarray(si, np.float32)),
                                     _p(out), B, heads, kvheads, hd, nsink, win)
     return out
+
+
+def attn_entries_f16(q, kc, vc, ent, qrank, co, si, B, heads, kvheads, hd, nslots, ne, trows) -> np.ndarray:
+    """kc, vc: uint16 fp16 caches [B][kvheads][nslots][hd]; ent int32 [B][ne][2] (slot, rank); qrank int32 [B];
+    co, si f32 [trows][hd/2]."""
+    out = np.empty(B * heads * hd, np.float32)
+    lib().or_attn_entries_f16(_p(np.ascontiguousarray(q, np.float32)), _p(np.ascontiguousarray(kc, np.uint16)),
+                              _p(np.ascontiguousarray(vc, np.uint16)), _p(np.ascontiguousarray(ent, np.int32)),
+                              _p(np.ascontiguousarray(qrank, np.int32)), _p(np.ascontiguousarray(co, np.float32)),
+                              _p(np.ascontiguousarray(si, np.float32)), _p(out), B, heads, kvheads, hd, nslots, ne,
+                              trows)
+    return out
+
+
+def block_copy_f16(kpool, vpool, pairs, npool, bs, kvdim) -> None:
+    """block-copy (kernels.el:1184-1193) on both fp16 pools [npool][bs*kvdim], in place, pairs (src, dst) in
+    order; pairs naming a block outside [0, npool) are skipped."""
+    kp, vp = kpool.reshape(npool, bs * kvdim), vpool.reshape(npool, bs * kvdim)
+    for src, dst in np.asarray(pairs, np.int64).reshape(-1, 2):
+        if 0 <= src < npool and 0 <= dst < npool:
+            kp[dst] = kp[src]
+            vp[dst] = vp[src]
 
 
 def cache_append_ring_f16(cache, src, pos, B, kvheads, hd, nsink, win) -> None:

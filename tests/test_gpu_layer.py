@@ -379,6 +379,55 @@ def test_ring_f16_append_then_attend_over_a_stream():
         assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max(), step
 
 
+@pytest.mark.parametrize("B,heads,kvh,hd,nslots,ne", [(1, 4, 2, 64, 12, 7), (3, 8, 1, 128, 300, 257),
+                                                      (32, 20, 5, 128, 640, 516)])
+def test_entries_f16_attention(B, heads, kvh, hd, nslots, ne):
+    """attn-stream-entries over fp16 caches: per-sequence entry lists with
+    repeated slots, a slot and a rank outside range (zero row, zero
+    rotation) and a query rank outside the tables, against the CPU
+    restatement."""
+    print(f"[gpu] entries attention B={B} heads={heads}/{kvh} hd={hd} nslots={nslots} ne={ne}", flush=True)
+    rng = np.random.default_rng(B * 5 + ne)
+    trows = nslots + 4
+    kc = nlgpu.normal(B + 21, B * kvh * nslots * hd).astype(np.float16).view(np.uint16)
+    vc = nlgpu.normal(B + 22, B * kvh * nslots * hd).astype(np.float16).view(np.uint16)
+    ent = np.stack([rng.integers(0, nslots, (B, ne)), rng.integers(0, trows, (B, ne))], axis=2).astype(np.int32)
+    ent[0, 0, 0] = nslots + 9
+    ent[B - 1, ne - 1, 1] = -3
+    qrank = rng.integers(0, trows, B).astype(np.int32)
+    if B > 2:
+        qrank[2] = trows + 100
+    co, si = _rope_tables(trows, hd)
+    q = (nlgpu.normal(B + 23, B * heads * hd) * f32(2.0)).astype(f32)
+    out = nlgpu.DeviceArray(B * heads * hd * 4)
+    ws = nlgpu.DeviceArray(nlgpu.attn_entries_f16_workspace(B, heads, kvh, hd, ne))
+    nlgpu.attn_entries_f16(nlgpu.to_device(q), nlgpu.to_device(kc), nlgpu.to_device(vc), nlgpu.to_device(ent),
+                           nlgpu.to_device(qrank), nlgpu.to_device(co), nlgpu.to_device(si), out, B, heads, kvh, hd,
+                           nslots, ne, trows, ws)
+    got = out.download(f32, B * heads * hd)
+    want = orc.attn_entries_f16(q, kc, vc, ent, qrank, co, si, B, heads, kvh, hd, nslots, ne, trows)
+    err = np.abs(got - want).max() / np.abs(want).max()
+    print(f"  max err / max|out| = {err:.2e}", flush=True)
+    assert err <= 1e-4
+
+
+@pytest.mark.parametrize("kvdim", [640, 36])
+def test_block_copy_f16(kvdim):
+    """block-copy on both fp16 pools at once: several copies in one launch
+    (16-byte and 2-byte paths), pairs naming blocks outside the pool skipped;
+    bit-exact against the restatement."""
+    npool, bs = 40, 16
+    print(f"[gpu] block copy kvdim={kvdim}", flush=True)
+    kp = nlgpu.normal(31, npool * bs * kvdim).astype(np.float16).view(np.uint16)
+    vp = nlgpu.normal(32, npool * bs * kvdim).astype(np.float16).view(np.uint16)
+    pairs = np.array([[3, 30], [5, 31], [7, 45], [-1, 2], [9, 0], [12, 13]], np.int32)
+    dk, dv = nlgpu.to_device(kp), nlgpu.to_device(vp)
+    nlgpu.block_copy_f16(dk, dv, nlgpu.to_device(pairs), len(pairs), npool, bs, kvdim)
+    orc.block_copy_f16(kp, vp, pairs, npool, bs, kvdim)
+    assert np.array_equal(dk.download(np.uint16, kp.size), kp)
+    assert np.array_equal(dv.download(np.uint16, vp.size), vp)
+
+
 def test_ring_f16_rejects_bad_shapes():
     d = nlgpu.DeviceArray(1 << 16)
     pos = nlgpu.to_device(np.array([0], np.int32))

@@ -275,3 +275,79 @@ def test_ring_f16_identity_rotation_is_plain_decode_attention():
     got = orc.decode_attn_stream_f16(q, kc, vc, np.full(B, pos, np.int32), one, zero, B, heads, kvh, hd, nsink, win)
     want = orc.decode_attn_f16(q, kc, vc, pos, B, heads, kvh, hd, cap)
     assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max()
+
+
+def test_entries_f16_attention_equals_the_dsl_restatement_bit_for_bit():
+    """or_attn_entries_f16 at one sequence performs attn-stream-entries'
+    operations in its order on the same (fp16-exact) values: bit for bit the
+    DSL restatement over the reference's f32 [nslots][kvdim] layout (entry
+    base = slot * kvdim)."""
+    rng = np.random.default_rng(14)
+    heads, kvh, hd, nslots, trows = 4, 2, 64, 12, 20
+    kvd = kvh * hd
+    co = rng.uniform(-1, 1, (trows, hd // 2)).astype(f32)
+    si = rng.uniform(-1, 1, (trows, hd // 2)).astype(f32)
+    for ne, qr in ((1, 0), (7, 9), (12, 19)):
+        kc16 = rng.standard_normal(kvh * nslots * hd).astype(np.float16)
+        vc16 = rng.standard_normal(kvh * nslots * hd).astype(np.float16)
+        ent = np.stack([rng.permutation(nslots)[:ne], rng.integers(0, trows, ne)], axis=1).astype(np.int32)
+        q = rng.standard_normal(heads * hd).astype(f32)
+        got = orc.attn_entries_f16(q, kc16.view(np.uint16), vc16.view(np.uint16), ent, np.array([qr], np.int32), co,
+                                   si, 1, heads, kvh, hd, nslots, ne, trows)
+        kref = kc16.astype(f32).reshape(kvh, nslots, hd).transpose(1, 0, 2).reshape(nslots * kvd).copy()
+        vref = vc16.astype(f32).reshape(kvh, nslots, hd).transpose(1, 0, 2).reshape(nslots * kvd).copy()
+        eref = np.stack([ent[:, 0] * kvd, ent[:, 1]], axis=1).astype(f32).ravel()
+        out = np.zeros(heads * hd, f32)
+        orc.dispatch("attn-stream-entries", [q, kref, vref, eref, co.ravel(), si.ravel(), out],
+                     [heads * hd, heads, kvh, ne, qr], (heads * hd + 63) // 64)
+        assert np.array_equal(got.view(np.uint32), out.view(np.uint32)), ne
+
+
+def test_entries_f16_from_the_ring_rule_is_the_ring_attention():
+    """An entry list spelling out the ring's (slot, rank) walk gives the ring
+    attention's bits; a slot outside the cache counts as a zero row (score 0,
+    V 0), checked against float64."""
+    rng = np.random.default_rng(15)
+    B, heads, kvh, hd, nsink, win = 2, 4, 2, 64, 3, 6
+    cap = nsink + win
+    kc = rng.standard_normal(B * kvh * cap * hd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(B * kvh * cap * hd).astype(np.float16).view(np.uint16)
+    co = rng.uniform(-1, 1, (cap, hd // 2)).astype(f32)
+    si = rng.uniform(-1, 1, (cap, hd // 2)).astype(f32)
+    q = rng.standard_normal(B * heads * hd).astype(f32)
+    pos = np.array([30, 30], np.int32)  # same stream position: entry lists of one length
+    start = pos[0] - win + 1
+    woff = (start - nsink) % win
+    slots = [r if r < nsink else nsink + (woff + r - nsink) % win for r in range(cap)]
+    ent = np.tile(np.stack([slots, np.arange(cap)], axis=1), (B, 1)).astype(np.int32)
+    qrank = np.full(B, cap - 1, np.int32)
+    got = orc.attn_entries_f16(q, kc, vc, ent, qrank, co, si, B, heads, kvh, hd, cap, cap, cap)
+    want = orc.decode_attn_stream_f16(q, kc, vc, pos, co, si, B, heads, kvh, hd, nsink, win)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # an out-of-range slot: a zero K row (score 0) and a zero V row
+    ent2 = ent.copy().reshape(B, cap, 2)
+    ent2[0, 4, 0] = 1000
+    got2 = orc.attn_entries_f16(q, kc, vc, ent2, qrank, co, si, B, heads, kvh, hd, cap, cap, cap).reshape(B, heads,
+                                                                                                        hd)
+    K = kc.view(np.float16).astype(np.float64).reshape(B, kvh, cap, hd)
+    V = vc.view(np.float16).astype(np.float64).reshape(B, kvh, cap, hd)
+    c, sn = co.astype(np.float64), si.astype(np.float64)
+    for h in range(heads):
+        kv = h // (heads // kvh)
+        qh = q.reshape(B, heads, hd)[0, h].astype(np.float64)
+        qr0 = qh[0::2] * c[cap - 1] - qh[1::2] * sn[cap - 1]
+        qr1 = qh[0::2] * sn[cap - 1] + qh[1::2] * c[cap - 1]
+        sc, vv = [], []
+        for r in range(cap):
+            sl, rk = ent2[0, r]
+            if sl >= cap:
+                sc.append(0.0)
+                vv.append(np.zeros(hd))
+                continue
+            k = K[0, kv, sl]
+            kr0, kr1 = k[0::2] * c[rk] - k[1::2] * sn[rk], k[0::2] * sn[rk] + k[1::2] * c[rk]
+            sc.append((qr0 @ kr0 + qr1 @ kr1) / np.sqrt(hd))
+            vv.append(V[0, kv, sl])
+        e = np.exp(np.array(sc) - max(sc))
+        w = (e @ np.array(vv)) / e.sum()
+        assert np.abs(got2[0, h] - w).max() <= 1e-5 * max(1.0, np.abs(w).max())
