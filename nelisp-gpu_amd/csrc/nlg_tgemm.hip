@@ -191,13 +191,37 @@ struct GemmArgs {
 
 // One output element of the batched linear (every lane calls it: the SwiGLU
 // and RoPE pairs are exchanged across lanes l, l^1, which hold rows 2j, 2j+1).
+// the epilogue operands of one (token, row), fetched before the main loop
+struct TgPre {
+  float res, cs, sn;
+  uint32_t p;
+  bool pos_ok;
+};
+
 template <int EPI>
-__device__ __forceinline__ void tg_store(const GemmArgs &a, int lane, uint32_t row, uint32_t tk, bool live,
-                                         float val) {
+__device__ __forceinline__ TgPre tg_prefetch(const GemmArgs &a, uint32_t rowc, uint32_t tk) {
+  TgPre r{0.0f, 0.0f, 0.0f, 0u, false};
+  const uint32_t tkc = tk < a.seq ? tk : a.seq - 1;
+  if (EPI == NLG_EPI_RESID) r.res = a.res[(size_t)tkc * a.rstride + rowc];
+  if (EPI == NLG_EPI_QKV) {
+    const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(tkc % a.qper) : 0);
+    r.pos_ok = pr >= 0 && (uint32_t)pr < a.max_seq;
+    r.p = r.pos_ok ? (uint32_t)pr : 0u;
+    const uint32_t sec = rowc < a.nq ? rowc : (rowc < a.nq + a.nkv ? rowc - a.nq : rowc - a.nq - a.nkv);
+    const uint32_t ci = r.p * (a.hd >> 1) + ((sec % a.hd) >> 1);
+    r.cs = a.co[ci];
+    r.sn = a.si[ci];
+  }
+  return r;
+}
+
+template <int EPI>
+__device__ __forceinline__ void tg_store_pre(const GemmArgs &a, int lane, uint32_t row, uint32_t tk, bool live,
+                                             float val, const TgPre &pre) {
   if (EPI == NLG_EPI_STORE || EPI == NLG_EPI_ARGMAX) {
     if (live) a.y[(size_t)tk * a.ystride + row] = val;
   } else if (EPI == NLG_EPI_RESID) {
-    if (live) a.y[(size_t)tk * a.ystride + row] = __fadd_rn(a.res[(size_t)tk * a.rstride + row], val);
+    if (live) a.y[(size_t)tk * a.ystride + row] = __fadd_rn(pre.res, val);
   } else if (EPI == NLG_EPI_SWIGLU || EPI == NLG_EPI_QKV) {
     const float pv = __int_as_float(nlg_dpp<0xB1>(__float_as_int(val)));  // row ^ 1
     if (EPI == NLG_EPI_SWIGLU) {
@@ -206,27 +230,30 @@ __device__ __forceinline__ void tg_store(const GemmArgs &a, int lane, uint32_t r
         a.y[(size_t)tk * a.ystride + (row >> 1)] = (val * sg) * pv;
       }
     } else if (live) {
-      const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(tk % a.qper) : 0);
-      const bool pos_ok = pr >= 0 && (uint32_t)pr < a.max_seq;
-      const uint32_t p = pos_ok ? (uint32_t)pr : 0u;
       const uint32_t sec = row < a.nq ? row : (row < a.nq + a.nkv ? row - a.nq : row - a.nq - a.nkv);
-      const uint32_t dd = sec % a.hd, half = a.hd >> 1, ci = p * half + (dd >> 1);
-      const float cs = a.co[ci], sn = a.si[ci];
+      const uint32_t dd = sec % a.hd;
       const bool odd = lane & 1;
       const float a0 = odd ? pv : val, a1 = odd ? val : pv;
-      const float rot = odd ? __fadd_rn(__fmul_rn(a0, sn), __fmul_rn(a1, cs))
-                            : __fsub_rn(__fmul_rn(a0, cs), __fmul_rn(a1, sn));
+      const float rot = odd ? __fadd_rn(__fmul_rn(a0, pre.sn), __fmul_rn(a1, pre.cs))
+                            : __fsub_rn(__fmul_rn(a0, pre.cs), __fmul_rn(a1, pre.sn));
       if (row < a.nq) {
         a.y[(size_t)tk * a.ystride + row] = rot;
-      } else if (pos_ok) {
+      } else if (pre.pos_ok) {
         const bool isk = row < a.nq + a.nkv;
         const uint32_t kh = sec / a.hd, sq = a.qper ? tk / a.qper : tk;
-        const size_t at = (((size_t)sq * a.kvheads + kh) * a.max_seq + p) * a.hd + dd;
+        const size_t at = (((size_t)sq * a.kvheads + kh) * a.max_seq + pre.p) * a.hd + dd;
         if (isk) a.kc[at] = __builtin_bit_cast(uint16_t, (_Float16)rot);
         else a.vc[at] = __builtin_bit_cast(uint16_t, (_Float16)val);
       }
     }
   }
+}
+
+// the same with the operands fetched here (row < out, tk < seq where live)
+template <int EPI>
+__device__ __forceinline__ void tg_store(const GemmArgs &a, int lane, uint32_t row, uint32_t tk, bool live,
+                                         float val) {
+  tg_store_pre<EPI>(a, lane, row, tk, live, val, tg_prefetch<EPI>(a, row < a.out ? row : a.out - 1, tk));
 }
 
 #define TG_KC 256                 // columns per chunk (16 2-bit words of a row)
@@ -370,21 +397,27 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
 
 // ------------------------------------------------------------ k_tgemm_k
 //
-// Few tokens and few output rows (batch-32 decode: 2560..3840 rows): the
-// 64-row workgroups of k_tgemm leave most CUs idle, so here a workgroup owns
-// 16 output rows x 16 MB tokens and its four waves split the columns: wave w
-// takes chunks w*per .. (w+1)*per - 1 (per = ceil(chunks / 4)) and loads its
-// operands straight from global memory into registers in matrix-core order
-// (no LDS stage, no barrier until the end), three chunks in flight in
-// register sets that rotate through a three-chunk unrolled loop; chunks past
-// its range load a valid chunk with the weights masked to zero.  The four
-// int32 partial sums meet in LDS (integer adds: exact in any order) and wave
-// w finishes accumulator register w of every token block.
+// Few tokens (decode batches): the 64-row workgroups of k_tgemm leave most
+// CUs idle, so here a workgroup owns 16 output rows x 16 MB tokens and its
+// four waves split the columns: wave w takes chunks w*per .. (w+1)*per - 1
+// (per = ceil(chunks / 4) <= PM) and loads its operands straight from global
+// memory into registers in matrix-core order (no LDS stage, no barrier
+// until the end).  A wave's weights are short (one 16-byte load per chunk),
+// so all PM of them are issued first, then the epilogue's operands (gamma,
+// bias, beta, the residual, the RoPE table entries): the kernel pays one HBM
+// round trip.  The activations (shared by every workgroup, so L2-resident)
+// run TK_D chunks ahead of the matrix cores.  Steps past the wave's range
+// load a valid chunk and mask its weights to zero.  The four int32 partial
+// sums meet in LDS (integer adds: exact in any order) and wave w finishes
+// accumulator register w of every token block.
 
-template <int MB, int EPI>
+#define TK_D 3  // activation chunks in flight
+
+template <int MB, int EPI, int PM>
 __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
   constexpr int NA = 4 * MB;  // 16-byte activation pieces per lane and chunk
-  typedef uint32_t kvec __attribute__((ext_vector_type(4 + 4 * NA)));
+  constexpr int D = PM < TK_D ? PM : TK_D;
+  typedef uint32_t avec __attribute__((ext_vector_type(4 * NA)));
   __shared__ v4i s_red[4][MB][64];
   asm volatile("" ::"s"(a.xq), "s"(a.gamma), "s"(a.w2), "s"(a.bias), "s"(a.beta), "s"(a.y), "s"(a.seq),
                "s"(a.out), "s"(a.cols), "s"(a.wng), "s"(a.ystride), "s"(a.beta_per_row));
@@ -396,7 +429,6 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
   const uint32_t nchunks = a.cols / TG_KC;
   const uint32_t per = (nchunks + 3) / 4, cb = w * per;
   const uint32_t ce = min(cb + per, nchunks);
-  const uint32_t nsteps = (per + 2) / 3 * 3;  // whole rotations
   const uint4 *wrow = (const uint4 *)(a.w2 + (size_t)rowc * a.wng) + lg;
   // token rows of this lane (A row i = lr of each 16-token block), at column 64 lg
   const uint8_t *xa[MB];
@@ -405,69 +437,81 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
     const uint32_t tk = tok0 + 16 * m + lr;
     xa[m] = a.xq + (size_t)(tk < a.seq ? tk : a.seq - 1) * a.cols + 64 * lg;
   }
-  // set layout: [0..3] the lane's 4 weight words (64 columns), then for each
-  // token block m and step t the 16 activation bytes of columns 64 lg + 16 t
-#define TK_LOAD(S, k)                                                                     \
+  // 1. the lane's 4 weight words (64 columns of its row) of every chunk
+  uint4 wq[PM];
+#pragma unroll
+  for (int j = 0; j < PM; j++) {
+    const uint32_t c = cb + j;
+    wq[j] = wrow[4 * (c < ce ? c : nchunks - 1)];
+  }
+  // 2. the first D chunks' activations: for each token block m and step t the
+  //    16 bytes of columns 64 lg + 16 t
+  avec av[PM];
+#define TK_LOADA(k)                                                                       \
   do {                                                                                    \
     const uint32_t c = cb + (k);                                                          \
     const uint32_t cc = c < ce ? c : nchunks - 1;                                         \
-    const uint32_t keep = c < ce ? 0xffffffffu : 0u;                                      \
-    const uint4 u = wrow[4 * cc];                                                         \
-    S[0] = u.x & keep; S[1] = u.y & keep; S[2] = u.z & keep; S[3] = u.w & keep;            \
     _Pragma("unroll") for (int m = 0; m < MB; m++) {                                      \
       _Pragma("unroll") for (int t = 0; t < 4; t++) {                                     \
         const uint4 v = *(const uint4 *)(xa[m] + (size_t)cc * TG_KC + 16 * t);             \
-        S[4 + 16 * m + 4 * t] = v.x; S[5 + 16 * m + 4 * t] = v.y;                         \
-        S[6 + 16 * m + 4 * t] = v.z; S[7 + 16 * m + 4 * t] = v.w;                         \
+        av[k][16 * m + 4 * t] = v.x; av[k][16 * m + 4 * t + 1] = v.y;                     \
+        av[k][16 * m + 4 * t + 2] = v.z; av[k][16 * m + 4 * t + 3] = v.w;                 \
       }                                                                                   \
     }                                                                                     \
   } while (0)
-#define TK_MMA(S)                                                                         \
-  do {                                                                                    \
-    _Pragma("unroll") for (int t = 0; t < 4; t++) {                                       \
-      const uint32_t wd = S[t];                                                           \
-      const v4i bop = {(int)((wd << 6) & 0xC0C0C0C0u), (int)((wd << 4) & 0xC0C0C0C0u),    \
-                       (int)((wd << 2) & 0xC0C0C0C0u), (int)(wd & 0xC0C0C0C0u)};           \
-      _Pragma("unroll") for (int m = 0; m < MB; m++) {                                    \
-        const v4i aop = {(int)S[4 + 16 * m + 4 * t], (int)S[5 + 16 * m + 4 * t],          \
-                         (int)S[6 + 16 * m + 4 * t], (int)S[7 + 16 * m + 4 * t]};         \
-        acc[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop, acc[m], 0, 0, 0);       \
-      }                                                                                   \
-    }                                                                                     \
-  } while (0)
+#pragma unroll
+  for (int k = 0; k < D; k++) TK_LOADA(k);
+  // 3. the epilogue's operands: wave w finishes token tok0 + 16 m + 4 lg + w
+  const float bo_raw = (a.bias ? a.bias : a.beta)[a.bias ? rowc : 0];
+  const float be = a.beta[a.beta_per_row ? rowc : 0];
+  float gm[MB];
+  TgPre pre[MB];
+#pragma unroll
+  for (int m = 0; m < MB; m++) {
+    const uint32_t tk = tok0 + 16 * m + 4 * lg + w;
+    gm[m] = a.gamma[tk < a.seq ? tk : a.seq - 1];
+    pre[m] = tg_prefetch<EPI>(a, rowc, tk);
+  }
+  // keep every load above issued here: the scheduler would otherwise sink
+  // weight loads into the loop (to save registers) and pay HBM latency there
+  __builtin_amdgcn_sched_barrier(0);
+  // 4. the matrix-core steps, activations D chunks ahead
   v4i acc[MB];
 #pragma unroll
   for (int m = 0; m < MB; m++) acc[m] = (v4i){0, 0, 0, 0};
-  kvec sA, sB, sC;
-  TK_LOAD(sA, 0);
-  TK_LOAD(sB, 1);
-  for (uint32_t k = 0; k < nsteps; k += 3) {
-    TK_LOAD(sC, k + 2);
-    TK_MMA(sA);
-    TK_LOAD(sA, k + 3);
-    TK_MMA(sB);
-    TK_LOAD(sB, k + 4);
-    TK_MMA(sC);
+#pragma unroll
+  for (int k = 0; k < PM; k++) {
+    if (k + D < PM) TK_LOADA(k + D);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t keep = cb + k < ce ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const uint32_t wd = (t == 0 ? wq[k].x : t == 1 ? wq[k].y : t == 2 ? wq[k].z : wq[k].w) & keep;
+      const v4i bop = {(int)((wd << 6) & 0xC0C0C0C0u), (int)((wd << 4) & 0xC0C0C0C0u),
+                       (int)((wd << 2) & 0xC0C0C0C0u), (int)(wd & 0xC0C0C0C0u)};
+#pragma unroll
+      for (int m = 0; m < MB; m++) {
+        const v4i aop = {(int)av[k][16 * m + 4 * t], (int)av[k][16 * m + 4 * t + 1],
+                         (int)av[k][16 * m + 4 * t + 2], (int)av[k][16 * m + 4 * t + 3]};
+        acc[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop, acc[m], 0, 0, 0);
+      }
+    }
   }
-#undef TK_LOAD
-#undef TK_MMA
+#undef TK_LOADA
 #pragma unroll
   for (int m = 0; m < MB; m++) s_red[w][m][lane] = acc[m];
   __syncthreads();
   // wave w: register r = w of each token block (token tok0 + 16 m + 4 lg + w)
   const bool rlive = row < a.out;
-  const float bo_raw = (a.bias ? a.bias : a.beta)[a.bias ? rowc : 0];
-  const float be = a.beta[a.beta_per_row ? rowc : 0];
   const float bo = a.bias ? bo_raw : 0.0f;
 #pragma unroll
   for (int m = 0; m < MB; m++) {
     const int32_t q = s_red[0][m][lane][w] + s_red[1][m][lane][w] + s_red[2][m][lane][w] + s_red[3][m][lane][w];
     const uint32_t tk = tok0 + 16 * m + 4 * lg + w;
     const bool live = rlive && tk < a.seq;
-    const float gm = a.gamma[tk < a.seq ? tk : a.seq - 1];
     // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
-    const float val = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, gm), (float)(q >> 6)));
-    tg_store<EPI>(a, lane, row, tk, live, val);
+    const float val = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, gm[m]), (float)(q >> 6)));
+    tg_store_pre<EPI>(a, lane, row, tk, live, val, pre[m]);
   }
 }
 
@@ -724,10 +768,21 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
     // gain, 13,824 rows lose to the extra activation reads)
     const dim3 grid(nlg_blocks(a.out, 16), (a.seq + MT - 1) / MT), blk(256);
     if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
+    // weight chunks per wave: the smallest instantiated count >= ceil(chunks / 4)
+    const uint32_t per = (a.cols / TG_KC + 3) / 4;
+    const int pm = per <= 2 ? 2 : per <= 3 ? 3 : per <= 4 ? 4 : per <= 7 ? 7 : 16;
+#define TKP(M, E)                                                                         \
+  do {                                                                                    \
+    if (pm == 2) hipLaunchKernelGGL((k_tgemm_k<M, E, 2>), grid, blk, 0, st, a);           \
+    else if (pm == 3) hipLaunchKernelGGL((k_tgemm_k<M, E, 3>), grid, blk, 0, st, a);      \
+    else if (pm == 4) hipLaunchKernelGGL((k_tgemm_k<M, E, 4>), grid, blk, 0, st, a);      \
+    else if (pm == 7) hipLaunchKernelGGL((k_tgemm_k<M, E, 7>), grid, blk, 0, st, a);      \
+    else hipLaunchKernelGGL((k_tgemm_k<M, E, 16>), grid, blk, 0, st, a);                  \
+  } while (0)
 #define TKG(E)                                                                            \
   do {                                                                                    \
-    if (MB == 1) hipLaunchKernelGGL((k_tgemm_k<1, E>), grid, blk, 0, st, a);              \
-    else hipLaunchKernelGGL((k_tgemm_k<2, E>), grid, blk, 0, st, a);                      \
+    if (MB == 1) TKP(1, E);                                                               \
+    else TKP(2, E);                                                                       \
   } while (0)
     switch (epi) {
       case NLG_EPI_STORE: TKG(NLG_EPI_STORE); break;
@@ -737,6 +792,7 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
       default: return nlg_fail("ternary GEMM: unknown epilogue %d", epi);
     }
 #undef TKG
+#undef TKP
     NLG_LAUNCHED("ternary GEMM (int8 MFMA, split columns)");
     return NLG_OK;
   }
