@@ -661,7 +661,7 @@ def main():
                      "kernel": "k_tern_fused", "bytes_per_launch": STEP_BYTES,
                      "us_per_launch": round(r["step_ms"] * 1e3, 3)},
         "gemv_prequantised": {"gbs": round(gemv_gbs, 2), "us_per_launch": round(r["gemv_ms"] * 1e3, 3),
-                              "bytes_per_launch": GEMV_BYTES, "kernel": "k_tern_i8_fast"},
+                              "bytes_per_launch": GEMV_BYTES, "kernel": "k_tern_i8_dec"},
         "gemv_stacked_one_launch": {"gbs": round(stacked_gbs, 2), "frac": round(stacked_gbs / HBM_PEAK_GBS, 4),
                                     "rows": OUT * COPIES, "ms": round(r["stacked_ms"], 4)},
         "launch_floor_us": round(r["floor_ms"] * 1e3, 3),

@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
 #pragma unroll
     for (int i = 0; i < CPL; i++) {
       const uint32_t c = lane + 64 * i;
-      wv[r][i] = wr[c < nchunk ? c : nchunk - 1];
+      wv[r][i] = nlg_ld_stream(&wr[c < nchunk ? c : nchunk - 1]);
     }
   }
   const uint32_t orow_u = row0 + (lane < R ? lane : 0);

@@ -216,7 +216,7 @@ __global__ __launch_bounds__(256) void k_tern_i8_fast(TernArgs a) {
     const bool valid = true;
     uint4 wv[R];
 #pragma unroll
-    for (int r = 0; r < R; r++) wv[r] = wrow[r][c];
+    for (int r = 0; r < R; r++) wv[r] = nlg_ld_stream(&wrow[r][c]);
 #pragma unroll
     for (int s = 0; s < ST; s++) {
       const uint32_t tok = s0 + s;
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(256) void k_tern_i8_dec(TernArgs a) {
 #pragma unroll
     for (int i = 0; i < CPL; i++) {
       const uint32_t c = lane + 64u * i;
-      wv[r][i] = wr[c < nchunk ? c : nchunk - 1];
+      wv[r][i] = nlg_ld_stream(&wr[c < nchunk ? c : nchunk - 1]);
     }
   }
   const uint32_t orow_u = row0 + (lane < R ? lane : 0);

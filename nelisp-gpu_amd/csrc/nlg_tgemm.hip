@@ -442,7 +442,7 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
 #pragma unroll
   for (int j = 0; j < PM; j++) {
     const uint32_t c = cb + j;
-    wq[j] = wrow[4 * (c < ce ? c : nchunks - 1)];
+    wq[j] = nlg_ld_stream(&wrow[4 * (c < ce ? c : nchunks - 1)]);
   }
   // 2. the first D chunks' activations: for each token block m and step t the
   //    16 bytes of columns 64 lg + 16 t
