@@ -50,8 +50,16 @@ struct AttnArgs {
   uint32_t nslots, trows;
 };
 
-// how k_attn_part finds position p's K/V row
-enum { AM_CONTIG = 0, AM_PAGED = 1, AM_RING = 2, AM_ENTRIES = 3 };
+// how k_attn_part finds position p's K/V row (AM_CONTIG_NT: contiguous, read
+// with non-temporal loads)
+enum { AM_CONTIG = 0, AM_PAGED = 1, AM_RING = 2, AM_ENTRIES = 3, AM_CONTIG_NT = 4 };
+
+// A launch whose caches hold this many bytes of K and V streams them with
+// non-temporal loads: a decode step's layers then need more than the 256 MB
+// MALL, which cannot keep them from one step to the next anyway (measured at
+// the config-5 shape: B=32, 63 MB per layer, 13.9k -> 14.4k tok/s), while
+// smaller caches (B=1: 2 MB per layer) are left to be served from it.
+#define ATTN_NT_BYTES (16ull << 20)
 
 __device__ __forceinline__ float f4_at(const float4 &v, int j) {
   return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
@@ -197,8 +205,13 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
     for (int i = 0; i < NI; i++) {
       pp[i] = p0 + w * PW + i * PPI + grp;
       const uint32_t pc = pp[i] < a.max_seq ? pp[i] : a.max_seq - 1;
-      kr[i] = *(const uint4 *)(kb + (size_t)pc * HD);
-      vr[i] = *(const uint4 *)(vb + (size_t)pc * HD);
+      if (MODE == AM_CONTIG_NT) {
+        kr[i] = nlg_ld_stream((const uint4 *)(kb + (size_t)pc * HD));
+        vr[i] = nlg_ld_stream((const uint4 *)(vb + (size_t)pc * HD));
+      } else {
+        kr[i] = *(const uint4 *)(kb + (size_t)pc * HD);
+        vr[i] = *(const uint4 *)(vb + (size_t)pc * HD);
+      }
     }
   }
   const float *qb = a.q + (size_t)qr * a.heads * HD + (size_t)h0 * HD + d0;
@@ -403,6 +416,8 @@ static int attn_setup(AttnArgs &a, uint32_t batch, uint32_t heads, uint32_t kvhe
 static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, int mode, hipStream_t st) {
   const uint32_t ni = attn_ni(head_dim, a.max_seq);
   const uint32_t G = (uint64_t)rows * a.kvheads * a.nchunk >= 128 ? a.grp : 1;
+  const uint64_t seqs = a.qper ? (rows + a.qper - 1) / a.qper : rows;
+  const bool nt = mode == AM_CONTIG && seqs * a.kvheads * a.max_seq * head_dim * 4 >= ATTN_NT_BYTES;
   const dim3 grid(a.nchunk, a.heads / G, rows), blk(ATTN_WAVES * 64);
 #define AT1(HD, GG, PGV)                                                                   \
   do {                                                                                     \
@@ -414,6 +429,7 @@ static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, int
     if (mode == AM_PAGED) AT1(HD, GG, AM_PAGED);                                           \
     else if (mode == AM_RING) AT1(HD, GG, AM_RING);                                        \
     else if (mode == AM_ENTRIES) AT1(HD, GG, AM_ENTRIES);                                  \
+    else if (nt) AT1(HD, GG, AM_CONTIG_NT);                                                \
     else AT1(HD, GG, AM_CONTIG);                                                           \
   } while (0)
   if (head_dim == 128) {

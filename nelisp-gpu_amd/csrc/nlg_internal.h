@@ -111,6 +111,18 @@ __device__ __forceinline__ uint4 nlg_ld_stream(const uint4 *p) {
   return make_uint4(t.x, t.y, t.z, t.w);
 }
 
+// The same for rows read and written once (softmax in place: 5.49 -> 6.03 TB/s).
+__device__ __forceinline__ float4 nlg_ld_stream_f4(const float4 *p) {
+  typedef float v4f __attribute__((ext_vector_type(4)));
+  const v4f t = __builtin_nontemporal_load((const v4f *)p);
+  return make_float4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ void nlg_st_stream_f4(float4 *p, float4 v) {
+  typedef float v4f __attribute__((ext_vector_type(4)));
+  const v4f t = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(t, (v4f *)p);
+}
+
 __device__ __forceinline__ float nlg_wave_max_f32(float v) {
   // rotations keep every lane valid, so no identity is needed for them
   v = nlg_fmax_nn(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0xB1, 0xf, 0xf, false)));

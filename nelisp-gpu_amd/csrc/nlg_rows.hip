@@ -3,9 +3,9 @@
 // The reference gives each row to one invocation, which walks it serially
 // three times (softmax, kernels.el:28-42).  Here a workgroup owns a row: the
 // row is read from HBM once into registers (16 floats per thread at 4096
-// columns, float4 loads), reduced with DPP within waves and LDS across them,
-// and written once -- 8 bytes of traffic per element, the minimum for an
-// in-place softmax.  Reduction order differs from the serial reference, so
+// columns, non-temporal float4 loads), reduced with DPP within waves and LDS
+// across them, and written once (non-temporal stores) -- 8 bytes of traffic
+// per element, the minimum for an in-place softmax.  Reduction order differs from the serial reference, so
 // parity is by tolerance (<= 1e-5 relative for softmax, 1e-4 for RMSNorm).
 #include <math.h>
 
@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void k_softmax_reg(const float *a, float *c, u
     for (int k = 0; k < EPT / 4; k++) {
       const uint32_t i4 = threadIdx.x + 256u * k;
       float4 q = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-      if (4 * i4 < n) q = ((const float4 *)ar)[i4];
+      if (4 * i4 < n) q = nlg_ld_stream_f4((const float4 *)ar + i4);
       v[4 * k] = q.x; v[4 * k + 1] = q.y; v[4 * k + 2] = q.z; v[4 * k + 3] = q.w;
     }
   } else {
@@ -58,7 +58,8 @@ __global__ __launch_bounds__(256) void k_softmax_reg(const float *a, float *c, u
     for (int k = 0; k < EPT / 4; k++) {
       const uint32_t i4 = threadIdx.x + 256u * k;
       if (4 * i4 < n)
-        ((float4 *)cr)[i4] = make_float4(v[4 * k] / s, v[4 * k + 1] / s, v[4 * k + 2] / s, v[4 * k + 3] / s);
+        nlg_st_stream_f4((float4 *)cr + i4,
+                         make_float4(v[4 * k] / s, v[4 * k + 1] / s, v[4 * k + 2] / s, v[4 * k + 3] / s));
     }
   } else {
 #pragma unroll
