@@ -50,11 +50,17 @@ struct AttnArgs {
   uint32_t nslots, trows;
 };
 
-// how k_attn_part finds position p's K/V row (AM_CONTIG_NT: contiguous, read
-// with non-temporal loads)
-enum { AM_CONTIG = 0, AM_PAGED = 1, AM_RING = 2, AM_ENTRIES = 3, AM_CONTIG_NT = 4 };
+// how k_attn_part finds position p's K/V row; AM_NT added to a mode: K and V
+// read with non-temporal loads
+enum { AM_CONTIG = 0, AM_PAGED = 1, AM_RING = 2, AM_ENTRIES = 3, AM_NT = 8 };
 
-// A launch whose caches hold this many bytes of K and V streams them with
+// K/V row loads, plain or non-temporal
+template <bool NT>
+__device__ __forceinline__ uint4 kv_ld(const uint16_t *p) {
+  return NT ? nlg_ld_stream((const uint4 *)p) : *(const uint4 *)p;
+}
+
+// A launch that attends this many bytes of K and V streams them with
 // non-temporal loads: a decode step's layers then need more than the 256 MB
 // MALL, which cannot keep them from one step to the next anyway (measured at
 // the config-5 shape: B=32, 63 MB per layer, 13.9k -> 14.4k tok/s), while
@@ -105,7 +111,9 @@ uint32_t nlg_attn_chunk_count(uint32_t head_dim, uint32_t max_seq) { return attn
 // rank explicitly; chunk positions index the list.
 template <int HD, int G, int NI, int MODE>
 __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
-  constexpr bool PG = MODE == AM_PAGED, RG = MODE == AM_RING || MODE == AM_ENTRIES, EN = MODE == AM_ENTRIES;
+  constexpr int BM = MODE & ~AM_NT;
+  constexpr bool NT = (MODE & AM_NT) != 0;
+  constexpr bool PG = BM == AM_PAGED, RG = BM == AM_RING || BM == AM_ENTRIES, EN = BM == AM_ENTRIES;
   constexpr int LPP = HD / 8, PPI = 64 / LPP, PW = NI * PPI, NW = ATTN_WAVES, CS = NW * PW;
   __shared__ float s_m[NW][G], s_z[NW][G];
   __shared__ float s_ctx[NW][G][HD];
@@ -145,7 +153,7 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
       const bool sok = ev[i].x >= 0 && (uint32_t)ev[i].x < a.nslots;
       const bool rok = ev[i].y >= 0 && (uint32_t)ev[i].y < a.trows;
       const size_t sl = sok ? (uint32_t)ev[i].x : 0u, rk = rok ? (uint32_t)ev[i].y : 0u;
-      const uint4 k4 = *(const uint4 *)(kbe + sl * HD), v4 = *(const uint4 *)(vbe + sl * HD);
+      const uint4 k4 = kv_ld<NT>(kbe + sl * HD), v4 = kv_ld<NT>(vbe + sl * HD);
       const float4 c4 = *(const float4 *)(a.co + rk * (HD / 2) + d0 / 2);
       const float4 s4 = *(const float4 *)(a.si + rk * (HD / 2) + d0 / 2);
       const uint4 z4 = make_uint4(0, 0, 0, 0);
@@ -175,8 +183,8 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
         const uint32_t t = woff + (pc - a.nsink);  // < 2 win
         sl = a.nsink + (t >= a.win ? t - a.win : t);
       }
-      kr[i] = *(const uint4 *)(kb + (size_t)sl * HD);
-      vr[i] = *(const uint4 *)(vb + (size_t)sl * HD);
+      kr[i] = kv_ld<NT>(kb + (size_t)sl * HD);
+      vr[i] = kv_ld<NT>(vb + (size_t)sl * HD);
       rc[i] = *(const float4 *)(a.co + (size_t)pc * (HD / 2) + d0 / 2);
       rs[i] = *(const float4 *)(a.si + (size_t)pc * (HD / 2) + d0 / 2);
     }
@@ -195,7 +203,7 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
       const uint32_t pc = pp[i] < a.max_seq ? pp[i] : a.max_seq - 1;
       const bool ok = ph[i] >= 0 && (uint32_t)ph[i] < a.npool;
       const size_t row = (((size_t)(ok ? ph[i] : 0) * a.bs + pc % a.bs) * a.kvheads + kvh) * HD + d0;
-      const uint4 k4 = *(const uint4 *)(a.kc + row), v4 = *(const uint4 *)(a.vc + row);
+      const uint4 k4 = kv_ld<NT>(a.kc + row), v4 = kv_ld<NT>(a.vc + row);
       const uint4 z4 = make_uint4(0, 0, 0, 0);
       kr[i] = ok ? k4 : z4;
       vr[i] = ok ? v4 : z4;
@@ -205,13 +213,8 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
     for (int i = 0; i < NI; i++) {
       pp[i] = p0 + w * PW + i * PPI + grp;
       const uint32_t pc = pp[i] < a.max_seq ? pp[i] : a.max_seq - 1;
-      if (MODE == AM_CONTIG_NT) {
-        kr[i] = nlg_ld_stream((const uint4 *)(kb + (size_t)pc * HD));
-        vr[i] = nlg_ld_stream((const uint4 *)(vb + (size_t)pc * HD));
-      } else {
-        kr[i] = *(const uint4 *)(kb + (size_t)pc * HD);
-        vr[i] = *(const uint4 *)(vb + (size_t)pc * HD);
-      }
+      kr[i] = kv_ld<NT>(kb + (size_t)pc * HD);
+      vr[i] = kv_ld<NT>(vb + (size_t)pc * HD);
     }
   }
   const float *qb = a.q + (size_t)qr * a.heads * HD + (size_t)h0 * HD + d0;
@@ -416,8 +419,11 @@ static int attn_setup(AttnArgs &a, uint32_t batch, uint32_t heads, uint32_t kvhe
 static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, int mode, hipStream_t st) {
   const uint32_t ni = attn_ni(head_dim, a.max_seq);
   const uint32_t G = (uint64_t)rows * a.kvheads * a.nchunk >= 128 ? a.grp : 1;
+  // positions attended per sequence at most: the cache (contiguous, ring) or
+  // its block table's reach (paged); entry lists stay on plain loads
   const uint64_t seqs = a.qper ? (rows + a.qper - 1) / a.qper : rows;
-  const bool nt = mode == AM_CONTIG && seqs * a.kvheads * a.max_seq * head_dim * 4 >= ATTN_NT_BYTES;
+  if (mode != AM_ENTRIES && seqs * a.kvheads * a.max_seq * head_dim * 4 >= ATTN_NT_BYTES) mode |= AM_NT;
+  constexpr int AM_CONTIG_NT_ = AM_CONTIG | AM_NT;
   const dim3 grid(a.nchunk, a.heads / G, rows), blk(ATTN_WAVES * 64);
 #define AT1(HD, GG, PGV)                                                                   \
   do {                                                                                     \
@@ -427,9 +433,11 @@ static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, int
 #define AT(HD, GG)                                                                         \
   do {                                                                                     \
     if (mode == AM_PAGED) AT1(HD, GG, AM_PAGED);                                           \
+    else if (mode == (AM_PAGED | AM_NT)) AT1(HD, GG, AM_PAGED | AM_NT);                    \
     else if (mode == AM_RING) AT1(HD, GG, AM_RING);                                        \
+    else if (mode == (AM_RING | AM_NT)) AT1(HD, GG, AM_RING | AM_NT);                      \
     else if (mode == AM_ENTRIES) AT1(HD, GG, AM_ENTRIES);                                  \
-    else if (nt) AT1(HD, GG, AM_CONTIG_NT);                                                \
+    else if (mode == AM_CONTIG_NT_) AT1(HD, GG, AM_CONTIG | AM_NT);                        \
     else AT1(HD, GG, AM_CONTIG);                                                           \
   } while (0)
   if (head_dim == 128) {
@@ -439,10 +447,11 @@ static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, int
   }
 #undef AT
 #undef AT1
-  NLG_LAUNCHED(mode == AM_PAGED     ? "decode attention (paged fp16 KV)"
-               : mode == AM_RING    ? "decode attention (ring fp16 KV)"
-               : mode == AM_ENTRIES ? "decode attention (fp16 KV entry list)"
-                                    : "decode attention (fp16 KV)");
+  const int bm = mode & ~AM_NT;
+  NLG_LAUNCHED(bm == AM_PAGED     ? "decode attention (paged fp16 KV)"
+               : bm == AM_RING    ? "decode attention (ring fp16 KV)"
+               : bm == AM_ENTRIES ? "decode attention (fp16 KV entry list)"
+                                  : "decode attention (fp16 KV)");
   return NLG_OK;
 }
 

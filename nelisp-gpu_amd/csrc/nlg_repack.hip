@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void k_repack_i8(const uint32_t *wp, uint32_t 
   const uint32_t *row = wp + (size_t)o * ng;
   uint32_t lw[4];
   if (VEC) {
-    const uint4 u = *(const uint4 *)(row + 4 * wi);
+    const uint4 u = nlg_ld_stream((const uint4 *)(row + 4 * wi));  // read once, written once
     lw[0] = u.x; lw[1] = u.y; lw[2] = u.z; lw[3] = u.w;
   } else {
 #pragma unroll
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) void k_repack_i8(const uint32_t *wp, uint32_t 
       }
     }
   }
-  w2[idx] = word;
+  __builtin_nontemporal_store(word, &w2[idx]);
   if (nbad && bad) atomicAdd(nbad, bad);
 }
 
