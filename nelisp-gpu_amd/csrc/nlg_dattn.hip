@@ -134,6 +134,17 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   const size_t slot = (size_t)b * a.kvheads + kvh;
   const uint16_t *kb = a.kc + slot * a.max_seq * HD + d0;
   const uint16_t *vb = a.vc + slot * a.max_seq * HD + d0;
+  // q first: loads retire in issue order, so the first score then waits
+  // only for its own K row, and the scores overlap the rest of the stream
+  const float *qb = a.q + (size_t)qr * a.heads * HD + (size_t)h0 * HD + d0;
+  float q[G][8];
+#pragma unroll
+  for (int h = 0; h < G; h++) {
+    const float4 q0 = *(const float4 *)(qb + h * HD), q1 = *(const float4 *)(qb + h * HD + 4);
+    q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
+    q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
+  }
+  __builtin_amdgcn_sched_barrier(0);
   uint4 kr[NI], vr[NI];
   float4 rc[NI], rs[NI];  // ring: the ranks' rotation pairs (cos, sin)
   uint32_t pp[NI];
@@ -216,14 +227,6 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
       kr[i] = kv_ld<NT>(kb + (size_t)pc * HD);
       vr[i] = kv_ld<NT>(vb + (size_t)pc * HD);
     }
-  }
-  const float *qb = a.q + (size_t)qr * a.heads * HD + (size_t)h0 * HD + d0;
-  float q[G][8];
-#pragma unroll
-  for (int h = 0; h < G; h++) {
-    const float4 q0 = *(const float4 *)(qb + h * HD), q1 = *(const float4 *)(qb + h * HD + 4);
-    q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
-    q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
   }
   if (RG) {  // q rotated by the query's rank
     const bool qok = !EN || qrank < a.trows;
