@@ -316,9 +316,10 @@ size_t nlg_attn_entries_f16_workspace(uint32_t batch, uint32_t heads, uint32_t k
 int nlg_block_copy_f16(uint16_t *kpool, uint16_t *vpool, const int32_t *pairs, uint32_t n, uint32_t npool,
                        uint32_t bs, uint32_t kvdim, void *stream);
 
-/* The first of those launches alone: per chunk of positions and head, the
- * chunk's max score, sum of exp and exp-weighted sum of V, left in
- * `workspace` for nlg_attn_ternary_linear_residual. */
+/* The first of nlg_decode_attn_f16's two launches alone: per chunk of
+ * positions and head, the chunk's maximum score m (in base 2: q.k/sqrt(hd)
+ * times log2 e), its sum of 2^(s - m) and the matching weighted sum of V,
+ * left in `workspace` for nlg_attn_ternary_linear_residual. */
 int nlg_decode_attn_f16_chunks(const float *q, const uint16_t *kcache, const uint16_t *vcache,
                                const int32_t *pos, uint32_t batch, uint32_t heads, uint32_t kvheads,
                                uint32_t head_dim, uint32_t max_seq, void *workspace,

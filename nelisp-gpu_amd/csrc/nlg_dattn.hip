@@ -32,7 +32,7 @@ struct AttnArgs {
   uint32_t heads, kvheads, max_seq, nchunk;
   uint32_t qper;            // 0: row z = sequence z at pos[0]; else sequence z/qper at pos[0] + z%qper
   uint32_t grp;             // query heads per kv head (a workgroup takes G <= grp of them)
-  float coef;               // 1/sqrt(hd)
+  float coef;               // log2(e)/sqrt(hd): scores in base 2
   // paged caches (PG): pools [block][bs][kvheads][hd]; sequence b's position p
   // lives in block table[b*mbps + p/bs] at offset p%bs; its own position is
   // lens[b] (or pos[0] when lens is null); blocks >= npool read as zeros
@@ -127,9 +127,10 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   float *pctx = a.pctx + cb * a.heads * HD + (size_t)h0 * HD;
   float *pmz = a.pmz + (cb * a.heads + h0) * 2;
   const uint32_t p0 = c * CS;
-  // K, V and q are fetched before the position arrives (addresses clamped
-  // to the cache, not to the position), so the position's fetch is not a
-  // round trip ahead of theirs; positions past it are masked afterwards.
+  // For small caches K, V and q are fetched before the position arrives
+  // (addresses clamped to the cache, not to the position), so the position's
+  // fetch is not a round trip ahead of theirs; positions past it are masked
+  // afterwards.
   const int d0 = 8 * (lane % LPP), grp = lane / LPP;
   const size_t slot = (size_t)b * a.kvheads + kvh;
   const uint16_t *kb = a.kc + slot * a.max_seq * HD + d0;
@@ -149,6 +150,15 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   float4 rc[NI], rs[NI];  // ring: the ranks' rotation pairs (cos, sin)
   uint32_t pp[NI];
   uint32_t len = 0, qrank = 0;
+  // Rows fetched: positions clamp to lim - 1.  Large caches (NT) read the
+  // position first so that rows past it are never fetched (their addresses
+  // clamp to the last attended row, a cache hit): bytes over latency.  Small
+  // ones fetch the whole chunk while the position is in flight.
+  uint32_t lim = a.max_seq;
+  if (NT && !RG) {
+    const int32_t pr = PG ? (a.lens ? a.lens[b] : a.pos[0]) : a.pos[0] + (a.qper ? (int32_t)(qr % a.qper) : 0);
+    lim = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
+  }
   if (EN) {
     // the list entries first, then the rows and rotations they name
     const int2 *eb = (const int2 *)(a.ent + (size_t)b * a.max_seq * 2);
@@ -206,12 +216,12 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < NI; i++) {
       pp[i] = p0 + w * PW + i * PPI + grp;
-      const uint32_t pc = pp[i] < a.max_seq ? pp[i] : a.max_seq - 1;
+      const uint32_t pc = pp[i] < lim ? pp[i] : lim - 1;
       ph[i] = trow[pc / a.bs];
     }
 #pragma unroll
     for (int i = 0; i < NI; i++) {
-      const uint32_t pc = pp[i] < a.max_seq ? pp[i] : a.max_seq - 1;
+      const uint32_t pc = pp[i] < lim ? pp[i] : lim - 1;
       const bool ok = ph[i] >= 0 && (uint32_t)ph[i] < a.npool;
       const size_t row = (((size_t)(ok ? ph[i] : 0) * a.bs + pc % a.bs) * a.kvheads + kvh) * HD + d0;
       const uint4 k4 = kv_ld<NT>(a.kc + row), v4 = kv_ld<NT>(a.vc + row);
@@ -223,7 +233,7 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < NI; i++) {
       pp[i] = p0 + w * PW + i * PPI + grp;
-      const uint32_t pc = pp[i] < a.max_seq ? pp[i] : a.max_seq - 1;
+      const uint32_t pc = pp[i] < lim ? pp[i] : lim - 1;
       kr[i] = kv_ld<NT>(kb + (size_t)pc * HD);
       vr[i] = kv_ld<NT>(vb + (size_t)pc * HD);
     }
@@ -275,7 +285,7 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; j++) d = fmaf(q[h][j], kf[j], d);
       d = group_sum<LPP>(d);
-      s[i][h] = pp[i] < len ? d * a.coef : -INFINITY;
+      s[i][h] = pp[i] < len ? d * a.coef : -INFINITY;  // (q.k / sqrt(hd)) * log2(e)
     }
   }
   float m[G], z[G], ctx[G][8];
@@ -297,7 +307,7 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   for (int i = 0; i < NI; i++) {
 #pragma unroll
     for (int h = 0; h < G; h++) {
-      const float e = expf(s[i][h] - m[h]);
+      const float e = nlg_exp2(s[i][h] - m[h]);
       z[h] = z[h] + e;
 #pragma unroll
       for (int j = 0; j < 8; j++) ctx[h][j] = fmaf(e, f16x8_at(vr[i], j), ctx[h][j]);
@@ -328,7 +338,7 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
     float zz = 0.0f, cx = 0.0f;
 #pragma unroll
     for (int k = 0; k < NW; k++) {
-      const float sc = expf(s_m[k][h] - mm);
+      const float sc = nlg_exp2(s_m[k][h] - mm);
       zz = fmaf(s_z[k][h], sc, zz);
       cx = fmaf(s_ctx[k][h][d], sc, cx);
     }
@@ -377,7 +387,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ pc
     }
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-      const float sc = c0 + k < nchunk ? expf(v[k].x - mm) : 0.0f;
+      const float sc = c0 + k < nchunk ? nlg_exp2(v[k].x - mm) : 0.0f;
       zz = fmaf(v[k].y, sc, zz);
       acc = fmaf(x[k], sc, acc);
     }
@@ -408,7 +418,7 @@ static int attn_setup(AttnArgs &a, uint32_t batch, uint32_t heads, uint32_t kvhe
   a.pctx = (float *)workspace;
   a.pmz = (float *)((char *)workspace + (ctx + 255) / 256 * 256);
   a.heads = heads; a.kvheads = kvheads; a.max_seq = max_seq;
-  a.coef = 1.0f / sqrtf((float)head_dim);  // (/ 1.0 (sqrt (float hd)))
+  a.coef = (1.0f / sqrtf((float)head_dim)) * NLG_LOG2E;  // (/ 1.0 (sqrt (float hd))), in base 2
   a.table = nullptr; a.lens = nullptr; a.bs = a.mbps = a.npool = 0;
   a.co = a.si = nullptr; a.nsink = a.win = 0;
   a.ent = nullptr; a.nslots = a.trows = 0;

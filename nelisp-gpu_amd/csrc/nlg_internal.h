@@ -101,6 +101,12 @@ __device__ __forceinline__ float nlg_wave_sum_f32(float v) {
 // what masked lanes compare against.
 __device__ __forceinline__ float nlg_fmax_nn(float a, float b) { return b > a ? b : a; }
 
+// The split decode attention keeps its scores in base 2: s * log2(e), so
+// that every exponential is one v_exp_f32 (exp(s - m) = 2^(s2 - m2)); the
+// chunk maxima it leaves for the merges are in the same units.
+#define NLG_LOG2E 1.4426950408889634f
+__device__ __forceinline__ float nlg_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // A 16-byte load of data streamed once per launch (2-bit weights): marked
 // non-temporal (glc slc), so it neither allocates in the caches nor evicts
 // the activations and KV rows later kernels re-read.  Measured: the 4096^2

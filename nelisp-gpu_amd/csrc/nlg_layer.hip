@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
       float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
       for (int c = 0; c < NCA; c++) {
-        const float sc = (uint32_t)c < a.attn_nc ? expf(mz2[k][c].x - mm) : 0.0f;
+        const float sc = (uint32_t)c < a.attn_nc ? nlg_exp2(mz2[k][c].x - mm) : 0.0f;  // base-2 maxima
         zz = fmaf(mz2[k][c].y, sc, zz);
         acc.x = fmaf(cx4[k][c].x, sc, acc.x);
         acc.y = fmaf(cx4[k][c].y, sc, acc.y);

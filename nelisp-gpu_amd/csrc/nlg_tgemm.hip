@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
         float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (int c = 0; c < NLG_ATTN_MAX_CHUNKS; c++) {
-          const float sc = (uint32_t)c < a.attn_nc ? expf(mz[c].x - mm) : 0.0f;
+          const float sc = (uint32_t)c < a.attn_nc ? nlg_exp2(mz[c].x - mm) : 0.0f;  // base-2 maxima
           zz = fmaf(mz[c].y, sc, zz);
           acc.x = fmaf(cx[c].x, sc, acc.x);
           acc.y = fmaf(cx[c].y, sc, acc.y);
