@@ -145,22 +145,24 @@ __device__ __forceinline__ float nlg_wave_max_f32(float v) {
 // `scratch` needs blockDim.x/64 floats.  Every thread gets the result.
 // NW > 0 states the block's wave count at compile time (no read of the
 // launch's block size).
-template <int NW = 0>
+// FRESH: `scratch` has not been used before in this kernel, so the barrier
+// that guards its reuse is left out.
+template <int NW = 0, bool FRESH = false>
 __device__ __forceinline__ float nlg_block_sum_f32(float v, float *scratch) {
   v = nlg_wave_sum_f32(v);
   const int nw = NW > 0 ? NW : (int)(blockDim.x >> 6), w = threadIdx.x >> 6;
-  __syncthreads();
+  if (!FRESH) __syncthreads();
   if ((threadIdx.x & 63) == 0) scratch[w] = v;
   __syncthreads();
   float t = 0.0f;
   for (int i = 0; i < nw; i++) t = t + scratch[i];
   return t;
 }
-template <int NW = 0>
+template <int NW = 0, bool FRESH = false>
 __device__ __forceinline__ float nlg_block_max_f32(float v, float *scratch) {
   v = nlg_wave_max_f32(v);
   const int nw = NW > 0 ? NW : (int)(blockDim.x >> 6), w = threadIdx.x >> 6;
-  __syncthreads();
+  if (!FRESH) __syncthreads();
   if ((threadIdx.x & 63) == 0) scratch[w] = v;
   __syncthreads();
   float t = scratch[0];

@@ -36,7 +36,7 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
 template <int R, int CPL, int F4, int PRO, int EPI>
 __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   extern __shared__ uint4 s_xq4[];  // cols/16 uint4 = cols int8 lanes
-  __shared__ float red[4];
+  __shared__ float red[4], red2[4];  // the two reductions' own scratch: no reuse barrier
   // Every argument the kernel uses is pinned into SGPRs here, so they all
   // arrive with the first kernarg fetch instead of in later round trips.
   float *const y_out = a.y;
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
       sq = sq + xv4[k].z * xv4[k].z;
       sq = sq + xv4[k].w * xv4[k].w;
     }
-    sq = nlg_block_sum_f32<4>(sq, red);
+    sq = nlg_block_sum_f32<4, true>(sq, red);
     sq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq)));
     const float istd = 1.0f / sqrtf(sq / (float)a.cols + a.eps);
 #pragma unroll
@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
     t = dsl_abs(xv4[k].z); amax = t > amax ? t : amax;
     t = dsl_abs(xv4[k].w); amax = t > amax ? t : amax;
   }
-  amax = nlg_block_max_f32<4>(amax, red);
+  amax = nlg_block_max_f32<4, true>(amax, red2);
   const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
   const float ginv = 1.0f / g;
   if (gamma_out && blockIdx.x == 0 && threadIdx.x == 0) gamma_out[tok] = g;

@@ -46,7 +46,7 @@ struct ActQArgs {
 // G16: 16-column groups per thread (cols <= 4096 * G16).
 template <int G16, int PRO>
 __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
-  __shared__ float red[4];
+  __shared__ float red[4], red2[4];  // the two reductions' own scratch: no reuse barrier
   asm volatile("" ::"s"(a.x), "s"(a.gain), "s"(a.xq), "s"(a.gamma), "s"(a.cols));
   const uint32_t tok = blockIdx.x;
   const uint32_t ngrp = a.cols >> 4, nf4 = a.cols >> 2;
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
         sq = sq + v[k][q].z * v[k][q].z;
         sq = sq + v[k][q].w * v[k][q].w;
       }
-    sq = nlg_block_sum_f32<4>(sq, red);
+    sq = nlg_block_sum_f32<4, true>(sq, red);
     sq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq)));
     const float istd = 1.0f / sqrtf(sq / (float)a.cols + a.eps);
 #pragma unroll
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
       t = dsl_abs(v[k][q].z); amax = t > amax ? t : amax;
       t = dsl_abs(v[k][q].w); amax = t > amax ? t : amax;
     }
-  amax = nlg_block_max_f32<4>(amax, red);
+  amax = nlg_block_max_f32<4, true>(amax, red2);
   const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
   const float ginv = 1.0f / g;
   const bool fast = g > 0.0f && ginv < INFINITY;
