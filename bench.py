@@ -135,7 +135,7 @@ def gpu_bench(steps: int, warmup: int, sweep: bool):
     nlgpu.sync()
     if sweep:
         sw = {}
-        for rpw in (1, 2, 4):
+        for rpw in (1, 2, 4, 8):
             for i in range(warmup):
                 step(i, rpw)
             sw[f"fused rpw={rpw}"] = round(timed(lambda i: step(i, rpw), steps, stream) * 1e3, 3)

@@ -107,6 +107,15 @@ __device__ __forceinline__ float nlg_fmax_nn(float a, float b) { return b > a ? 
 #define NLG_LOG2E 1.4426950408889634f
 __device__ __forceinline__ float nlg_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// silu-mul's gate sg = 1/(1 + exp(0 - g)) (kernels.el:186-193) in the fused
+// epilogues: one v_exp_f32 and one v_rcp_f32 (relative error ~1e-6 at
+// |g| = 20, well inside the 1e-4 SwiGLU tolerance) in place of a correctly
+// rounded expf and division (~25 instructions, most of the prefill GEMM's
+// SwiGLU epilogue).
+__device__ __forceinline__ float nlg_silu_gate(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + nlg_exp2((0.0f - g) * NLG_LOG2E));
+}
+
 // A 16-byte load of data streamed once per launch (2-bit weights): marked
 // non-temporal (glc slc), so it neither allocates in the caches nor evicts
 // the activations and KV rows later kernels re-read.  Measured: the 4096^2

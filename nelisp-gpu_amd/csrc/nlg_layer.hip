@@ -243,7 +243,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
     const float pv = __int_as_float(nlg_dpp<0xB1>(__float_as_int(val)));
     if (EPI == NLG_EPI_SWIGLU) {
       if (olive && !(lane & 1)) {
-        const float sg = 1.0f / (1.0f + expf(0.0f - val));
+        const float sg = nlg_silu_gate(val);
         y_out[(size_t)tok * ystride + (orow >> 1)] = (val * sg) * pv;
       }
     } else if (olive) {

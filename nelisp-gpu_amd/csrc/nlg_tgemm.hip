@@ -226,7 +226,7 @@ __device__ __forceinline__ void tg_store_pre(const GemmArgs &a, int lane, uint32
     const float pv = __int_as_float(nlg_dpp<0xB1>(__float_as_int(val)));  // row ^ 1
     if (EPI == NLG_EPI_SWIGLU) {
       if (live && !(lane & 1)) {
-        const float sg = 1.0f / (1.0f + expf(0.0f - val));
+        const float sg = nlg_silu_gate(val);
         a.y[(size_t)tk * a.ystride + (row >> 1)] = (val * sg) * pv;
       }
     } else if (live) {
@@ -678,7 +678,7 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
           const float g = odd ? got : keep, u = odd ? keep : got;
           const uint32_t tk = odd ? thi : tlo;
           if (lr && tk < a.seq) {
-            const float sg = 1.0f / (1.0f + expf(0.0f - g));
+            const float sg = nlg_silu_gate(g);
             a.y[(size_t)tk * a.ystride + (rw[nt] >> 1)] = (g * sg) * u;
           }
         }
