@@ -122,7 +122,8 @@ def test_fused_linear_bit_exact(seq, out, cols, rpw):
 BATCHED = [(8, 64, 256), (16, 300, 2560), (17, 2560, 2560), (32, 13824, 2560), (33, 2560, 6912),
            (64, 512, 4096), (100, 256, 1024), (512, 2560, 2560), (512, 6912, 2560),
            (200, 1000, 512), (600, 16448, 256),  # 64-row tiles, ragged; 128-row tiles, ragged
-           (40, 16400, 512), (32, 8200, 768)]  # enough 64-row workgroups: the unsplit small-batch kernel
+           (40, 16400, 512), (32, 8200, 768),  # enough 64-row workgroups: the unsplit small-batch kernel
+           (24, 1000, 12288), (9, 130, 8192)]  # split columns, 12 and 8 chunks per wave (the 16-chunk form)
 
 
 @pytest.mark.parametrize("seq,out,cols", BATCHED)
