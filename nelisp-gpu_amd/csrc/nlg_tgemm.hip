@@ -266,11 +266,14 @@ __device__ __forceinline__ void tg_store(const GemmArgs &a, int lane, uint32_t r
 // MT x 2048 activation block (to LDS), so a phase costs one memory round
 // trip; then 8 x 4 x MB matrix-core steps run out of registers and LDS.
 // NPH: phases (compile-time, so the loop over them unrolls and the staging
-// arrays stay in registers): cols <= 2048 * NPH.
-template <int MB, int NPH, int EPI>
+// arrays stay in registers) of PH chunks: cols <= 256 * PH * NPH.  The
+// epilogue's operands (gamma, the residual, RoPE entries) are fetched
+// before the first phase, not after the last.
+template <int MB, int NPH, int PH, int EPI>
 __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
   constexpr int MT = 16 * MB;
-  extern __shared__ __align__(16) uint8_t s_a[];  // MT x TG_PITCH
+  constexpr int PITCH = PH * TG_KC + 16;  // LDS row pitch in bytes (staggers the banks)
+  extern __shared__ __align__(16) uint8_t s_a[];  // MT x PITCH
   __shared__ float s_bv[4][MT];
   __shared__ int32_t s_bi[4][MT];
   asm volatile("" ::"s"(a.xq), "s"(a.gamma), "s"(a.w2), "s"(a.bias), "s"(a.beta), "s"(a.y), "s"(a.seq),
@@ -282,27 +285,39 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
   const uint32_t tok0 = blockIdx.y * MT;
   const uint32_t nchunks = a.cols / TG_KC;
   const uint4 *wrow = (const uint4 *)(a.w2 + (size_t)rowc * a.wng);
-  // activation staging: piece p = threadIdx.x + 256 i is token p / 128,
-  // 16-byte slot p % 128 of the phase's 2048 columns
-  constexpr int NA = MT * (TG_PH * TG_KC / 16) / 256;  // pieces per thread (8 MB)
-  const uint32_t slot = threadIdx.x % 128u, tsub = threadIdx.x / 128u;  // token = tsub + 2i
+  // activation staging: piece p = threadIdx.x + 256 i is token p / SL,
+  // 16-byte slot p % SL of the phase's 256 PH columns
+  constexpr int SL = PH * TG_KC / 16;          // slots per token row
+  constexpr int NA = MT * SL / 256;            // pieces per thread
+  static_assert(MT * SL % 256 == 0, "whole staging pieces per thread");
   const float bo_raw = (a.bias ? a.bias : a.beta)[a.bias ? rowc : 0];
   const float be = a.beta[a.beta_per_row ? rowc : 0];
   const float bo = a.bias ? bo_raw : 0.0f;
+  // epilogue operands of the lane's (token, row) pairs
+  float gm[MB][4];
+  TgPre pre[MB][4];
+#pragma unroll
+  for (int m = 0; m < MB; m++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t tk = tok0 + 16 * m + 4 * lg + r;
+      gm[m][r] = a.gamma[tk < a.seq ? tk : a.seq - 1];
+      pre[m][r] = tg_prefetch<EPI>(a, rowc, tk);
+    }
   v4i acc[MB];
 #pragma unroll
   for (int m = 0; m < MB; m++) acc[m] = (v4i){0, 0, 0, 0};
   // The staging registers are ext_vector values indexed by constants, not
   // arrays: an array here ends up in scratch once the phase loop unrolls.
-  typedef uint32_t wvec_t __attribute__((ext_vector_type(4 * TG_PH)));
+  typedef uint32_t wvec_t __attribute__((ext_vector_type(4 * PH)));
   typedef uint32_t avec_t __attribute__((ext_vector_type(4 * NA)));
 #pragma unroll
   for (int ph = 0; ph < NPH; ph++) {
-    const uint32_t c0 = ph * TG_PH;
+    const uint32_t c0 = ph * PH;
     if (c0 >= nchunks) break;  // uniform
     wvec_t wv;
 #pragma unroll
-    for (int i = 0; i < TG_PH; i++) {
+    for (int i = 0; i < PH; i++) {
       const uint32_t cc = c0 + i < nchunks ? c0 + i : nchunks - 1;
       const uint4 u = wrow[4 * cc + lg];
       // chunks past the end contribute zero
@@ -313,11 +328,12 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
       wv[4 * i + 3] = u.w & keep;
     }
     avec_t ar;
-    const uint32_t col = c0 * TG_KC + 16 * slot;
-    const uint32_t colc = col < a.cols ? col : a.cols - 16;
 #pragma unroll
     for (int i = 0; i < NA; i++) {
-      const uint32_t t = tsub + 2 * i, tk = tok0 + t < a.seq ? tok0 + t : a.seq - 1;
+      const uint32_t p = threadIdx.x + 256u * i, t = p / SL, slot = p % SL;
+      const uint32_t tk = tok0 + t < a.seq ? tok0 + t : a.seq - 1;
+      const uint32_t col = c0 * TG_KC + 16 * slot;
+      const uint32_t colc = col < a.cols ? col : a.cols - 16;
       const uint4 u = *(const uint4 *)(a.xq + (size_t)tk * a.cols + colc);
       ar[4 * i + 0] = u.x;
       ar[4 * i + 1] = u.y;
@@ -326,12 +342,13 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
     }
     if (c0) __syncthreads();  // every wave is done with the previous phase's block
 #pragma unroll
-    for (int i = 0; i < NA; i++)
-      *(uint4 *)(&s_a[(tsub + 2 * i) * TG_PITCH + 16 * slot]) =
-          make_uint4(ar[4 * i], ar[4 * i + 1], ar[4 * i + 2], ar[4 * i + 3]);
+    for (int i = 0; i < NA; i++) {
+      const uint32_t p = threadIdx.x + 256u * i;
+      *(uint4 *)(&s_a[(p / SL) * PITCH + 16 * (p % SL)]) = make_uint4(ar[4 * i], ar[4 * i + 1], ar[4 * i + 2], ar[4 * i + 3]);
+    }
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < TG_PH; i++) {
+    for (int i = 0; i < PH; i++) {
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         const uint32_t wd = wv[4 * i + t];
@@ -339,7 +356,7 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
                          (int)((wd << 2) & 0xC0C0C0C0u), (int)(wd & 0xC0C0C0C0u)};
 #pragma unroll
         for (int m = 0; m < MB; m++) {
-          const uint4 av = *(const uint4 *)(s_a + (16 * m + lr) * TG_PITCH + i * TG_KC + 16 * (4 * lg + t));
+          const uint4 av = *(const uint4 *)(s_a + (16 * m + lr) * PITCH + i * TG_KC + 16 * (4 * lg + t));
           const v4i aop = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
           acc[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop, acc[m], 0, 0, 0);
         }
@@ -354,11 +371,9 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
     for (int r = 0; r < 4; r++) {
       const uint32_t tk = tok0 + 16 * m + 4 * lg + r;
       const bool live = rlive && tk < a.seq;
-      const uint32_t tkc = tk < a.seq ? tk : a.seq - 1;
-      const float gm = a.gamma[tkc];
       // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
-      const float val = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, gm), (float)(acc[m][r] >> 6)));
-      tg_store<EPI>(a, lane, row, tk, live, val);
+      const float val = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, gm[m][r]), (float)(acc[m][r] >> 6)));
+      tg_store_pre<EPI>(a, lane, row, tk, live, val, pre[m][r]);
       if (EPI == NLG_EPI_ARGMAX) {
         // first maximum over the wave's 16 rows for this token
         float bv = live && val == val ? val : -INFINITY;
@@ -798,15 +813,21 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   }
   const dim3 grid(nlg_blocks(a.out, 64), (a.seq + MT - 1) / MT), blk(256);
   if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
-  const size_t lds = (size_t)MT * TG_PITCH;
   if (epi == NLG_EPI_ARGMAX) a.nparts = grid.x;
+  // Rows of 9..10 chunks (2560 columns) take one 10-chunk phase, one memory
+  // round trip instead of two, when the grid is a single round of workgroups
+  // (its 82 KB stage admits one per CU)
+  const uint32_t nch = a.cols / TG_KC;
+  const bool ph10 = nch > TG_PH && nch <= 10 && (uint64_t)grid.x * grid.y <= 256;
+  const size_t lds = (size_t)MT * (ph10 ? 10 * TG_KC + 16 : TG_PITCH);
   const int nph = a.cols <= 2048 ? 1 : (a.cols <= 4096 ? 2 : (a.cols <= 8192 ? 4 : 8));
 #define TGP(M, E)                                                                                 \
   do {                                                                                            \
-    if (nph == 1) hipLaunchKernelGGL((k_tgemm<M, 1, E>), grid, blk, lds, st, a);                  \
-    else if (nph == 2) hipLaunchKernelGGL((k_tgemm<M, 2, E>), grid, blk, lds, st, a);             \
-    else if (nph == 4) hipLaunchKernelGGL((k_tgemm<M, 4, E>), grid, blk, lds, st, a);             \
-    else hipLaunchKernelGGL((k_tgemm<M, 8, E>), grid, blk, lds, st, a);                           \
+    if (ph10) hipLaunchKernelGGL((k_tgemm<M, 1, 10, E>), grid, blk, lds, st, a);                  \
+    else if (nph == 1) hipLaunchKernelGGL((k_tgemm<M, 1, TG_PH, E>), grid, blk, lds, st, a);      \
+    else if (nph == 2) hipLaunchKernelGGL((k_tgemm<M, 2, TG_PH, E>), grid, blk, lds, st, a);      \
+    else if (nph == 4) hipLaunchKernelGGL((k_tgemm<M, 4, TG_PH, E>), grid, blk, lds, st, a);      \
+    else hipLaunchKernelGGL((k_tgemm<M, 8, TG_PH, E>), grid, blk, lds, st, a);                    \
   } while (0)
 #define TG(E)                                                                                     \
   do {                                                                                            \

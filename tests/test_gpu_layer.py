@@ -102,7 +102,7 @@ def test_residual_linear_bit_exact(seq, out, cols, inplace):
 
 
 @pytest.mark.parametrize("seq,dff,cols", [(1, 6912, 2560), (2, 96, 256), (1, 128, 6912), (32, 6912, 2560),
-                                          (8, 96, 256)])
+                                          (8, 96, 256), (16, 6912, 2560)])
 def test_swiglu(seq, dff, cols):
     print(f"[gpu] swiglu seq={seq} dff={dff} cols={cols}", flush=True)
     x, g = int_rows(dff + seq, seq * cols), gains(cols + 2, cols)
@@ -119,7 +119,7 @@ def test_swiglu(seq, dff, cols):
 
 QKV = [(1, 20, 5, 128, 2560, 768, 0), (1, 20, 5, 128, 2560, 768, 517), (2, 4, 2, 64, 256, 80, 79),
        (3, 8, 8, 64, 512, 16, 3), (1, 4, 2, 64, 256, 80, 80), (32, 20, 5, 128, 2560, 768, 640),
-       (8, 4, 2, 64, 256, 80, 0)]
+       (8, 4, 2, 64, 256, 80, 0), (16, 64, 32, 128, 2560, 16, 3)]  # last: one-phase 64-row GEMM
 
 
 @pytest.mark.parametrize("B,heads,kvh,hd,cols,max_seq,pos", QKV)
@@ -155,7 +155,8 @@ def test_qkv_rope_and_fp16_append(B, heads, kvh, hd, cols, max_seq, pos):
 
 
 @pytest.mark.parametrize("seq,vocab,cols,dup", [(1, 128256, 2560, False), (2, 1000, 256, True), (1, 37, 64, True),
-                                                (32, 128256, 2560, False), (8, 1000, 256, True)])
+                                                (32, 128256, 2560, False), (8, 1000, 256, True),
+                                                (16, 9000, 2560, False), (32, 9000, 2560, True)])
 def test_lm_head_argmax(seq, vocab, cols, dup):
     print(f"[gpu] argmax seq={seq} vocab={vocab} cols={cols}", flush=True)
     x, g = int_rows(vocab, seq * cols), gains(cols + 9, cols)
