@@ -54,6 +54,14 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   //    loads are straight-line (clamped addresses, validity applied with
   //    selects afterwards): a branch around a load makes the wait-count pass
   //    drain every outstanding load at the join.
+  // QKV: the device position is a scalar load (the constant address space;
+  // the scalar cache is invalidated at every dispatch, and nothing in this
+  // kernel writes the position), so waiting for it never waits for a vector
+  // load: a vector load of it, issued behind the weights, made the RoPE
+  // lookup wait for their whole HBM fetch.
+  int32_t pos0 = 0;
+  if (EPI == NLG_EPI_QKV) pos0 = *(const __attribute__((address_space(4))) int32_t *)a.pos;
+  __builtin_amdgcn_sched_barrier(0);
   const uint32_t nf4 = a.cols >> 2;
   float4 xv4[F4], gv4[F4];
   // PRO_ATTN: the chunk contexts and (max, sum) pairs of every element
@@ -116,7 +124,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   uint32_t dd = 0, p = 0;
   bool pos_ok = false;
   if (EPI == NLG_EPI_QKV) {
-    const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(tok % a.qper) : 0);
+    const int32_t pr = pos0 + (a.qper ? (int32_t)(tok % a.qper) : 0);
     pos_ok = pr >= 0 && (uint32_t)pr < a.max_seq;
     p = pos_ok ? (uint32_t)pr : 0u;
     const uint32_t sec = orow < a.nq ? orow : (orow < a.nq + a.nkv ? orow - a.nq : orow - a.nq - a.nkv);
@@ -125,14 +133,12 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
     cc = a.co[ci];
     ss = a.si[ci];  // SG[0] = +1: SI*SG is SI exactly
   }
+  // Chunks past the row stay as loaded (the dots skip them): writing a
+  // register whose load is in flight waits for that load, which would put
+  // the weights' HBM fetch in front of the quantisation.
 #pragma unroll
   for (int k = 0; k < F4; k++)
     if (threadIdx.x + 256u * k >= nf4) xv4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-  for (int r = 0; r < R; r++)
-#pragma unroll
-    for (int i = 0; i < CPL; i++)
-      if (lane + 64u * i >= nchunk) wv[r][i] = make_uint4(0, 0, 0, 0);
   // 2a. attention merge: x = sum_c ctx_c*exp(m_c - M) / sum_c z_c*exp(m_c - M)
   //     in k_attn_merge's exact operation order, so the two agree bit for bit
   if (PRO == NLG_PRO_ATTN) {
