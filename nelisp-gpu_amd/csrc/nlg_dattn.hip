@@ -109,6 +109,15 @@ uint32_t nlg_attn_chunk_count(uint32_t head_dim, uint32_t max_seq) { return attn
 // (2m, 2m+1)) before the product, as decode-attn-stream does.  An entry
 // list (AM_ENTRIES, attn-stream-entries) names each attended row's slot and
 // rank explicitly; chunk positions index the list.
+// v if ok, else zeros: per component, so that no select of whole vectors
+// is lowered through private memory
+__device__ __forceinline__ uint4 keep_u4(bool ok, uint4 v) {
+  return make_uint4(ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u);
+}
+__device__ __forceinline__ float4 keep_f4(bool ok, float4 v) {
+  return make_float4(ok ? v.x : 0.0f, ok ? v.y : 0.0f, ok ? v.z : 0.0f, ok ? v.w : 0.0f);
+}
+
 template <int HD, int G, int NI, int MODE>
 __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   constexpr int BM = MODE & ~AM_NT;
@@ -150,6 +159,12 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   float4 rc[NI], rs[NI];  // ring: the ranks' rotation pairs (cos, sin)
   uint32_t pp[NI];
   uint32_t len = 0, qrank = 0;
+  // paged / entries: bit i set when row i is a real cache row (else it reads
+  // as zeros) and, for entries, when its rotation is real (else zero).  The
+  // zeros are applied where a row is used, not where it is loaded: a select
+  // on a row in flight waits for it, and one after each load put the rows'
+  // fetches one behind the other.
+  uint32_t rowm = 0, rotm = 0;
   // Rows fetched: positions clamp to lim - 1.  Large caches (NT) read the
   // position first so that rows past it are never fetched (their addresses
   // clamp to the last attended row, a cache hit): bytes over latency.  Small
@@ -169,21 +184,20 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
       pp[i] = p0 + w * PW + i * PPI + grp;
       ev[i] = eb[pp[i] < a.max_seq ? pp[i] : a.max_seq - 1];
     }
+    __builtin_amdgcn_sched_barrier(0);  // all entries in flight before the first use
 #pragma unroll
     for (int i = 0; i < NI; i++) {
       const bool sok = ev[i].x >= 0 && (uint32_t)ev[i].x < a.nslots;
       const bool rok = ev[i].y >= 0 && (uint32_t)ev[i].y < a.trows;
       const size_t sl = sok ? (uint32_t)ev[i].x : 0u, rk = rok ? (uint32_t)ev[i].y : 0u;
-      const uint4 k4 = kv_ld<NT>(kbe + sl * HD), v4 = kv_ld<NT>(vbe + sl * HD);
-      const float4 c4 = *(const float4 *)(a.co + rk * (HD / 2) + d0 / 2);
-      const float4 s4 = *(const float4 *)(a.si + rk * (HD / 2) + d0 / 2);
-      const uint4 z4 = make_uint4(0, 0, 0, 0);
-      const float4 f0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      kr[i] = sok ? k4 : z4;
-      vr[i] = sok ? v4 : z4;
-      rc[i] = rok ? c4 : f0;
-      rs[i] = rok ? s4 : f0;
+      kr[i] = kv_ld<NT>(kbe + sl * HD);
+      vr[i] = kv_ld<NT>(vbe + sl * HD);
+      rc[i] = *(const float4 *)(a.co + rk * (HD / 2) + d0 / 2);
+      rs[i] = *(const float4 *)(a.si + rk * (HD / 2) + d0 / 2);
+      rowm |= sok ? 1u << i : 0u;
+      rotm |= rok ? 1u << i : 0u;
     }
+    __builtin_amdgcn_sched_barrier(0);
     len = a.max_seq;
     const int32_t qk = a.lens[b];
     qrank = qk >= 0 && (uint32_t)qk < a.trows ? (uint32_t)qk : a.trows;  // trows: a zero rotation
@@ -219,16 +233,20 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
       const uint32_t pc = pp[i] < lim ? pp[i] : lim - 1;
       ph[i] = trow[pc / a.bs];
     }
+    // all table entries in flight before the first use: left to itself the
+    // scheduler issued each entry's load after the previous row's address
+    // (one full memory round trip per position)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < NI; i++) {
       const uint32_t pc = pp[i] < lim ? pp[i] : lim - 1;
       const bool ok = ph[i] >= 0 && (uint32_t)ph[i] < a.npool;
       const size_t row = (((size_t)(ok ? ph[i] : 0) * a.bs + pc % a.bs) * a.kvheads + kvh) * HD + d0;
-      const uint4 k4 = kv_ld<NT>(a.kc + row), v4 = kv_ld<NT>(a.vc + row);
-      const uint4 z4 = make_uint4(0, 0, 0, 0);
-      kr[i] = ok ? k4 : z4;
-      vr[i] = ok ? v4 : z4;
+      kr[i] = kv_ld<NT>(a.kc + row);
+      vr[i] = kv_ld<NT>(a.vc + row);
+      rowm |= ok ? 1u << i : 0u;
     }
+    __builtin_amdgcn_sched_barrier(0);
   } else {
 #pragma unroll
     for (int i = 0; i < NI; i++) {
@@ -269,12 +287,15 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < NI; i++) {
     float kf[8];
+    const uint4 ki = PG || EN ? keep_u4((rowm >> i) & 1u, kr[i]) : kr[i];
 #pragma unroll
-    for (int j = 0; j < 8; j++) kf[j] = f16x8_at(kr[i], j);
+    for (int j = 0; j < 8; j++) kf[j] = f16x8_at(ki, j);
     if (RG) {  // K rotated by its rank
+      const bool rk = !EN || ((rotm >> i) & 1u);
+      const float4 ci = keep_f4(rk, rc[i]), si = keep_f4(rk, rs[i]);
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const float k0 = kf[2 * j], k1 = kf[2 * j + 1], c = f4_at(rc[i], j), sn = f4_at(rs[i], j);
+        const float k0 = kf[2 * j], k1 = kf[2 * j + 1], c = f4_at(ci, j), sn = f4_at(si, j);
         kf[2 * j] = k0 * c - k1 * sn;
         kf[2 * j + 1] = k0 * sn + k1 * c;
       }
@@ -305,12 +326,13 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   }
 #pragma unroll
   for (int i = 0; i < NI; i++) {
+    const uint4 vi = PG || EN ? keep_u4((rowm >> i) & 1u, vr[i]) : vr[i];
 #pragma unroll
     for (int h = 0; h < G; h++) {
       const float e = nlg_exp2(s[i][h] - m[h]);
       z[h] = z[h] + e;
 #pragma unroll
-      for (int j = 0; j < 8; j++) ctx[h][j] = fmaf(e, f16x8_at(vr[i], j), ctx[h][j]);
+      for (int j = 0; j < 8; j++) ctx[h][j] = fmaf(e, f16x8_at(vi, j), ctx[h][j]);
     }
   }
 #pragma unroll

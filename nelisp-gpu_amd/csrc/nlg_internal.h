@@ -126,6 +126,16 @@ __device__ __forceinline__ uint4 nlg_ld_stream(const uint4 *p) {
   return make_uint4(t.x, t.y, t.z, t.w);
 }
 
+// A device-resident int32 that the kernel does not write (the decode
+// position), read with a scalar load from the constant address space.  Its
+// wait counts scalar loads only, so code that needs it early (RoPE table
+// addresses) no longer waits for every vector load issued before it -- the
+// weights' whole HBM fetch.  The scalar cache is invalidated at every
+// dispatch, so a value written by an earlier kernel is seen.
+__device__ __forceinline__ int32_t nlg_ld_uniform_i32(const int32_t *p) {
+  return *(const __attribute__((address_space(4))) int32_t *)p;
+}
+
 // The same for rows read and written once (softmax in place: 5.49 -> 6.03 TB/s).
 __device__ __forceinline__ float4 nlg_ld_stream_f4(const float4 *p) {
   typedef float v4f __attribute__((ext_vector_type(4)));

@@ -54,13 +54,10 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   //    loads are straight-line (clamped addresses, validity applied with
   //    selects afterwards): a branch around a load makes the wait-count pass
   //    drain every outstanding load at the join.
-  // QKV: the device position is a scalar load (the constant address space;
-  // the scalar cache is invalidated at every dispatch, and nothing in this
-  // kernel writes the position), so waiting for it never waits for a vector
-  // load: a vector load of it, issued behind the weights, made the RoPE
-  // lookup wait for their whole HBM fetch.
+  // QKV: the device position, as a scalar load (a vector load of it, issued
+  // behind the weights, made the RoPE lookup wait for their HBM fetch)
   int32_t pos0 = 0;
-  if (EPI == NLG_EPI_QKV) pos0 = *(const __attribute__((address_space(4))) int32_t *)a.pos;
+  if (EPI == NLG_EPI_QKV) pos0 = nlg_ld_uniform_i32(a.pos);
   __builtin_amdgcn_sched_barrier(0);
   const uint32_t nf4 = a.cols >> 2;
   float4 xv4[F4], gv4[F4];

@@ -204,7 +204,7 @@ __device__ __forceinline__ TgPre tg_prefetch(const GemmArgs &a, uint32_t rowc, u
   const uint32_t tkc = tk < a.seq ? tk : a.seq - 1;
   if (EPI == NLG_EPI_RESID) r.res = a.res[(size_t)tkc * a.rstride + rowc];
   if (EPI == NLG_EPI_QKV) {
-    const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(tkc % a.qper) : 0);
+    const int32_t pr = nlg_ld_uniform_i32(a.pos) + (a.qper ? (int32_t)(tkc % a.qper) : 0);
     r.pos_ok = pr >= 0 && (uint32_t)pr < a.max_seq;
     r.p = r.pos_ok ? (uint32_t)pr : 0u;
     const uint32_t sec = rowc < a.nq ? rowc : (rowc < a.nq + a.nkv ? rowc - a.nq : rowc - a.nq - a.nkv);
