@@ -28,49 +28,47 @@ __device__ __forceinline__ uint32_t pack_lane(float v, float gamma) {
 //
 // pack-act-rows' lane magnitude is ri = min(trunc(t'), 127) with
 // t' = RN(RN(|v|/gamma) + 0.5).  With ginv = RN(1/gamma) finite, the estimate
-// t = RN(RN(|v|*ginv) + 0.5) differs from t' by less than 4e-5 whenever
-// t < 128 (the reciprocal, the product and the quotient each err by at most
-// 2^-24 relative on a value below 128.5, plus half an ulp of the final add),
-// so trunc(t) == trunc(t') unless t lies within 2^-13 of an integer; and
+// t = RN(|v|*ginv + 0.5) (one fused rounding) differs from t' by less than
+// 3e-5 whenever t < 128 (the reciprocal errs by at most 2^-24 relative on a
+// quotient below 128.5, and each of the three roundings by half an ulp of a
+// value below 128.5), so trunc(t) == trunc(t') unless t lies within 2^-13 of
+// an integer, i.e. unless |frac(t) - 1/2| > 1/2 - 2^-13 (both sides exact).
 // t >= 128 means t' > 127.99, which the clamp maps to 127 either way.  The
-// few elements that fall inside that band (and NaNs) are recomputed with the
+// few elements inside that band (and NaNs) are recomputed with the
 // reference's IEEE division.  |v|/gamma = |v/gamma| under round-to-nearest,
-// and a nonzero lane implies |v/gamma| >= 0.5, so the sign is v's.
-__device__ __forceinline__ uint32_t lane_est(float v, float ginv, bool &near) {
-  const float t = __fadd_rn(__fmul_rn(fabsf(v), ginv), 0.5f);
-  const float kf = truncf(t), fr = t - kf;
-  const bool big = t >= 128.0f;
-  near = !(big || (fr >= 0x1p-13f && fr <= 1.0f - 0x1p-13f));  // NaN lands here
-  const uint32_t k = big ? 127u : (uint32_t)kf;
-  return v < 0.0f ? (256u - k) & 255u : k;
+// and a nonzero lane implies |v/gamma| >= 0.5, so the sign is v's: the
+// stored byte is the low byte of the signed magnitude, (256 - ri) % 256 for
+// a negative v.  About 9 instructions per lane: fma, trunc, two subtracts, a
+// compare, min, copysign, convert and a third of a byte permute.
+__device__ __forceinline__ int32_t lane_est(float v, float ginv, bool &near) {
+  const float t = fmaf(fabsf(v), ginv, 0.5f);
+  const float kf = truncf(t);
+  near = !(fabsf((t - kf) - 0.5f) <= 0.5f - 0x1p-13f);  // NaN lands here
+  return (int32_t)__builtin_copysignf(fminf(kf, 127.0f), v);
 }
-// Packed word of four lanes; `near` gets one bit per lane that needs the
-// exact path.
-__device__ __forceinline__ uint32_t word_est(float4 v, float ginv, uint32_t &near) {
-  bool n0, n1, n2, n3;
-  const uint32_t w = lane_est(v.x, ginv, n0) | (lane_est(v.y, ginv, n1) << 8) |
-                     (lane_est(v.z, ginv, n2) << 16) | (lane_est(v.w, ginv, n3) << 24);
-  near = (n0 ? 1u : 0u) | (n1 ? 2u : 0u) | (n2 ? 4u : 0u) | (n3 ? 8u : 0u);
-  return w;
-}
-// Replace the flagged lanes of a word with the reference's own computation.
-__device__ __forceinline__ uint32_t word_fix(uint32_t w, float4 v, float gamma, uint32_t near) {
-  if (near & 1u) w = (w & 0xFFFFFF00u) | pack_lane(v.x, gamma);
-  if (near & 2u) w = (w & 0xFFFF00FFu) | (pack_lane(v.y, gamma) << 8);
-  if (near & 4u) w = (w & 0xFF00FFFFu) | (pack_lane(v.z, gamma) << 16);
-  if (near & 8u) w = (w & 0x00FFFFFFu) | (pack_lane(v.w, gamma) << 24);
-  return w;
+// the low bytes of a, b, c, d as one word (a in bits 0..7)
+__device__ __forceinline__ uint32_t pack_low_bytes(int32_t a, int32_t b, int32_t c, int32_t d) {
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000c0cu);
+  return lo | hi;
 }
 // The packed word pack-act-rows stores for v.  `fast` (1/gamma finite and
-// gamma > 0) is uniform across the block.  The exact fix-up sits behind a
-// wave-uniform vote, so a wave with no flagged lane skips it entirely.
+// gamma > 0) is uniform across the block.  The exact fix-up of flagged lanes
+// sits behind a wave-uniform vote, so a wave with no flagged lane skips it.
 __device__ __forceinline__ uint32_t quant_word(float4 v, float gamma, float ginv, bool fast) {
   if (!fast)
     return pack_lane(v.x, gamma) | (pack_lane(v.y, gamma) << 8) | (pack_lane(v.z, gamma) << 16) |
            (pack_lane(v.w, gamma) << 24);
-  uint32_t near;
-  uint32_t w = word_est(v, ginv, near);
-  if (__builtin_amdgcn_ballot_w64(near != 0u) != 0ull) w = word_fix(w, v, gamma, near);
+  bool n0, n1, n2, n3;
+  const int32_t k0 = lane_est(v.x, ginv, n0), k1 = lane_est(v.y, ginv, n1);
+  const int32_t k2 = lane_est(v.z, ginv, n2), k3 = lane_est(v.w, ginv, n3);
+  uint32_t w = pack_low_bytes(k0, k1, k2, k3);
+  if (__builtin_amdgcn_ballot_w64(n0 || n1 || n2 || n3) != 0ull) {
+    if (n0) w = (w & 0xFFFFFF00u) | pack_lane(v.x, gamma);
+    if (n1) w = (w & 0xFFFF00FFu) | (pack_lane(v.y, gamma) << 8);
+    if (n2) w = (w & 0xFF00FFFFu) | (pack_lane(v.z, gamma) << 16);
+    if (n3) w = (w & 0x00FFFFFFu) | (pack_lane(v.w, gamma) << 24);
+  }
   return w;
 }
 
