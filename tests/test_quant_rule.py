@@ -1,15 +1,20 @@
 """The division-free exact quantisation of the GPU kernels (lane_est /
-quant_word in nelisp-gpu_amd/csrc/nlg_ternary.hip) against the reference's
+quant_word in nelisp-gpu_amd/csrc/nlg_quant.h) against the reference's
 rounding (pack-act-rows, lisp/nelisp-gpu-kernels.el:912-926:
-ri = min(trunc(RN(RN(|v|/g) + 0.5)), 127)), both restated in float32 numpy.
+ri = min(trunc(RN(RN(|v|/g) + 0.5)), 127)), both restated in numpy.
 
-The kernels take t = RN(RN(|v| * RN(1/g)) + 0.5), trust trunc(t) when t is
-at least 2^-13 from an integer (or t >= 128), and recompute every other
-element with the IEEE division; a row whose 1/g is not finite (g = 0 or
-subnormal) divides throughout.  The claim under test is that the trusted
-estimates are never wrong: checked on random rows across 60 decades of scale
-and on values walked ulp by ulp across every rounding boundary, where a guard
-band that is too narrow would show.  CPU only.
+The kernels take t = RN(|v| * RN(1/g) + 0.5) (one fused multiply-add),
+trust min(trunc(t), 127) when |frac(t) - 1/2| <= 1/2 - 2^-13 (t at least
+2^-13 from an integer), and recompute every other element with the IEEE
+division; a row whose 1/g is not finite (g = 0 or subnormal) divides
+throughout.  The fused rounding is restated exactly: the product of two
+float32 values is exact in float64, adding 0.5 to it is exact in float64
+whenever the product is at least 2^-6, and below that t is within 2^-6 of
+1/2, where a second rounding cannot move trunc(t) or the band test.  The
+claim under test is that the trusted estimates are never wrong: checked on
+random rows across 60 decades of scale and on values walked ulp by ulp across
+every rounding boundary, where a guard band that is too narrow would show.
+CPU only.
 """
 import numpy as np
 
@@ -28,12 +33,11 @@ def kernel_ri(v, g):
     """The kernels' rule; returns (ri, fraction of elements sent to the exact path)."""
     with np.errstate(all="ignore"):
         ginv = (f32(1.0) / g).astype(f32)
-        t = ((np.abs(v).astype(f32) * ginv).astype(f32) + f32(0.5)).astype(f32)
+        t = (np.abs(v).astype(np.float64) * np.float64(ginv) + 0.5).astype(f32)
         kf = np.trunc(t)
         fr = (t - kf).astype(f32)
-        big = t >= f32(128.0)
-        near = ~(big | ((fr >= BAND) & (fr <= f32(1.0) - BAND)))
-        est = np.where(big, 127, np.nan_to_num(kf)).astype(np.int64)
+        near = ~(np.abs((fr - f32(0.5)).astype(f32)) <= f32(0.5) - BAND)  # NaN lands here
+        est = np.minimum(np.nan_to_num(kf), 127).astype(np.int64)
     if not (g > 0 and np.isfinite(ginv)):
         near = np.ones(v.shape, bool)
     return np.where(near, exact_ri(v, g), est), near.mean()
