@@ -63,12 +63,8 @@ __global__ __launch_bounds__(256) void k_repack_i8(const uint32_t *wp, uint32_t 
 // the codes are read as (packed >> 2z) & 3, which is what z divisions by 4
 // and a % 4 leave of a uint.
 template <int NF>
-__global__ __launch_bounds__(256) void k_repack_packed(const float *wpk, uint32_t out, uint32_t cols, uint32_t pk,
-                                                       uint32_t fcount, uint32_t wng, uint32_t *w2, uint32_t *nbad) {
-  const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (uint64_t)out * wng) return;
-  const uint32_t o = (uint32_t)(idx / wng), wi = (uint32_t)(idx % wng);
-  const float *row = wpk + (size_t)o * fcount;
+__device__ __forceinline__ uint32_t packed_word(const float *row, uint32_t cols, uint32_t pk, uint32_t fcount,
+                                                uint32_t wi, uint32_t &bad) {
   const uint32_t f0 = 16 * wi / pk;
   uint32_t pv[NF];
 #pragma unroll
@@ -76,7 +72,7 @@ __global__ __launch_bounds__(256) void k_repack_packed(const float *wpk, uint32_
     const uint32_t fi = f0 + j < fcount ? f0 + j : fcount - 1;
     pv[j] = nlg_f2u(row[fi]);
   }
-  uint32_t word = 0, bad = 0, z = 16 * wi - f0 * pk, j = 0;
+  uint32_t word = 0, z = 16 * wi - f0 * pk, j = 0;
 #pragma unroll
   for (int f = 0; f < 16; f++) {
     const uint32_t col = 16 * wi + f, fi = f0 + j;
@@ -90,7 +86,66 @@ __global__ __launch_bounds__(256) void k_repack_packed(const float *wpk, uint32_
     }
     if (++z == pk) { z = 0; j++; }
   }
-  w2[idx] = word;
+  return word;
+}
+
+template <int NF>
+__global__ __launch_bounds__(256) void k_repack_packed(const float *wpk, uint32_t out, uint32_t cols, uint32_t pk,
+                                                       uint32_t fcount, uint32_t wng, uint32_t *w2, uint32_t *nbad) {
+  const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (uint64_t)out * wng) return;
+  const uint32_t o = (uint32_t)(idx / wng), wi = (uint32_t)(idx % wng);
+  uint32_t bad = 0;
+  w2[idx] = packed_word<NF>(wpk + (size_t)o * fcount, cols, pk, fcount, wi, bad);
+  if (nbad && bad) atomicAdd(nbad, bad);
+}
+
+// pk = 12 (codes below 4^12 = 2^24, exact in f32): four floats hold 48 codes,
+// three 2-bit words.  Code c sits in bits 2z, 2z+1 (lo, hi) and the 2-bit
+// field of c - 1 is (~lo, ~(lo | hi)) bit for bit -- 0 -> 11, 1 -> 00,
+// 2 -> 01, and the unrepresentable 3 -> 00 like the per-word path -- so a
+// float's twelve fields are five bitwise operations, and the three words
+// are shifts of the four.  One thread per 48-column group of a row; a row's
+// last, partial group takes the per-word path.
+__device__ __forceinline__ uint32_t fields12(uint32_t u, uint32_t &bad) {
+  const uint32_t lo = u & 0x555555u, hi = (u >> 1) & 0x555555u;
+  bad += __builtin_popcount(lo & hi);
+  return (~lo & 0x555555u) | ((~(lo | hi) & 0x555555u) << 1);
+}
+
+// W32: out * ngr < 2^32, so the index splits with a 32-bit division
+template <bool W32>
+__global__ __launch_bounds__(256) void k_repack_pk12(const float *wpk, uint32_t out, uint32_t cols, uint32_t fcount,
+                                                     uint32_t wng, uint32_t ngr, uint32_t *w2, uint32_t *nbad) {
+  uint32_t o, gi;
+  if (W32) {
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx >= out * ngr) return;
+    o = idx / ngr;
+    gi = idx - o * ngr;
+  } else {
+    const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (uint64_t)out * ngr) return;
+    o = (uint32_t)(idx / ngr);
+    gi = (uint32_t)(idx % ngr);
+  }
+  const float *row = wpk + (size_t)o * fcount;
+  uint32_t *dst = w2 + (size_t)o * wng + 3 * gi;
+  uint32_t bad = 0;
+  if (48 * gi + 48 <= cols && 4 * gi + 4 <= fcount) {
+    // one 16-byte load and one 12-byte store (rows are only 4-byte aligned;
+    // global memory takes unaligned vector accesses)
+    float v[4];
+    __builtin_memcpy(v, row + 4 * gi, sizeof v);
+    const uint32_t f0 = fields12(nlg_f2u(v[0]), bad), f1 = fields12(nlg_f2u(v[1]), bad);
+    const uint32_t f2 = fields12(nlg_f2u(v[2]), bad), f3 = fields12(nlg_f2u(v[3]), bad);
+    const uint32_t wo[3] = {f0 | (f1 << 24),          // columns 0..15: float 0 codes 0..11, float 1 codes 0..3
+                            (f1 >> 8) | (f2 << 16),   // columns 16..31: float 1 codes 4..11, float 2 codes 0..7
+                            (f2 >> 16) | (f3 << 8)};  // columns 32..47: float 2 codes 8..11, float 3 codes 0..11
+    __builtin_memcpy(dst, wo, sizeof wo);
+  } else {
+    for (uint32_t k = 0; k < 3 && 3 * gi + k < wng; k++) dst[k] = packed_word<5>(row, cols, 12, fcount, 3 * gi + k, bad);
+  }
   if (nbad && bad) atomicAdd(nbad, bad);
 }
 
@@ -122,7 +177,15 @@ extern "C" int nlg_repack_packed_to_2bit(const float *wpk, uint32_t out, uint32_
   const uint64_t n = (uint64_t)out * wng;
   if (!fcount) return nlg_fail("repack base-4: fcount is 0");
   const dim3 grid((unsigned)((n + 255) / 256)), blk(256);
-  if (pk >= 4)
+  if (pk == 12) {
+    const uint32_t ngr = (wng + 2) / 3;
+    const uint64_t ng = (uint64_t)out * ngr;
+    const dim3 g12((unsigned)((ng + 255) / 256));
+    if (ng + 255 < (1ull << 32))
+      hipLaunchKernelGGL(k_repack_pk12<true>, g12, blk, 0, nlg_stream(stream), wpk, out, cols, fcount, wng, ngr, w2, nbad);
+    else
+      hipLaunchKernelGGL(k_repack_pk12<false>, g12, blk, 0, nlg_stream(stream), wpk, out, cols, fcount, wng, ngr, w2, nbad);
+  } else if (pk >= 4)
     hipLaunchKernelGGL(k_repack_packed<5>, grid, blk, 0, nlg_stream(stream), wpk, out, cols, pk, fcount, wng, w2, nbad);
   else
     hipLaunchKernelGGL(k_repack_packed<16>, grid, blk, 0, nlg_stream(stream), wpk, out, cols, pk, fcount, wng, w2, nbad);
