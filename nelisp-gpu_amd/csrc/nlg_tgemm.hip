@@ -427,6 +427,7 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
 // accumulator register w of every token block.
 
 #define TK_D 3  // activation chunks in flight
+#define TK_PITCH 68  // LDS row pitch (words) of a wave's activation tile: 256 bytes + 16
 
 template <int MB, int EPI, int PM>
 __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
@@ -434,6 +435,9 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
   constexpr int D = PM < TK_D ? PM : TK_D;
   typedef uint32_t avec __attribute__((ext_vector_type(4 * NA)));
   __shared__ v4i s_red[4][MB][64];
+  // each wave's activation tile of one chunk: MB blocks x 16 tokens x 256
+  // bytes, rows padded to TK_PITCH words
+  __shared__ __align__(16) uint32_t s_at[4][MB][16][TK_PITCH];
   asm volatile("" ::"s"(a.xq), "s"(a.gamma), "s"(a.w2), "s"(a.bias), "s"(a.beta), "s"(a.y), "s"(a.seq),
                "s"(a.out), "s"(a.cols), "s"(a.wng), "s"(a.ystride), "s"(a.beta_per_row));
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -445,13 +449,21 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
   const uint32_t per = (nchunks + 3) / 4, cb = w * per;
   const uint32_t ce = min(cb + per, nchunks);
   const uint4 *wrow = (const uint4 *)(a.w2 + (size_t)rowc * a.wng) + lg;
-  // token rows of this lane (A row i = lr of each 16-token block), at column 64 lg
-  const uint8_t *xa[MB];
+  // Activations are fetched whole rows at a time -- load u of block m brings
+  // token 16 m + 4 u + lane / 16, bytes 16 (lane % 16) of a chunk, so each
+  // instruction reads four full 256-byte row chunks -- and reach the matrix
+  // cores' layout (lane (i, g) at step t: token i, bytes 64 g + 16 t) through
+  // the wave's LDS tile.  Fetched in that layout directly, one instruction
+  // touched 16 rows in 16-byte pieces: twice the cache lines, each half used,
+  // for data every workgroup re-reads.
+  const uint8_t *xa[MB][4];
 #pragma unroll
-  for (int m = 0; m < MB; m++) {
-    const uint32_t tk = tok0 + 16 * m + lr;
-    xa[m] = a.xq + (size_t)(tk < a.seq ? tk : a.seq - 1) * a.cols + 64 * lg;
-  }
+  for (int m = 0; m < MB; m++)
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint32_t tk = tok0 + 16 * m + 4 * u + (lane >> 4);
+      xa[m][u] = a.xq + (size_t)(tk < a.seq ? tk : a.seq - 1) * a.cols + 16 * (lane & 15);
+    }
   // 1. the lane's 4 weight words (64 columns of its row) of every chunk
   uint4 wq[PM];
 #pragma unroll
@@ -459,18 +471,17 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
     const uint32_t c = cb + j;
     wq[j] = nlg_ld_stream(&wrow[4 * (c < ce ? c : nchunks - 1)]);
   }
-  // 2. the first D chunks' activations: for each token block m and step t the
-  //    16 bytes of columns 64 lg + 16 t
+  // 2. the first D chunks' activations, whole rows per load (see above)
   avec av[PM];
 #define TK_LOADA(k)                                                                       \
   do {                                                                                    \
     const uint32_t c = cb + (k);                                                          \
     const uint32_t cc = c < ce ? c : nchunks - 1;                                         \
     _Pragma("unroll") for (int m = 0; m < MB; m++) {                                      \
-      _Pragma("unroll") for (int t = 0; t < 4; t++) {                                     \
-        const uint4 v = *(const uint4 *)(xa[m] + (size_t)cc * TG_KC + 16 * t);             \
-        av[k][16 * m + 4 * t] = v.x; av[k][16 * m + 4 * t + 1] = v.y;                     \
-        av[k][16 * m + 4 * t + 2] = v.z; av[k][16 * m + 4 * t + 3] = v.w;                 \
+      _Pragma("unroll") for (int u = 0; u < 4; u++) {                                     \
+        const uint4 v = *(const uint4 *)(xa[m][u] + (size_t)cc * TG_KC);                   \
+        av[k][16 * m + 4 * u] = v.x; av[k][16 * m + 4 * u + 1] = v.y;                     \
+        av[k][16 * m + 4 * u + 2] = v.z; av[k][16 * m + 4 * u + 3] = v.w;                 \
       }                                                                                   \
     }                                                                                     \
   } while (0)
@@ -499,6 +510,20 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
     if (k + D < PM) TK_LOADA(k + D);
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t keep = cb + k < ce ? 0xffffffffu : 0u;
+    // chunk k through the wave's tile: rows in, matrix-core layout out (one
+    // wave's LDS operations run in order, so no barrier is needed)
+#pragma unroll
+    for (int m = 0; m < MB; m++)
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        *(uint4 *)&s_at[w][m][4 * u + (lane >> 4)][4 * (lane & 15)] =
+            make_uint4(av[k][16 * m + 4 * u], av[k][16 * m + 4 * u + 1], av[k][16 * m + 4 * u + 2],
+                       av[k][16 * m + 4 * u + 3]);
+    uint4 at[MB][4];
+#pragma unroll
+    for (int m = 0; m < MB; m++)
+#pragma unroll
+      for (int t = 0; t < 4; t++) at[m][t] = *(const uint4 *)&s_at[w][m][lr][4 * (4 * lg + t)];
 #pragma unroll
     for (int t = 0; t < 4; t++) {
       const uint32_t wd = (t == 0 ? wq[k].x : t == 1 ? wq[k].y : t == 2 ? wq[k].z : wq[k].w) & keep;
@@ -506,8 +531,7 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
                        (int)((wd << 2) & 0xC0C0C0C0u), (int)(wd & 0xC0C0C0C0u)};
 #pragma unroll
       for (int m = 0; m < MB; m++) {
-        const v4i aop = {(int)av[k][16 * m + 4 * t], (int)av[k][16 * m + 4 * t + 1],
-                         (int)av[k][16 * m + 4 * t + 2], (int)av[k][16 * m + 4 * t + 3]};
+        const v4i aop = {(int)at[m][t].x, (int)at[m][t].y, (int)at[m][t].z, (int)at[m][t].w};
         acc[m] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop, acc[m], 0, 0, 0);
       }
     }
