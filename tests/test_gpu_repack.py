@@ -36,7 +36,8 @@ def test_repack_int8_lanes_bit_exact(out, cols):
     assert int(nbad.download(np.uint32, 1)[0]) == bad
 
 
-@pytest.mark.parametrize("out,cols,pk", [(6912, 2560, 12), (37, 300, 12), (4, 33, 1), (2, 48, 16), (9, 100, 5)])
+@pytest.mark.parametrize("out,cols,pk", [(6912, 2560, 12), (37, 300, 12), (5, 96, 12), (3, 48, 12),
+                                         (4, 33, 1), (2, 48, 16), (9, 100, 5)])
 def test_repack_base4_bit_exact(out, cols, pk):
     print(f"[gpu] repack base-4 out={out} cols={cols} pk={pk}", flush=True)
     rng = np.random.default_rng(out * pk + cols)

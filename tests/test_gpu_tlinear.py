@@ -69,3 +69,33 @@ def test_adjoint_identity_on_gpu():
     left, right = float(np.dot(y.astype(np.float64), g)), float(np.dot(x.astype(np.float64), xt))
     print(f"  <Wx,g> = {left:.6f}  <x,W'g> = {right:.6f}", flush=True)
     assert abs(left - right) <= 1e-5 * max(1e-6, abs(left))
+
+
+@pytest.mark.parametrize("name,groups", [("ternary-rows-t", 7), ("dp4a-rows-t", 5)])
+def test_rows_t_partial_grid(name, groups):
+    """groups * 64 below seq * cols (a cut inside a position): only the first
+    64 * groups outputs are written, bit-identical to the CPU restatement's,
+    and the rest of X keeps its contents (the vkserver dispatch semantics)."""
+    out, cols, seq = 70, 300, 3
+    print(f"[gpu] {name} partial grid: out={out} cols={cols} seq={seq} groups={groups}", flush=True)
+    rng = np.random.default_rng(groups)
+    if name == "ternary-rows-t":
+        wng, nblk = (cols + 15) // 16, (cols + 127) // 128
+        w = nlgpu.pack_ternary(nlgpu.trits(11, (out, cols))).reshape(-1).view(f32)
+        beta = (np.abs(rng.standard_normal(out * nblk)) * 0.05).astype(f32)
+        push = [out, cols, nblk, wng, seq]
+    else:
+        ng = (cols + 3) // 4
+        w = rng.integers(0, 2 ** 32, out * ng, dtype=np.uint64).astype(np.uint32).view(f32)
+        beta = (np.abs(rng.standard_normal(out)) * 0.05).astype(f32)
+        push = [out, cols, ng, seq]
+    g = rng.standard_normal(seq * out).astype(f32)
+    x = np.full(seq * cols, -7.0, f32)
+    devs = [nlgpu.to_device(b) for b in (w, beta, g, x)]
+    nlgpu.dispatch(name, devs, push, groups)
+    got = devs[-1].download(f32, x.size)
+    want = x.copy()
+    orc.dispatch(name, [w.copy(), beta, g, want], push, groups)
+    k = 64 * groups
+    assert np.all(got[k:] == -7.0)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
