@@ -53,8 +53,9 @@ __global__ __launch_bounds__(256) void k_rows_t(TArgs a) {
   const uint32_t wi0 = c0 / FPW;
   const uint32_t blk = FPW == 16 ? c0 / 128 : 0u;  // CG columns lie in one 128-column block
   const uint32_t gb = p * a.out;
-  // rows' words as 16-byte loads when every row's piece is aligned and inside the buffer
-  const bool vec = a.stride % 4 == 0 && (uint64_t)(a.out - 1) * a.stride + wi0 + NWD <= a.nwp;
+  // rows' words as 16-byte loads when every row's piece is 16-byte aligned and inside the buffer
+  const bool vec = ((uintptr_t)a.wp & 15) == 0 && a.stride % 4 == 0 &&
+                   (uint64_t)(a.out - 1) * a.stride + wi0 + NWD <= a.nwp;
   float acc = 0.0f;  // the consumer lane's column
   for (uint32_t r0 = 0; r0 < a.out; r0 += RT_RS) {
     const uint32_t nr = a.out - r0 < (uint32_t)RT_RS ? a.out - r0 : (uint32_t)RT_RS;
