@@ -559,15 +559,16 @@ def pmc_probe():
     print("pmc probe: 64 steps of k_tern_fused (4096x4096), 4 copies of 64 MiB", flush=True)
 
 
-def profile_eager():
+def profile_eager(stack=True):
     """Launch, without graphs (rocprofv3's kernel trace follows eager launches
     only), what the rocprof summaries cover: the config-5 decoder stack at
-    batch 1 and 32 (512-row prefill, then 16 decode steps) and the config-4
-    FFN at 512 and 16384 tokens (10 passes each).  Prints one line per phase."""
+    batch 1 and 32 (512-row prefill, then 16 decode steps; left out when
+    `stack` is false) and the config-4 FFN at 512 and 16384 tokens (10 passes
+    each).  Prints one line per phase."""
     import nlgpu
     nlgpu.init()
     c = STACK
-    for batch in (1, 32):
+    for batch in ((1, 32) if stack else ()):
         s = nlgpu.Stack(**c, max_seq=PROMPT + DECODE, batch=batch, seed=20260921 + 5)
         ids = (nlgpu.uniform(20260921 + 55, batch * PROMPT) * c["vocab"]).astype(np.int32).reshape(batch, PROMPT)
         s.prefill(ids)
@@ -604,12 +605,14 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true", help="only the launches the PMC profiles count")
     ap.add_argument("--profile-eager", action="store_true",
                     help="only the eager stack and FFN launches the rocprof kernel summaries cover")
+    ap.add_argument("--profile-ffn", action="store_true",
+                    help="only the eager FFN launches (the MFMA counter summary)")
     args = ap.parse_args()
     if args.pmc_probe:
         pmc_probe()
         return
-    if args.profile_eager:
-        profile_eager()
+    if args.profile_eager or args.profile_ffn:
+        profile_eager(stack=not args.profile_ffn)
         return
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the decode path is not sharded); "
