@@ -196,6 +196,8 @@ enum {
   NLG_PRO_NONE = 0,  // x as given
   NLG_PRO_RMS = 1,   // x = rmsnorm(x) * gain
   NLG_PRO_ATTN = 2,  // x = decode attention merged from its chunk partials
+  // kernel-internal: NLG_PRO_ATTN over exactly 3 chunks (decode at 512 < max_seq <= 768)
+  NLG_PRO_ATTN3 = 3,
 };
 // Most attention chunks the PRO_ATTN prologue merges, and how many chunks
 // the decode attention splits max_seq positions into.

@@ -62,10 +62,14 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   const uint32_t nf4 = a.cols >> 2;
   float4 xv4[F4], gv4[F4];
   // PRO_ATTN: the chunk contexts and (max, sum) pairs of every element
-  constexpr int NCA = PRO == NLG_PRO_ATTN ? NLG_ATTN_MAX_CHUNKS : 1;
+  // (PRO_ATTN3: exactly three chunks, so no clamped repeat of the last one
+  // is loaded; the fourth chunk's weight is 0 in the general form, so the
+  // merged values differ at most in the sign of a zero, which quantises alike)
+  constexpr bool ATT = PRO == NLG_PRO_ATTN || PRO == NLG_PRO_ATTN3;
+  constexpr int NCA = PRO == NLG_PRO_ATTN3 ? 3 : (ATT ? NLG_ATTN_MAX_CHUNKS : 1);
   float4 cx4[F4][NCA];
   float2 mz2[F4][NCA];
-  if (PRO == NLG_PRO_ATTN) {
+  if (ATT) {
     const float4 *c4 = (const float4 *)a.x;
     const uint32_t heads = a.cols / a.hd;
 #pragma unroll
@@ -138,7 +142,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
     if (threadIdx.x + 256u * k >= nf4) xv4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   // 2a. attention merge: x = sum_c ctx_c*exp(m_c - M) / sum_c z_c*exp(m_c - M)
   //     in k_attn_merge's exact operation order, so the two agree bit for bit
-  if (PRO == NLG_PRO_ATTN) {
+  if (ATT) {
 #pragma unroll
     for (int k = 0; k < F4; k++) {
       float mm = -1.0e30f;
@@ -353,7 +357,8 @@ int nlg_fused_launch(const FusedArgs &a0, int pro, int epi, int rpw, hipStream_t
   else if (pro == NLG_PRO_ATTN && epi == NLG_EPI_RESID) {
     if (!a.hd || a.hd % 4 || a.cols % a.hd || !a.attn_nc || a.attn_nc > NLG_ATTN_MAX_CHUNKS || !a.attn_mz)
       return nlg_fail("fused ternary linear: bad attention partials (hd %u, chunks %u)", a.hd, a.attn_nc);
-    PE(NLG_PRO_ATTN, NLG_EPI_RESID);
+    if (a.attn_nc == 3) PE(NLG_PRO_ATTN3, NLG_EPI_RESID);
+    else PE(NLG_PRO_ATTN, NLG_EPI_RESID);
   }
   else return nlg_fail("fused ternary linear: unsupported prologue/epilogue %d/%d", pro, epi);
 #undef PE
