@@ -51,7 +51,10 @@ __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
   const uint32_t tok = blockIdx.x;
   const uint32_t ngrp = a.cols >> 4, nf4 = a.cols >> 2;
   float4 v[G16][4];
-  if (PRO == NLG_PRO_ATTN) {
+  // PRO_ATTN3: exactly three chunks (see k_tern_fused's prologue)
+  constexpr bool ATT = PRO == NLG_PRO_ATTN || PRO == NLG_PRO_ATTN3;
+  constexpr int NC = PRO == NLG_PRO_ATTN3 ? 3 : NLG_ATTN_MAX_CHUNKS;
+  if (ATT) {
     // attention merged from its chunks, in k_attn_merge's operation order
     const uint32_t heads = a.cols / a.hd;
     const float4 *c4 = (const float4 *)a.x;
@@ -61,10 +64,10 @@ __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const uint32_t f = 4 * gc + q, h = (4 * f) / a.hd;
-        float4 cx[NLG_ATTN_MAX_CHUNKS];
-        float2 mz[NLG_ATTN_MAX_CHUNKS];
+        float4 cx[NC];
+        float2 mz[NC];
 #pragma unroll
-        for (int c = 0; c < NLG_ATTN_MAX_CHUNKS; c++) {
+        for (int c = 0; c < NC; c++) {
           const uint32_t cc = (uint32_t)c < a.attn_nc ? (uint32_t)c : a.attn_nc - 1;
           const size_t tc = (size_t)tok * a.attn_nc + cc;
           cx[c] = c4[tc * nf4 + f];
@@ -72,11 +75,11 @@ __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
         }
         float mm = -1.0e30f;
 #pragma unroll
-        for (int c = 0; c < NLG_ATTN_MAX_CHUNKS; c++) mm = mz[c].x > mm ? mz[c].x : mm;
+        for (int c = 0; c < NC; c++) mm = mz[c].x > mm ? mz[c].x : mm;
         float zz = 0.0f;
         float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int c = 0; c < NLG_ATTN_MAX_CHUNKS; c++) {
+        for (int c = 0; c < NC; c++) {
           const float sc = (uint32_t)c < a.attn_nc ? nlg_exp2(mz[c].x - mm) : 0.0f;  // base-2 maxima
           zz = fmaf(mz[c].y, sc, zz);
           acc.x = fmaf(cx[c].x, sc, acc.x);
@@ -758,6 +761,7 @@ int nlg_act_q_launch(const float *x, const float *gain, float eps, const float *
     else hipLaunchKernelGGL((k_act_q<4, P>), grid, blk, 0, st, a);                                 \
   } while (0)
   if (pro == NLG_PRO_RMS) AQ(NLG_PRO_RMS);
+  else if (pro == NLG_PRO_ATTN && attn_nc == 3) AQ(NLG_PRO_ATTN3);
   else if (pro == NLG_PRO_ATTN) AQ(NLG_PRO_ATTN);
   else AQ(NLG_PRO_NONE);
 #undef AQ
