@@ -225,6 +225,20 @@ int nlg_rms_ternary_qkv_rope(const float *x, const float *gain, float eps, const
                              uint16_t *vcache, const float *rope_cos, const float *rope_sin,
                              const int32_t *pos, uint32_t seq, uint32_t heads, uint32_t kvheads,
                              uint32_t head_dim, uint32_t max_seq, uint32_t cols, void *stream);
+/* The same for a whole prompt (the prefill rows nlg_prefill_attn_f16 reads):
+ * row r of x is sequence r / qper at position pos[0] + r % qper; q of row r
+ * is rotated at that position and k, v go to that position of sequence
+ * r / qper's caches [rows/qper][kvheads][max_seq][head_dim].  Rows whose
+ * position lies outside [0, max_seq) store nothing to the caches.  rows must
+ * be a multiple of qper > 0.  The reference runs a prompt as decode-rope-b /
+ * cache-append-b per position (kernels.el:340-365); this is those steps for
+ * every position at once. */
+int nlg_rms_ternary_qkv_rope_prompt(const float *x, const float *gain, float eps, const uint32_t *w2qkv,
+                                    const float *beta, int beta_per_row, float *q, uint16_t *kcache,
+                                    uint16_t *vcache, const float *rope_cos, const float *rope_sin,
+                                    const int32_t *pos, uint32_t rows, uint32_t qper, uint32_t heads,
+                                    uint32_t kvheads, uint32_t head_dim, uint32_t max_seq, uint32_t cols,
+                                    void *stream);
 
 /* LM head + greedy choice: logits = linear(rmsnorm(x)) and argmax[s] = the
  * lowest index of the largest logit (NaN never chosen; -1 if none). */
@@ -401,6 +415,13 @@ int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt);
  * the prompt lasts, else the greedy choice.  use_graph != 0 replays one
  * captured graph per step. */
 int nlg_stack_step(nlg_stack *s, uint32_t steps, int use_graph);
+/* One eager token step, as nlg_stack_step(s, 1, 0), that also returns the
+ * residual stream it went through: xs (host) receives [layers + 1][batch]
+ * [d_model] f32, the embedded token before layer 0 and the stream after
+ * each layer.  For checking a layer at a time against a reference
+ * composition; the reference has no counterpart (its model code runs the
+ * named kernels from Lisp and can read any buffer back). */
+int nlg_stack_step_trace(nlg_stack *s, float *xs);
 /* Current position (tokens consumed per sequence). */
 int nlg_stack_position(nlg_stack *s, uint32_t *pos);
 /* Token history [batch x max_seq] (prompt, then generated; -1 unwritten) and

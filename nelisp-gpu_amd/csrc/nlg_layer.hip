@@ -401,22 +401,42 @@ extern "C" int nlg_rms_ternary_swiglu(const float *x, const float *gain, float e
   return nlg_fused_launch(a, gain ? NLG_PRO_RMS : NLG_PRO_NONE, NLG_EPI_SWIGLU, 0, nlg_stream(stream));
 }
 
+static int qkv_rope(const float *x, const float *gain, float eps, const uint32_t *w2qkv, const float *beta,
+                    int beta_per_row, float *q, uint16_t *kcache, uint16_t *vcache, const float *rope_cos,
+                    const float *rope_sin, const int32_t *pos, uint32_t rows, uint32_t qper, uint32_t heads,
+                    uint32_t kvheads, uint32_t head_dim, uint32_t max_seq, uint32_t cols, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!heads || !kvheads || !head_dim || head_dim % 2 || !max_seq)
+    return nlg_fail("qkv: heads, kvheads, max_seq must be nonzero and head_dim even");
+  if (qper && rows % qper) return nlg_fail("qkv: rows (%u) must be a multiple of qper (%u)", rows, qper);
+  FusedArgs a{};
+  a.x = x; a.gain = gain; a.eps = eps; a.w2 = w2qkv; a.beta = beta; a.beta_per_row = beta_per_row;
+  a.seq = rows; a.nq = heads * head_dim; a.nkv = kvheads * head_dim; a.out = a.nq + 2 * a.nkv;
+  a.cols = cols; a.y = q; a.ystride = a.nq; a.hd = head_dim; a.kvheads = kvheads; a.max_seq = max_seq;
+  a.co = rope_cos; a.si = rope_sin; a.pos = pos; a.kc = kcache; a.vc = vcache; a.qper = qper;
+  if (a.nq % 4 || a.nkv % 4) return nlg_fail("qkv: heads*head_dim and kvheads*head_dim must be multiples of 4");
+  return nlg_fused_launch(a, NLG_PRO_RMS, NLG_EPI_QKV, 0, nlg_stream(stream));
+}
+
 extern "C" int nlg_rms_ternary_qkv_rope(const float *x, const float *gain, float eps, const uint32_t *w2qkv,
                                         const float *beta, int beta_per_row, float *q, uint16_t *kcache,
                                         uint16_t *vcache, const float *rope_cos, const float *rope_sin,
                                         const int32_t *pos, uint32_t seq, uint32_t heads,
                                         uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
                                         uint32_t cols, void *stream) {
-  if (nlg_ensure_init()) return NLG_ERR;
-  if (!heads || !kvheads || !head_dim || head_dim % 2 || !max_seq)
-    return nlg_fail("qkv: heads, kvheads, max_seq must be nonzero and head_dim even");
-  FusedArgs a{};
-  a.x = x; a.gain = gain; a.eps = eps; a.w2 = w2qkv; a.beta = beta; a.beta_per_row = beta_per_row;
-  a.seq = seq; a.nq = heads * head_dim; a.nkv = kvheads * head_dim; a.out = a.nq + 2 * a.nkv;
-  a.cols = cols; a.y = q; a.ystride = a.nq; a.hd = head_dim; a.kvheads = kvheads; a.max_seq = max_seq;
-  a.co = rope_cos; a.si = rope_sin; a.pos = pos; a.kc = kcache; a.vc = vcache;
-  if (a.nq % 4 || a.nkv % 4) return nlg_fail("qkv: heads*head_dim and kvheads*head_dim must be multiples of 4");
-  return nlg_fused_launch(a, NLG_PRO_RMS, NLG_EPI_QKV, 0, nlg_stream(stream));
+  return qkv_rope(x, gain, eps, w2qkv, beta, beta_per_row, q, kcache, vcache, rope_cos, rope_sin, pos, seq, 0,
+                  heads, kvheads, head_dim, max_seq, cols, stream);
+}
+
+extern "C" int nlg_rms_ternary_qkv_rope_prompt(const float *x, const float *gain, float eps,
+                                               const uint32_t *w2qkv, const float *beta, int beta_per_row,
+                                               float *q, uint16_t *kcache, uint16_t *vcache,
+                                               const float *rope_cos, const float *rope_sin, const int32_t *pos,
+                                               uint32_t rows, uint32_t qper, uint32_t heads, uint32_t kvheads,
+                                               uint32_t head_dim, uint32_t max_seq, uint32_t cols, void *stream) {
+  if (!qper) return nlg_fail("qkv prompt: qper must be nonzero");
+  return qkv_rope(x, gain, eps, w2qkv, beta, beta_per_row, q, kcache, vcache, rope_cos, rope_sin, pos, rows, qper,
+                  heads, kvheads, head_dim, max_seq, cols, stream);
 }
 
 // ------------------------------------------------------------ sampling

@@ -417,9 +417,13 @@ static int stack_head(nlg_stack *s);
 static int upload_prompt(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt, bool all_hist);
 
 // One token step for the whole batch, enqueued on the library stream.
-static int stack_enqueue(nlg_stack *s) {
+// trace (device, may be null) receives the residual stream before layer 0
+// and after every layer, [layers + 1][batch][d_model].
+static int stack_enqueue(nlg_stack *s, float *trace = nullptr) {
   const nlg_stack_config &c = s->c;
   const uint32_t d = c.d_model, f = c.d_ff, B = c.batch;
+  const size_t xbytes = (size_t)B * d * 4;
+  if (trace && nlg_copy_d2d(trace, s->x, xbytes, nullptr)) return NLG_ERR;
   for (uint32_t l = 0; l < c.layers; l++) {
     Layer &y = s->L[l];
     if (nlg_rms_ternary_qkv_rope(s->x, y.gattn, c.rms_eps, y.wqkv, y.bqkv, 1, s->q, y.kc, y.vc, s->co,
@@ -429,6 +433,7 @@ static int stack_enqueue(nlg_stack *s) {
         nlg_rms_ternary_swiglu(s->x, y.gffn, c.rms_eps, y.wgu, y.bgu, 1, s->h, B, f, d, nullptr) ||
         nlg_ternary_linear_residual(s->h, y.wd, nullptr, y.bd, 0, s->x, s->x, B, d, f, nullptr))
       return NLG_ERR;
+    if (trace && nlg_copy_d2d(trace + (size_t)(l + 1) * B * d, s->x, xbytes, nullptr)) return NLG_ERR;
   }
   return stack_head(s);
 }
@@ -584,6 +589,21 @@ extern "C" int nlg_stack_step(nlg_stack *s, uint32_t steps, int use_graph) {
   NLG_HIP(hipStreamSynchronize(nlg_stream(nullptr)));
   s->host_pos += steps;
   return NLG_OK;
+}
+
+extern "C" int nlg_stack_step_trace(nlg_stack *s, float *xs) {
+  if (!s || !s->started) return nlg_fail("stack step trace: not started");
+  if (!xs) return nlg_fail("stack step trace: null argument");
+  if ((uint64_t)s->host_pos + 1 > s->c.max_seq)
+    return nlg_fail("stack step trace: position %u is at max_seq %u", s->host_pos, s->c.max_seq);
+  const size_t bytes = (size_t)(s->c.layers + 1) * s->c.batch * s->c.d_model * 4;
+  float *dev = (float *)nlg_malloc(bytes);
+  if (!dev) return NLG_ERR;
+  int rc = stack_enqueue(s, dev);
+  if (!rc) rc = nlg_download(xs, dev, bytes);  // synchronous: ordered after the step
+  nlg_free(dev);
+  if (!rc) s->host_pos += 1;
+  return rc;
 }
 
 extern "C" int nlg_stack_position(nlg_stack *s, uint32_t *pos) {

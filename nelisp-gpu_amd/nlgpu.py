@@ -95,6 +95,8 @@ def lib() -> C.CDLL:
         "nlg_rms_ternary_swiglu": (i32, [vp, vp, C.c_float, vp, vp, i32, vp, u32, u32, u32, vp]),
         "nlg_rms_ternary_qkv_rope": (i32, [vp, vp, C.c_float, vp, vp, i32, vp, vp, vp, vp, vp, vp,
                                            u32, u32, u32, u32, u32, u32, vp]),
+        "nlg_rms_ternary_qkv_rope_prompt": (i32, [vp, vp, C.c_float, vp, vp, i32, vp, vp, vp, vp, vp, vp,
+                                                  u32, u32, u32, u32, u32, u32, u32, vp]),
         "nlg_rms_ternary_argmax": (i32, [vp, vp, C.c_float, vp, vp, i32, vp, vp, u32, u32, u32, vp,
                                          sz, vp]),
         "nlg_rms_ternary_argmax_workspace": (sz, [u32, u32]),
@@ -124,6 +126,7 @@ def lib() -> C.CDLL:
         "nlg_stack_start": (i32, [vp, vp, u32]),
         "nlg_stack_prefill": (i32, [vp, vp, u32]),
         "nlg_stack_step": (i32, [vp, u32, i32]),
+        "nlg_stack_step_trace": (i32, [vp, vp]),
         "nlg_stack_position": (i32, [vp, C.POINTER(u32)]),
         "nlg_stack_tokens": (i32, [vp, vp, vp]),
         "nlg_stack_logits": (i32, [vp, vp]),
@@ -324,6 +327,15 @@ def rms_ternary_qkv_rope(x, gain, eps, w2, beta, q, kc, vc, co, si, pos, seq, he
            "rms_ternary_qkv_rope")
 
 
+def rms_ternary_qkv_rope_prompt(x, gain, eps, w2, beta, q, kc, vc, co, si, pos, rows, qper, heads, kvheads,
+                                head_dim, max_seq, cols, beta_per_row=True, stream=None) -> None:
+    """Prompt rows: row r = sequence r // qper at position pos[0] + r % qper."""
+    _check(lib().nlg_rms_ternary_qkv_rope_prompt(x.ptr, gain.ptr, eps, w2.ptr, beta.ptr, int(beta_per_row),
+                                                 q.ptr, kc.ptr, vc.ptr, co.ptr, si.ptr, pos.ptr, rows, qper,
+                                                 heads, kvheads, head_dim, max_seq, cols, stream),
+           "rms_ternary_qkv_rope_prompt")
+
+
 def rms_ternary_argmax(x, gain, eps, w2, beta, logits, argmax, seq, vocab, cols, workspace,
                        beta_per_row=False, stream=None) -> None:
     _check(lib().nlg_rms_ternary_argmax(x.ptr, gain.ptr, eps, w2.ptr, beta.ptr, int(beta_per_row),
@@ -456,6 +468,14 @@ class Stack:
 
     def step(self, steps: int = 1, graph: bool = True) -> None:
         _check(lib().nlg_stack_step(self.h, steps, int(graph)), "stack_step")
+
+    def step_trace(self) -> np.ndarray:
+        """One eager step; returns the residual stream [layers + 1, batch,
+        d_model]: the embedded token, then the stream after each layer."""
+        c = self.cfg
+        xs = np.empty((c.layers + 1) * c.batch * c.d_model, np.float32)
+        _check(lib().nlg_stack_step_trace(self.h, xs.ctypes.data), "stack_step_trace")
+        return xs.reshape(c.layers + 1, c.batch, c.d_model)
 
     def position(self) -> int:
         p = C.c_uint32(0)

@@ -1,0 +1,177 @@
+"""The fused epilogues of the int8 matrix-core GEMM (128 tokens and more:
+config 4 at B = 512 and every prefill) against the chained reference
+kernels on the CPU (tests/layer_ref.py):
+
+* SwiGLU  -- rmsnorm-istd/-fwd, pack-act-rows, bitlinear-dp4a-1f on the
+  interleaved gate|up rows, silu-mul (kernels.el:1249-1265, :884-932,
+  :619-634, :186-193);
+* residual -- the linear then add2 (kernels.el:812-821), in place and not;
+* QKV     -- the linear, decode-rope-b on q and k and cache-append-b of k
+  and v into fp16 caches (kernels.el:340-365), for decode rows (row s =
+  sequence s) and for prompt rows (row r = sequence r / qper at position
+  pos0 + r % qper).
+
+Each shape is chosen so the GEMM runs a given row tile: 256, 128 or 64 rows
+per workgroup (the largest whose grid still gives 256 workgroups).  The
+activations of the RMSNorm cases are small integers, so the sum of squares
+is exact in any order and everything but SiLU's exp is bit-exact; SwiGLU's
+gate uses the device exp and is held to 1e-5 relative (the north star's
+bar is 1e-4).
+"""
+import numpy as np
+import pytest
+
+import layer_ref as ref
+import nlgpu
+
+pytestmark = pytest.mark.gpu
+f32 = np.float32
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    nlgpu.init()
+    yield
+
+
+def int_rows(seed, n):
+    """Integer activations in [-3, 3]: every partial sum of squares is exact."""
+    return (nlgpu.trits(seed, (n,)).astype(f32) * f32(3) - nlgpu.trits(seed + 1, (n,)).astype(f32)).astype(f32)
+
+
+def weights(seed, out, cols, per_row):
+    w2 = nlgpu.pack_ternary(nlgpu.trits(seed, (out, cols)))
+    beta = (f32(0.5) + nlgpu.uniform(seed + 1, out if per_row else 1).astype(f32)) / f32(np.sqrt(cols))
+    return w2, beta.astype(f32)
+
+
+def gains(seed, n):
+    return (f32(0.75) + f32(0.5) * nlgpu.uniform(seed, n).astype(f32)).astype(f32)
+
+
+def same_bits(a, b, what=""):
+    a, b = np.asarray(a, f32).ravel(), np.asarray(b, f32).ravel()
+    bad = np.flatnonzero(a.view(np.uint32) != b.view(np.uint32))
+    assert bad.size == 0, f"{what}: {bad.size} differ, first {bad[:4]}: {a[bad[:3]]} vs {b[bad[:3]]}"
+
+
+def row_tile(seq, out):
+    """The GEMM's row tile for seq >= 128 tokens (nlg_tgemm.hip's choice)."""
+    ty = (seq + 127) // 128
+    for t in (256, 128):
+        if (out + t - 1) // t * ty >= 256:
+            return t
+    return 64
+
+
+SWIGLU = [(128, 6912, 2560, True, 64), (512, 6912, 2560, True, 128), (600, 6912, 2560, True, 256),
+          (512, 640, 2560, False, 64), (400, 4096, 1024, True, 128)]
+
+
+@pytest.mark.parametrize("seq,dff,cols,rms,tile", SWIGLU)
+def test_batched_swiglu(seq, dff, cols, rms, tile):
+    assert row_tile(seq, 2 * dff) == tile
+    print(f"[gpu] batched swiglu seq={seq} dff={dff} cols={cols} rms={rms} tile={tile}", flush=True)
+    x = int_rows(dff + seq, seq * cols) if rms else nlgpu.normal(dff + seq, seq * cols)
+    g = gains(cols + 2, cols)
+    w2, beta = weights(dff + 11, 2 * dff, cols, per_row=True)
+    dh = nlgpu.DeviceArray(seq * dff * 4)
+    nlgpu.rms_ternary_swiglu(nlgpu.to_device(x), nlgpu.to_device(g) if rms else None, 1e-5, nlgpu.to_device(w2),
+                             nlgpu.to_device(beta), dh, seq, dff, cols)
+    xn = ref.rms(x, g, 1e-5, seq, cols) if rms else x
+    gu = ref.linear(xn, w2, beta, seq, 2 * dff, cols, per_row=True).reshape(seq, 2 * dff)
+    want = ref.silu_mul(gu[:, 0::2].ravel(), gu[:, 1::2].ravel())
+    got = dh.download(f32, seq * dff)
+    err = np.abs(got - want)
+    print(f"  max rel err {np.max(err / np.maximum(np.abs(want), 1e-30)):.2e}", flush=True)
+    assert np.all(err <= 1e-5 * np.abs(want) + 1e-7 * np.abs(want).max())
+
+
+RESID = [(128, 2560, 6912, 64), (512, 2560, 6912, 64), (512, 8192, 2560, 128), (600, 13824, 2560, 256),
+         (200, 1000, 512, 64)]
+
+
+@pytest.mark.parametrize("inplace", [False, True])
+@pytest.mark.parametrize("seq,out,cols,tile", RESID)
+def test_batched_residual(seq, out, cols, tile, inplace):
+    assert row_tile(seq, out) == tile
+    print(f"[gpu] batched residual seq={seq} out={out} cols={cols} tile={tile} inplace={inplace}", flush=True)
+    x, res = nlgpu.normal(cols + seq, seq * cols), nlgpu.normal(out + seq, seq * out)
+    w2, beta = weights(cols + out, out, cols, per_row=bool(out % 3))
+    bias = (nlgpu.normal(out + 1, out) * f32(0.1)).astype(f32)
+    dres = nlgpu.to_device(res)
+    dy = dres if inplace else nlgpu.DeviceArray(seq * out * 4)
+    nlgpu.ternary_linear_residual(nlgpu.to_device(x), nlgpu.to_device(w2), nlgpu.to_device(bias),
+                                  nlgpu.to_device(beta), dres, dy, seq, out, cols, beta_per_row=bool(out % 3))
+    want = (res + ref.linear(x, w2, beta, seq, out, cols, bias=bias, per_row=bool(out % 3))).astype(f32)
+    same_bits(dy.download(f32, seq * out), want, "residual")
+
+
+def rope_tables(max_seq, hd, theta=500000.0):
+    half = hd // 2
+    p = np.arange(max_seq)[:, None] / (theta ** (2.0 * np.arange(half)[None, :] / hd))
+    return np.cos(p).astype(f32).ravel(), np.sin(p).astype(f32).ravel()
+
+
+# rows, qper (0: decode rows), heads, kvheads, head_dim, cols, max_seq, pos0, tile
+QKV = [(512, 512, 20, 5, 128, 2560, 768, 0, 64),      # config 5's prompt at B = 1
+       (600, 200, 64, 16, 128, 2560, 256, 40, 128),   # three prompts
+       (512, 128, 64, 32, 128, 2560, 160, 20, 256),   # four prompts
+       (128, 64, 8, 2, 64, 1024, 100, 50, 64),        # positions run past max_seq: no cache store there
+       (128, 0, 20, 5, 128, 2560, 16, 5, 64)]         # 128 decode rows at one position
+
+
+@pytest.mark.parametrize("rows,qper,heads,kvh,hd,cols,max_seq,pos0,tile", QKV)
+def test_batched_qkv_rope_append(rows, qper, heads, kvh, hd, cols, max_seq, pos0, tile):
+    nq, nkv = heads * hd, kvh * hd
+    out = nq + 2 * nkv
+    assert row_tile(rows, out) == tile
+    print(f"[gpu] batched qkv rows={rows} qper={qper} heads={heads}/{kvh} hd={hd} pos0={pos0} tile={tile}",
+          flush=True)
+    nseq = rows // qper if qper else rows
+    x, g = int_rows(cols + rows + pos0, rows * cols), gains(cols + 5, cols)
+    w2, beta = weights(nq + pos0, out, cols, per_row=True)
+    co, si = rope_tables(max_seq, hd)
+    sentinel = np.full(nseq * kvh * max_seq * hd, 0x7BCD, np.uint16)
+    dkc, dvc = nlgpu.to_device(sentinel), nlgpu.to_device(sentinel)
+    dq = nlgpu.DeviceArray(rows * nq * 4)
+    args = (nlgpu.to_device(x), nlgpu.to_device(g), 1e-5, nlgpu.to_device(w2), nlgpu.to_device(beta), dq, dkc,
+            dvc, nlgpu.to_device(co), nlgpu.to_device(si), nlgpu.to_device(np.array([pos0], np.int32)))
+    if qper:
+        nlgpu.rms_ternary_qkv_rope_prompt(*args, rows, qper, heads, kvh, hd, max_seq, cols)
+    else:
+        nlgpu.rms_ternary_qkv_rope(*args, rows, heads, kvh, hd, max_seq, cols)
+    qkv = ref.linear(ref.rms(x, g, 1e-5, rows, cols), w2, beta, rows, out, cols, per_row=True).reshape(rows, -1)
+    gq = dq.download(f32, rows * nq).reshape(rows, nq)
+    kc = dkc.download(np.uint16).reshape(nseq, kvh, max_seq, hd)
+    vc = dvc.download(np.uint16).reshape(nseq, kvh, max_seq, hd)
+    if not qper:  # every row at pos0: decode-rope-b over the whole batch at once
+        q = ref.rope_b(qkv[:, :nq].ravel(), co, si, pos0, rows, nq, heads).reshape(rows, nq)
+        k = ref.rope_b(qkv[:, nq:nq + nkv].ravel(), co, si, pos0, rows, nkv, kvh).reshape(rows, kvh, hd)
+        same_bits(gq, q, "q")
+        assert np.array_equal(kc[:, :, pos0], k.astype(np.float16).view(np.uint16))
+        assert np.array_equal(vc[:, :, pos0], qkv[:, nq + nkv:].reshape(rows, kvh, hd).astype(np.float16).view(np.uint16))
+        kc[:, :, pos0] = 0x7BCD
+        vc[:, :, pos0] = 0x7BCD
+    else:
+        for r in range(rows):
+            b, p = r // qper, pos0 + r % qper
+            if p >= max_seq:
+                continue  # q of such a row is unspecified; nothing may reach the caches
+            q = ref.rope_b(qkv[r, :nq], co, si, p, 1, nq, heads)
+            k = ref.rope_b(qkv[r, nq:nq + nkv], co, si, p, 1, nkv, kvh).reshape(kvh, hd)
+            same_bits(gq[r], q, f"q row {r}")
+            assert np.array_equal(kc[b, :, p], k.astype(np.float16).view(np.uint16)), r
+            assert np.array_equal(vc[b, :, p], qkv[r, nq + nkv:].reshape(kvh, hd).astype(np.float16).view(np.uint16)), r
+            kc[b, :, p] = 0x7BCD
+            vc[b, :, p] = 0x7BCD
+    assert np.all(kc == 0x7BCD) and np.all(vc == 0x7BCD)  # nothing else written
+
+
+def test_qkv_prompt_rejects_ragged_rows():
+    d = nlgpu.DeviceArray(1 << 16)
+    pos = nlgpu.to_device(np.array([0], np.int32))
+    with pytest.raises(nlgpu.NlgError, match="qper"):
+        nlgpu.rms_ternary_qkv_rope_prompt(d, d, 1e-5, d, d, d, d, d, d, d, pos, 10, 4, 4, 2, 64, 16, 256)
+    with pytest.raises(nlgpu.NlgError, match="qper"):
+        nlgpu.rms_ternary_qkv_rope_prompt(d, d, 1e-5, d, d, d, d, d, d, d, pos, 10, 0, 4, 2, 64, 16, 256)
