@@ -170,6 +170,7 @@ int nlg_ternary_linear(const float *x, const uint32_t *w2, const float *bias, co
                        int beta_per_row, float *y, float *gamma_out, uint32_t seq, uint32_t out,
                        uint32_t cols, void *workspace, size_t workspace_bytes, void *stream);
 size_t nlg_ternary_linear_workspace(uint32_t seq, uint32_t cols);
+
 /* Tuning variant: rows_per_wave in {1,2,4} for the one-launch form (0 = default). */
 int nlg_ternary_linear_cfg(const float *x, const uint32_t *w2, const float *bias, const float *beta,
                            int beta_per_row, float *y, float *gamma_out, uint32_t seq, uint32_t out,
@@ -190,6 +191,14 @@ int nlg_softmax_rows(const float *a, float *c, uint32_t rows, uint32_t cols, voi
  * The RMSNorm is rmsnorm-istd + rmsnorm-fwd (kernels.el:1249-1265) with eps
  * a parameter: S = 1/sqrt(sum(x*x)/cols + eps), xn = (x*S)*gain; its sum is
  * a tree, so S may differ from the serial loop's in the last bit.
+ * With 8 or more tokens and cols % 256 == 0 each of them (and
+ * nlg_ternary_linear) runs as per-token quantisation into library scratch
+ * followed by the int8 matrix-core GEMM.  That scratch is one per stream:
+ * calls on different streams may overlap.  It grows by allocating, so on a
+ * stream being captured into a graph it must already be large enough (make
+ * the call once on that stream first).  A captured graph keeps using the
+ * scratch of the stream it was captured on: do not replay it while other
+ * batched calls on that stream, or another replay of it, may run.
  * ---------------------------------------------------------------------- */
 
 /* y = linear(rmsnorm(x)) (rmsnorm-istd, rmsnorm-fwd, pack-act-rows,

@@ -268,8 +268,8 @@ bool nlg_batched(uint32_t seq, uint32_t cols);
 int nlg_batched_launch(const FusedArgs &a, int pro, int epi, hipStream_t st);
 // (max, index) partials per token an ARGMAX launch of `out` rows writes.
 uint32_t nlg_argmax_parts(uint32_t seq, uint32_t cols, uint32_t out);
-// Grow-only device scratch owned by the library (NULL on failure).  It
-// cannot grow while `st` is being captured into a graph.
+// Grow-only device scratch owned by the library, one per stream (NULL on
+// failure).  It cannot grow while `st` is being captured into a graph.
 void *nlg_scratch(size_t bytes, hipStream_t st);
 // Bytes the batched form needs for seq tokens of cols columns.
 size_t nlg_batched_scratch_bytes(uint32_t seq, uint32_t cols);

@@ -9,6 +9,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <map>
 #include <mutex>
 #include <vector>
 
@@ -64,31 +65,37 @@ int nlg_num_cu(void) { return g_num_cu; }
 
 hipStream_t nlg_stream(void *s) { return s ? (hipStream_t)s : g_stream; }
 
-// Library scratch for the batched linears' int8 activations: grown by
-// allocating a larger buffer; older ones stay allocated (a captured graph may
-// still use them) until nlg_shutdown.
-static std::vector<void *> g_scratch;
-static size_t g_scratch_bytes = 0;
+// Library scratch for the batched linears' int8 activations, one per stream
+// (calls on different streams may run concurrently; calls on one stream run
+// in order, so they can share).  Grown by allocating a larger buffer; older
+// ones stay allocated (a captured graph may still use them) until
+// nlg_shutdown.
+struct StreamScratch {
+  std::vector<void *> bufs;
+  size_t bytes = 0;
+};
+static std::map<hipStream_t, StreamScratch> g_scratch;
 static std::mutex g_scratch_mu;
 
 void *nlg_scratch(size_t bytes, hipStream_t st) {
   std::lock_guard<std::mutex> lk(g_scratch_mu);
-  if (bytes <= g_scratch_bytes) return g_scratch.back();
+  StreamScratch &e = g_scratch[st];
+  if (bytes <= e.bytes) return e.bufs.back();
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
-    nlg_fail("batched linear: its %zu-byte scratch must be reserved before graph capture "
-             "(run the call once outside the capture first)", bytes);
+    nlg_fail("batched linear: its %zu-byte scratch must be reserved on this stream before graph capture "
+             "(run the call once on it outside the capture first)", bytes);
     return nullptr;
   }
-  size_t want = g_scratch_bytes ? g_scratch_bytes : (1u << 20);
+  size_t want = e.bytes ? e.bytes : (1u << 20);
   while (want < bytes) want *= 2;
   void *p = nullptr;
   if (hipMalloc(&p, want) != hipSuccess) {
     nlg_fail("scratch: hipMalloc(%zu) failed", want);
     return nullptr;
   }
-  g_scratch.push_back(p);
-  g_scratch_bytes = want;
+  e.bufs.push_back(p);
+  e.bytes = want;
   return p;
 }
 
@@ -97,9 +104,9 @@ extern "C" int nlg_shutdown(void) {
   (void)hipDeviceSynchronize();
   {
     std::lock_guard<std::mutex> lk(g_scratch_mu);
-    for (void *p : g_scratch) (void)hipFree(p);
+    for (auto &kv : g_scratch)
+      for (void *p : kv.second.bufs) (void)hipFree(p);
     g_scratch.clear();
-    g_scratch_bytes = 0;
   }
   if (g_stage) {
     (void)hipEventDestroy(g_stage_ev[0]);

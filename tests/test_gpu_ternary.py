@@ -156,3 +156,28 @@ def test_linear_two_launch_path_with_workspace(seq, out, cols):
     ws = nlgpu.DeviceArray(nlgpu.ternary_linear_workspace(seq, cols))
     nlgpu.ternary_linear(dx, dw, db, dbe, dy, seq, out, cols, workspace=ws)
     assert np.array_equal(dy.download(np.float32, seq * out).view(np.uint32), y_ref.view(np.uint32))
+
+
+def test_batched_linears_on_two_streams_do_not_share_scratch():
+    """Batched calls (per-token quantisation into library scratch, then the
+    GEMM) issued back to back on two streams may overlap; each stream has
+    its own scratch, so both give the single-stream bits."""
+    seq, out, cols = 64, 2560, 2560
+    streams = [nlgpu.lib().nlg_stream_create() for _ in range(2)]
+    cases, want = [], []
+    for i in range(2):
+        t, w2, x, bias, beta = make(1000 + i, seq, out, cols)
+        xq, g = orc.pack_act_rows(x, seq, cols)
+        want.append(orc.ternary_linear_i8(xq, g, w2, bias, beta, seq, out, cols))
+        cases.append([nlgpu.to_device(a) for a in (x, w2, bias, beta)] + [nlgpu.DeviceArray(seq * out * 4)])
+    nlgpu.sync()
+    for rep in range(20):  # interleaved: stream 0's quantisation can land between stream 1's
+        for i in (0, 1):
+            dx, dw, db, dbe, dy = cases[i]
+            nlgpu.ternary_linear(dx, dw, db, dbe, dy, seq, out, cols, stream=streams[i])
+    for st in streams:
+        nlgpu.sync(st)
+    for i in (0, 1):
+        assert np.array_equal(cases[i][4].download(np.uint32, seq * out), want[i].view(np.uint32)), i
+    for st in streams:
+        nlgpu.lib().nlg_stream_destroy(st)
