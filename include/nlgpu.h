@@ -171,6 +171,20 @@ int nlg_ternary_linear(const float *x, const uint32_t *w2, const float *bias, co
                        uint32_t cols, void *workspace, size_t workspace_bytes, void *stream);
 size_t nlg_ternary_linear_workspace(uint32_t seq, uint32_t cols);
 
+/* nlg_ternary_linear for callers that cannot allocate (code under graph
+ * capture, tight serving loops): same results, bit for bit, with no
+ * workspace argument and no device allocation on any path.  Whatever
+ * scratch the form needs (packed activations for the two-launch form, int8
+ * activations and scales for the batched form) is a fixed array of
+ * NLG_NOALLOC_SCRATCH_BYTES that the library holds on each GPU until the
+ * process ends; shapes needing more (about seq x cols > 16.7 M) fail with
+ * NLG_ERR and launch nothing.  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams, concurrent graph
+ * replays) race and must not be issued.  No reference counterpart. */
+#define NLG_NOALLOC_SCRATCH_BYTES (16u << 20)
+int nlg_ternary_linear_noalloc(const float *x, const uint32_t *w2, const float *bias, const float *beta,
+                               int beta_per_row, float *y, float *gamma_out, uint32_t seq, uint32_t out,
+                               uint32_t cols, void *stream);
 /* Tuning variant: rows_per_wave in {1,2,4} for the one-launch form (0 = default). */
 int nlg_ternary_linear_cfg(const float *x, const uint32_t *w2, const float *bias, const float *beta,
                            int beta_per_row, float *y, float *gamma_out, uint32_t seq, uint32_t out,

@@ -271,6 +271,9 @@ uint32_t nlg_argmax_parts(uint32_t seq, uint32_t cols, uint32_t out);
 // Grow-only device scratch owned by the library, one per stream (NULL on
 // failure).  It cannot grow while `st` is being captured into a graph.
 void *nlg_scratch(size_t bytes, hipStream_t st);
+// The active device's fixed scratch array (NLG_NOALLOC_SCRATCH_BYTES), or
+// null with the error set.
+void *nlg_noalloc_scratch(void);
 // Bytes the batched form needs for seq tokens of cols columns.
 size_t nlg_batched_scratch_bytes(uint32_t seq, uint32_t cols);
 // The rows-per-wave the launcher uses for `out` rows in mode `epi`.

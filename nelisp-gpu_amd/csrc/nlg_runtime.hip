@@ -27,6 +27,14 @@ static const size_t kStageBytes = 64u << 20;
 static char *g_stage = nullptr;
 static hipEvent_t g_stage_ev[2];
 
+// Scratch of the allocation-free entry points: one fixed array per GPU (the
+// code object's device globals exist once per device), reached through the
+// device address looked up for each device at init.  Host code never uses
+// the array's own name, which on the host is only a stand-in symbol.
+static __device__ __align__(256) uint8_t scratch[NLG_NOALLOC_SCRATCH_BYTES];
+#define NLG_MAX_DEVICES 64
+static void *g_noalloc_scratch[NLG_MAX_DEVICES];
+
 extern "C" const char *nlg_last_error(void) { return g_err; }
 
 int nlg_fail(const char *fmt, ...) {
@@ -48,6 +56,13 @@ extern "C" int nlg_init(int device) {
   if (n <= 0) return nlg_fail("no GPU device visible");
   if (device < 0 || device >= n) device = 0;  // vkcompute.c:100's fallback
   NLG_HIP(hipSetDevice(device));
+  if (device < NLG_MAX_DEVICES && !g_noalloc_scratch[device]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return nlg_fail("init: no device address for the fixed scratch array (%s)", hipGetErrorString(e));
+    g_noalloc_scratch[device] = p;
+  }
   hipDeviceProp_t prop;
   NLG_HIP(hipGetDeviceProperties(&prop, device));
   g_num_cu = prop.multiProcessorCount;
@@ -61,6 +76,14 @@ extern "C" int nlg_init(int device) {
 }
 
 int nlg_ensure_init(void) { return g_inited ? NLG_OK : nlg_init(-1); }
+
+void *nlg_noalloc_scratch(void) {
+  if (!g_inited || g_device >= NLG_MAX_DEVICES || !g_noalloc_scratch[g_device]) {
+    nlg_fail("fixed scratch: device %d has none (library not initialised?)", g_device);
+    return nullptr;
+  }
+  return g_noalloc_scratch[g_device];
+}
 int nlg_num_cu(void) { return g_num_cu; }
 
 hipStream_t nlg_stream(void *s) { return s ? (hipStream_t)s : g_stream; }

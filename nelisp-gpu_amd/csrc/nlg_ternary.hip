@@ -442,20 +442,24 @@ extern "C" int nlg_ternary_linear_i8(const uint32_t *xq, const float *gamma, con
 // ---------------------------------------- fused: quantise + GEMV, one launch
 // (k_tern_fused in nlg_layer.hip; this entry point is its plain form)
 
-extern "C" int nlg_ternary_linear_cfg(const float *x, const uint32_t *w2, const float *bias,
-                                      const float *beta, int beta_per_row, float *y, float *gamma_out,
-                                      uint32_t seq, uint32_t out, uint32_t cols, int rows_per_wave,
-                                      void *workspace, size_t workspace_bytes, void *stream) {
-  if (nlg_ensure_init()) return NLG_ERR;
-  if (!seq || !out) return NLG_OK;
-  hipStream_t st = nlg_stream(stream);
+// The three forms of the whole linear: one fused launch for a few tokens,
+// the batched matrix-core form for many (its int8 activations in act_scratch,
+// or the library's per-stream scratch when null), else pack-act-rows into
+// the workspace and the GEMV.
+static bool linear_fusable(const float *x, const uint32_t *w2, uint32_t seq, uint32_t cols) {
   const bool aligned = (((uintptr_t)x & 15) == 0) && (((uintptr_t)w2 & 15) == 0);
-  // one launch for a few tokens; many tokens take the batched matrix-core form
-  const bool fusable = (cols % 64 == 0) && cols <= 16384 && aligned && (seq <= 4 || nlg_batched(seq, cols));
-  if (fusable) {
+  return (cols % 64 == 0) && cols <= 16384 && aligned && (seq <= 4 || nlg_batched(seq, cols));
+}
+
+static int linear_go(const float *x, const uint32_t *w2, const float *bias, const float *beta, int beta_per_row,
+                     float *y, float *gamma_out, uint32_t seq, uint32_t out, uint32_t cols, int rows_per_wave,
+                     void *workspace, size_t workspace_bytes, void *act_scratch, size_t act_scratch_bytes,
+                     hipStream_t st) {
+  if (linear_fusable(x, w2, seq, cols)) {
     FusedArgs a{};
     a.x = x; a.w2 = w2; a.bias = bias; a.beta = beta; a.beta_per_row = beta_per_row;
     a.y = y; a.ystride = out; a.gamma_out = gamma_out; a.seq = seq; a.out = out; a.cols = cols;
+    a.act_scratch = act_scratch; a.act_scratch_bytes = act_scratch_bytes;
     int rpw = rows_per_wave;
     if (rpw != 1 && rpw != 2 && rpw != 4) rpw = 0;  // the launcher's default
     return nlg_fused_launch(a, NLG_PRO_NONE, NLG_EPI_STORE, rpw, st);
@@ -472,6 +476,36 @@ extern "C" int nlg_ternary_linear_cfg(const float *x, const uint32_t *w2, const 
   int rpw, wpb;
   tern_default_geometry(out, seq, &rpw, &wpb);
   return tern_launch(ta, rpw, wpb, st);
+}
+
+extern "C" int nlg_ternary_linear_cfg(const float *x, const uint32_t *w2, const float *bias,
+                                      const float *beta, int beta_per_row, float *y, float *gamma_out,
+                                      uint32_t seq, uint32_t out, uint32_t cols, int rows_per_wave,
+                                      void *workspace, size_t workspace_bytes, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!seq || !out) return NLG_OK;
+  return linear_go(x, w2, bias, beta, beta_per_row, y, gamma_out, seq, out, cols, rows_per_wave, workspace,
+                   workspace_bytes, nullptr, 0, nlg_stream(stream));
+}
+
+// The same linear with every scratch byte in the library's fixed array:
+// no allocation on any path (for graph capture and callers that cannot
+// allocate).  Calls that overlap on one GPU share the array and race.
+extern "C" int nlg_ternary_linear_noalloc(const float *x, const uint32_t *w2, const float *bias,
+                                          const float *beta, int beta_per_row, float *y, float *gamma_out,
+                                          uint32_t seq, uint32_t out, uint32_t cols, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!seq || !out) return NLG_OK;
+  const size_t need = linear_fusable(x, w2, seq, cols)
+                          ? (nlg_batched(seq, cols) ? nlg_batched_scratch_bytes(seq, cols) : 0)
+                          : nlg_ternary_linear_workspace(seq, cols);
+  if (need > NLG_NOALLOC_SCRATCH_BYTES)
+    return nlg_fail("ternary linear (no allocation): %u tokens x %u columns need %zu bytes of scratch, "
+                    "more than the fixed %zu", seq, cols, need, (size_t)NLG_NOALLOC_SCRATCH_BYTES);
+  void *scr = nlg_noalloc_scratch();
+  if (!scr) return NLG_ERR;
+  return linear_go(x, w2, bias, beta, beta_per_row, y, gamma_out, seq, out, cols, 0, scr,
+                   NLG_NOALLOC_SCRATCH_BYTES, scr, NLG_NOALLOC_SCRATCH_BYTES, nlg_stream(stream));
 }
 
 extern "C" size_t nlg_ternary_linear_workspace(uint32_t seq, uint32_t cols) {

@@ -90,6 +90,7 @@ def lib() -> C.CDLL:
         "nlg_ternary_linear": (i32, [vp, vp, vp, vp, i32, vp, vp, u32, u32, u32, vp, sz, vp]),
         "nlg_ternary_linear_cfg": (i32, [vp, vp, vp, vp, i32, vp, vp, u32, u32, u32, i32, vp, sz, vp]),
         "nlg_ternary_linear_workspace": (sz, [u32, u32]),
+        "nlg_ternary_linear_noalloc": (i32, [vp, vp, vp, vp, i32, vp, vp, u32, u32, u32, vp]),
         "nlg_rms_ternary_linear": (i32, [vp, vp, C.c_float, vp, vp, vp, i32, vp, u32, u32, u32, vp]),
         "nlg_ternary_linear_residual": (i32, [vp, vp, vp, vp, i32, vp, vp, u32, u32, u32, vp]),
         "nlg_rms_ternary_swiglu": (i32, [vp, vp, C.c_float, vp, vp, i32, vp, u32, u32, u32, vp]),
@@ -285,6 +286,13 @@ def ternary_linear(x, w2, bias, beta, y, seq, out, cols, beta_per_row=False, gam
     else:
         rc = L.nlg_ternary_linear(*args, ws, wsb, stream)
     _check(rc, "ternary_linear")
+
+
+def ternary_linear_noalloc(x, w2, bias, beta, y, seq, out, cols, beta_per_row=False, gamma_out=None,
+                           stream=None) -> None:
+    """ternary_linear with its scratch in the library's fixed array."""
+    _check(lib().nlg_ternary_linear_noalloc(x.ptr, w2.ptr, _ptr(bias), beta.ptr, int(beta_per_row), y.ptr,
+                                            _ptr(gamma_out), seq, out, cols, stream), "ternary_linear_noalloc")
 
 
 def ternary_linear_workspace(seq: int, cols: int) -> int:
