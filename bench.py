@@ -50,26 +50,54 @@ STEP_TRAFFIC = 4520462 + 16384
 METRIC = "ternary GEMV GB/s (% HBM peak) at 4096²; decode tok/s, 2B ternary model, batch 1"
 
 
-def timed(fn, n, stream):
-    """Average ms per call of fn(i) for i in 0..n-1.  The calls are captured
-    into a HIP graph of COPIES launches (one pass over the rotating weight
-    copies) replayed n/COPIES times between two events, so host-side launch
-    overhead (Python, ctypes, hipLaunchKernel) is not what gets measured."""
+def timed(fn, n, stream, stats=None):
+    """Average ms per call of fn(i) over at least max(n, 200) calls.  The
+    calls are captured into a HIP graph of COPIES launches (one pass over the
+    rotating weight copies) replayed R = max(16, ceil(max(n, 200) / COPIES))
+    times, each replay between its own pair of events on the launch stream,
+    so host-side launch overhead (Python, ctypes, hipLaunchKernel) is not
+    what gets measured.  Returns the mean over all R * COPIES launches; when
+    `stats` is a dict it also receives the launch count and the median / p10
+    / p90 of the per-launch time across the replays."""
     import nlgpu
     nlgpu.graph_begin(stream)
     for i in range(COPIES):
         fn(i)
     g = nlgpu.graph_end(stream)
-    reps = max(1, n // COPIES)
+    reps = max(16, -(-max(n, 200) // COPIES))
     nlgpu.graph_launch(g, stream)  # warm replay
+    ev = [nlgpu.Event() for _ in range(reps + 1)]
+    ev[0].record(stream)
+    for r in range(reps):
+        nlgpu.graph_launch(g, stream)
+        ev[r + 1].record(stream)
+    per = np.array([ev[r].elapsed_ms(ev[r + 1]) / COPIES for r in range(reps)])
+    ms = ev[0].elapsed_ms(ev[reps]) / (reps * COPIES)
+    nlgpu.graph_destroy(g)
+    if stats is not None:
+        stats.update(launches=reps * COPIES, replays=reps, mean_us=round(ms * 1e3, 4),
+                     median_us=round(float(np.median(per)) * 1e3, 4),
+                     p10_us=round(float(np.percentile(per, 10)) * 1e3, 4),
+                     p90_us=round(float(np.percentile(per, 90)) * 1e3, 4))
+    return ms
+
+
+def copy_peak_gbs(stream, nbytes=1 << 30, reps=10):
+    """Device-to-device copy rate (bytes read + written per second) of a
+    1 GiB buffer, the measured ceiling next to the 8 TB/s spec peak."""
+    import nlgpu
+    a, b = nlgpu.DeviceArray(nbytes), nlgpu.DeviceArray(nbytes)
+    L = nlgpu.lib()
+    L.nlg_copy_d2d(b.ptr, a.ptr, nbytes, stream)
     e0, e1 = nlgpu.Event(), nlgpu.Event()
     e0.record(stream)
     for _ in range(reps):
-        nlgpu.graph_launch(g, stream)
+        L.nlg_copy_d2d(b.ptr, a.ptr, nbytes, stream)
     e1.record(stream)
-    ms = e0.elapsed_ms(e1) / (reps * COPIES)
-    nlgpu.graph_destroy(g)
-    return ms
+    gbs = 2 * nbytes * reps / (e0.elapsed_ms(e1) * 1e-3) / 1e9
+    a.free()
+    b.free()
+    return gbs
 
 
 def gpu_bench(steps: int, warmup: int, sweep: bool):
@@ -112,7 +140,8 @@ def gpu_bench(steps: int, warmup: int, sweep: bool):
     for i in range(warmup):
         step(i)
     nlgpu.sync()
-    res["step_ms"] = timed(step, steps, stream)
+    res["step_stats"] = {}
+    res["step_ms"] = timed(step, steps, stream, res["step_stats"])
     nlgpu.sync()
     for i in range(warmup):
         gemv(i)
@@ -132,6 +161,8 @@ def gpu_bench(steps: int, warmup: int, sweep: bool):
     nlgpu.sync()
     # launch floor: an empty fill of 16 bytes, back to back
     res["floor_ms"] = timed(lambda i: L.nlg_zero(dg.ptr, 4, stream), steps, stream)
+    nlgpu.sync()
+    res["copy_gbs"] = copy_peak_gbs(stream)
     nlgpu.sync()
     if sweep:
         sw = {}
@@ -514,22 +545,154 @@ def ring_bench(stream):
     return res
 
 
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _lavapipe_probe():
+    """Whether the reference's own kernels could run through Vulkan on Mesa
+    lavapipe here: that needs Emacs (the kernels are an Elisp DSL compiled to
+    SPIR-V by Elisp), a Vulkan loader, the lavapipe ICD and the reference
+    sources, which never reach the GPU box."""
+    import ctypes.util
+    import glob
+    import shutil
+    missing = []
+    if not shutil.which("emacs"):
+        missing.append("emacs")
+    if not ctypes.util.find_library("vulkan"):
+        missing.append("libvulkan")
+    if not glob.glob("/usr/share/vulkan/icd.d/lvp_icd*.json") + glob.glob("/etc/vulkan/icd.d/lvp_icd*.json"):
+        missing.append("lavapipe ICD (lvp_icd*.json)")
+    missing.append("the reference sources (only this repository is on the GPU box)")
+    return "not run: missing " + ", ".join(missing)
+
+
+def _cpu_trits2(rng, out, cols):
+    """Random 2-bit ternary rows for the CPU samples: field = 00 (p 1/2),
+    01 or 11 (p 1/4 each), the trit distribution of the configs."""
+    wng = (cols + 15) // 16
+    lo = rng.integers(0, 1 << 32, (out, wng), dtype=np.uint64).astype(np.uint32) & np.uint32(0x55555555)
+    r = rng.integers(0, 1 << 32, (out, wng), dtype=np.uint64).astype(np.uint32) & np.uint32(0x55555555)
+    return lo | ((lo & r) << np.uint32(1))
+
+
+def _time_loop(fn, seconds):
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            return n, dt
+
+
 def cpu_baseline(x, w_one, seconds: float):
+    """The C restatement of the reference kernels (oracle/, OpenMP over
+    invocations, -O2 -ffp-contract=off) on the host cores: config 2 for
+    `seconds`, then bounded samples of configs 3, 4 and 5."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import nlg_oracle as orc
 
     beta = np.array([1.0], np.float32)
-    n, t0 = 0, time.perf_counter()
-    while True:
+
+    def step():
         xq, g = orc.pack_act_rows(x, 1, COLS)
         orc.ternary_linear_i8(xq, g, w_one, None, beta, 1, OUT, COLS)
-        n += 1
-        dt = time.perf_counter() - t0
-        if dt >= seconds:
-            break
-    return dict(value=round(STEP_BYTES * n / dt / 1e9, 3), unit="GB/s", cores=orc.threads(), kind="port",
-                sample=f"{n} steps of the 4096x4096 config-2 step (pack-act-rows + ternary GEMV, C "
-                       f"restatement of the reference kernels, OpenMP over output rows) in {dt:.1f} s")
+
+    n, dt = _time_loop(step, seconds)
+    res = dict(value=round(STEP_BYTES * n / dt / 1e9, 3), unit="GB/s", cores=orc.threads(), kind="port",
+               sample=f"{n} steps of the 4096x4096 config-2 step (pack-act-rows + ternary GEMV, C "
+                      f"restatement of the reference kernels, OpenMP over output rows) in {dt:.1f} s",
+               cpu_model=_cpu_model(), threads=orc.threads(), lavapipe=_lavapipe_probe())
+    rng = np.random.default_rng(20260921)
+    part = max(1.0, seconds / 3)
+    other = {}
+    # config 3: softmax rows of one causal 4096-wide head tile (rows 2048..2559)
+    rows = 512
+    a = (rng.standard_normal((rows, SM_N)) * 3.0).astype(np.float32)
+    a[np.arange(SM_N)[None, :] > (2048 + np.arange(rows))[:, None]] = -np.inf
+    n, dt = _time_loop(lambda: orc.softmax_rows(a, rows, SM_N), part)
+    other["softmax_config3"] = {"gbs": round(2 * 4 * rows * SM_N * n / dt / 1e9, 3),
+                                "sample": f"{n} x {rows} causal rows of 4096 in {dt:.1f} s (bytes = read + write)"}
+    # config 4: the SwiGLU FFN at B = 1 (gate|up linear, silu-mul, down linear)
+    wgu, wd = _cpu_trits2(rng, 2 * FFN_F, FFN_D), _cpu_trits2(rng, FFN_D, FFN_F)
+    xf = rng.standard_normal(FFN_D).astype(np.float32)
+    bgu = np.full(2 * FFN_F, 1.0 / np.sqrt(FFN_D / 2), np.float32)
+    bdn = np.array([1.0 / np.sqrt(FFN_F / 2)], np.float32)
+
+    def ffn():
+        xq, g = orc.pack_act_rows(xf, 1, FFN_D)
+        gu = orc.ternary_linear_i8(xq, g, wgu, None, bgu, 1, 2 * FFN_F, FFN_D, beta_per_row=True)
+        h = np.zeros(FFN_F, np.float32)
+        orc.dispatch("silu-mul", [np.ascontiguousarray(gu[0::2]), np.ascontiguousarray(gu[1::2]), h], [FFN_F],
+                     (FFN_F + 63) // 64)
+        hq, hg = orc.pack_act_rows(h, 1, FFN_F)
+        orc.ternary_linear_i8(hq, hg, wd, None, bdn, 1, FFN_D, FFN_F)
+
+    n, dt = _time_loop(ffn, part)
+    ffn_bytes = wgu.nbytes + wd.nbytes + 2 * FFN_D * 4
+    other["swiglu_ffn_config4_B1"] = {"us": round(dt / n * 1e6, 1), "gbs": round(ffn_bytes * n / dt / 1e9, 3),
+                                      "sample": f"{n} FFNs at one token in {dt:.1f} s"}
+    # config 5 at B = 1: one decoder layer at position 640 (the mean attended
+    # length), extrapolated to 30 layers, plus the LM head timed on a slice
+    c = STACK
+    d, f, hd = c["d_model"], c["d_ff"], c["head_dim"]
+    nq, nkv, ms = c["heads"] * hd, c["kv_heads"] * hd, PROMPT + DECODE
+    wqkv, wo = _cpu_trits2(rng, nq + 2 * nkv, d), _cpu_trits2(rng, d, nq)
+    bq = np.full(nq + 2 * nkv, 1.0 / np.sqrt(d / 2), np.float32)
+    bo = np.array([1.0 / np.sqrt(nq / 2)], np.float32)
+    gain = np.ones(d, np.float32)
+    kc = rng.standard_normal(c["kv_heads"] * ms * hd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(c["kv_heads"] * ms * hd).astype(np.float16).view(np.uint16)
+    xs = rng.standard_normal(d).astype(np.float32)
+    ang = np.outer(np.arange(ms), 1.0 / c.get("rope_theta", 500000.0) ** (np.arange(hd // 2) * 2.0 / hd))
+    co, si = np.cos(ang).astype(np.float32).ravel(), np.sin(ang).astype(np.float32).ravel()
+    pos = 640
+
+    def lin(v, w, b, out, cols, per_row=False):
+        vq, vg = orc.pack_act_rows(np.ascontiguousarray(v, np.float32), 1, cols)
+        return orc.ternary_linear_i8(vq, vg, w, None, b, 1, out, cols, beta_per_row=per_row)
+
+    def rope(v, cols, heads):
+        o = np.zeros(cols, np.float32)
+        orc.dispatch("decode-rope-b", [np.ascontiguousarray(v, np.float32), co, si, np.array([1.0], np.float32),
+                                       np.array([float(pos)], np.float32), o], [1, cols, heads], (cols // 2 + 63) // 64)
+        return o
+
+    def layer():
+        xn = orc.rmsnorm_rows(xs, gain, 1e-5, 1, d)
+        qkv = lin(xn, wqkv, bq, nq + 2 * nkv, d, True)
+        q = rope(qkv[:nq], nq, c["heads"])
+        rope(qkv[nq:nq + nkv], nkv, c["kv_heads"])
+        att = orc.decode_attn_f16(q, kc, vc, pos, 1, c["heads"], c["kv_heads"], hd, ms)
+        x1 = (xs + lin(att, wo, bo, d, nq)).astype(np.float32)
+        xn = orc.rmsnorm_rows(x1, gain, 1e-5, 1, d)
+        gu = lin(xn, wgu, bgu, 2 * f, d, True)
+        h = np.zeros(f, np.float32)
+        orc.dispatch("silu-mul", [np.ascontiguousarray(gu[0::2]), np.ascontiguousarray(gu[1::2]), h], [f],
+                     (f + 63) // 64)
+        return (x1 + lin(h, wd, bdn, d, f)).astype(np.float32)
+
+    n, dt = _time_loop(layer, part)
+    t_layer = dt / n
+    head_rows = 16384
+    wlm = _cpu_trits2(rng, head_rows, d)
+    nh, dth = _time_loop(lambda: lin(xs, wlm, bo, head_rows, d), 0.5)
+    t_head = dth / nh * c["vocab"] / head_rows
+    t_tok = c["layers"] * t_layer + t_head
+    other["decode_config5_B1"] = {"tok_s": round(1.0 / t_tok, 3), "ms_per_token": round(t_tok * 1e3, 1),
+                                  "sample": f"{n} decoder layers at position {pos} in {dt:.1f} s (x30), plus the "
+                                            f"LM head timed on {head_rows} of its {c['vocab']} rows "
+                                            f"({nh} passes, scaled by rows)"}
+    res["other_configs"] = other
+    return res
 
 
 def pmc_probe():
@@ -645,7 +808,8 @@ def main():
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": r["step_stats"]["launches"],
+        "steps_requested": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(r["step_ms"], 6),
         "higher_is_better": True,
@@ -657,8 +821,12 @@ def main():
                                "128 rotated weight copies (512 MiB)",
                    "out": OUT, "cols": COLS, "batch": 1, "weight_copies": COPIES,
                    "step": "one launch: pack-act-rows quantisation fused into the ternary GEMV"},
+        "timing": dict(r["step_stats"], how="HIP events around each replay of a 128-launch graph on the "
+                                             "kernel's stream; value uses the mean over every launch"),
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4), "traffic": STEP_TRAFFIC,
+                     "copy_peak_gbs": round(r["copy_gbs"], 1),
+                     "frac_of_copy_peak": round(value / r["copy_gbs"], 4),
                      "traffic_source": "profiles/ternary_gemv_4096_decode_pmc_traffic.md (FETCH_SIZE x 1.9993 "
                                        "+ WRITE_SIZE, calibrated on a 64 MiB copy)",
                      "kernel": "k_tern_fused", "bytes_per_launch": STEP_BYTES,
