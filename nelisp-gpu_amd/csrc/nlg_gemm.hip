@@ -1,89 +1,110 @@
 // nlg_gemm.hip -- f32 GEMM behind matmul, matmul-tiled, matmul-reg, linear
 // (lisp/nelisp-gpu-kernels.el:17-27, :71-107, :129).
 //
-// The reference has three schedules of the same product (naive, 16x16 LDS
-// tiles, 4x4 register tiles) plus `linear` (X.W^T + bias).  One 64x64-tile
-// kernel serves all four: 256 threads, each accumulating a 4x4 block strided
-// by 16 so LDS reads are conflict-free, 16-deep K steps staged through LDS.
-// Accumulation uses FMA; parity with the serial reference is by tolerance,
-// and integer-valued inputs (host/vkmatmul.c:92-93) are exact.
+// Each output element is one dependent chain of f32 additions in the
+// reference, so one kernel serves all four names with the reference's own
+// summation order per name (bit-identical results):
+//   matmul, matmul-reg, linear  acc = acc + a*b for k = 0..K-1 (acc starts at
+//                               0, or at the bias for linear);
+//   matmul-tiled                per 16-wide k tile, p0 + (p1 + (... + (p14 +
+//                               p15))) added to acc (the tile sum the
+//                               reference writes out, zero products past K).
+// The chain length bounds the time, not the flops, so the work is spread
+// as wide as it goes: one 256-thread workgroup per 16 x 16 output tile (a
+// 256^3 product is 256 workgroups, one per CU), one output per thread, the
+// tile's A rows and B columns for 256 values of k staged through LDS with
+// every global load of a chunk issued before the first is used.
+//
+// Partial grids: a dispatch of `groups` workgroups covers only the outputs
+// the reference's invocations gid < 64*groups (matmul-tiled: workgroups
+// wg < groups) would write; the rest of C is left as it was.
 #include "nlg_internal.h"
 
-template <bool TRANS_B, bool BIAS>
-__global__ __launch_bounds__(256) void k_sgemm(const float *__restrict__ A, const float *__restrict__ B,
-                                               const float *__restrict__ bias, float *__restrict__ C,
-                                               uint32_t M, uint32_t N, uint32_t K) {
-  __shared__ float As[16][64 + 4];
-  __shared__ float Bs[16][64 + 4];
-  const uint32_t m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-  const uint32_t t = threadIdx.x, tx = t % 16, ty = t / 16;
-  float acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
+#define MM_T 16    // output tile edge
+#define MM_KC 256  // k per LDS stage
 
-  for (uint32_t k0 = 0; k0 < K; k0 += 16) {
-    {  // A tile: 64 rows x 16 k; thread t loads row t/4, k (t%4)*4 .. +3
-      const uint32_t m = t / 4, kq = (t % 4) * 4;
+enum { MM_SERIAL = 0, MM_TILE16 = 1 };
+// which outputs a partial grid covers: by row-major index, by 4x4 block
+// index (matmul-reg), or by 16x16 tile index (matmul-tiled)
+enum { LIM_INDEX = 0, LIM_BLOCK4 = 1, LIM_TILE16 = 2 };
+
+template <int ORDER, bool TRANS_B, bool BIAS>
+__global__ __launch_bounds__(256) void k_mm(const float *__restrict__ A, const float *__restrict__ B,
+                                            const float *__restrict__ bias, float *__restrict__ C, uint32_t M,
+                                            uint32_t N, uint32_t K, int lim_mode, uint64_t lim) {
+  __shared__ float As[MM_T][MM_KC + 1];
+  __shared__ float Bs[MM_KC][MM_T + 1];
+  const uint32_t t = threadIdx.x, tx = t & 15, ty = t >> 4;
+  const uint32_t m0 = blockIdx.y * MM_T, n0 = blockIdx.x * MM_T;
+  const uint32_t row = m0 + ty, col = n0 + tx;
+  float acc = 0.0f;
+  if (BIAS) acc = col < N ? bias[col] : 0.0f;
+  for (uint32_t k0 = 0; k0 < K; k0 += MM_KC) {
+    const uint32_t kc = K - k0 < MM_KC ? K - k0 : MM_KC;
+    float ra[MM_T], rb[MM_T];
+    // A rows m0..m0+15, k0..k0+255: lane t reads column k0+t of each row
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint32_t gm = m0 + m, gk = k0 + kq + q;
-        As[kq + q][m] = (gm < M && gk < K) ? A[(size_t)gm * K + gk] : 0.0f;
+    for (int j = 0; j < MM_T; j++) {
+      const uint32_t r = m0 + j;
+      ra[j] = (r < M && t < kc) ? A[(size_t)r * K + k0 + t] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < MM_T; j++) {
+      if (TRANS_B) {  // W [N x K]: lane t reads k0+t of rows n0..n0+15
+        const uint32_t c = n0 + j;
+        rb[j] = (c < N && t < kc) ? B[(size_t)c * K + k0 + t] : 0.0f;
+      } else {  // B [K x N]: lanes read 16 consecutive columns of 16 k rows
+        const uint32_t kk = 16 * j + (t >> 4), c = n0 + (t & 15);
+        rb[j] = (kk < kc && c < N) ? B[(size_t)(k0 + kk) * N + c] : 0.0f;
       }
     }
-    if (TRANS_B) {  // W is N x K (linear): thread t loads n t/4, k (t%4)*4 .. +3
-      const uint32_t n = t / 4, kq = (t % 4) * 4;
+    __syncthreads();  // the previous stage has been consumed
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint32_t gn = n0 + n, gk = k0 + kq + q;
-        Bs[kq + q][n] = (gn < N && gk < K) ? B[(size_t)gn * K + gk] : 0.0f;
-      }
-    } else {  // B is K x N: thread t loads k t/16, n (t%16)*4 .. +3
-      const uint32_t kk = t / 16, nq = (t % 16) * 4;
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint32_t gk = k0 + kk, gn = n0 + nq + q;
-        Bs[kk][nq + q] = (gk < K && gn < N) ? B[(size_t)gk * N + gn] : 0.0f;
-      }
+    for (int j = 0; j < MM_T; j++) {
+      As[j][t] = ra[j];
+      if (TRANS_B) Bs[t][j] = rb[j];
+      else Bs[16 * j + (t >> 4)][t & 15] = rb[j];
     }
     __syncthreads();
+    if (ORDER == MM_SERIAL) {
+      // acc = acc + a*b, k ascending (kernels.el:24-26, :78-80)
+      for (uint32_t k = 0; k < kc; k++) acc = __fadd_rn(acc, __fmul_rn(As[ty][k], Bs[k][tx]));
+    } else {
+      // kernels.el:99-104: acc + (p0 + (p1 + ... (p14 + p15))) per tile of 16
+      for (uint32_t kb = 0; kb < kc; kb += 16) {
+        float s = __fmul_rn(As[ty][kb + 15], Bs[kb + 15][tx]);
 #pragma unroll
-    for (int kk = 0; kk < 16; kk++) {
-      float a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) a[i] = As[kk][ty + 16 * i];
-#pragma unroll
-      for (int j = 0; j < 4; j++) b[j] = Bs[kk][tx + 16 * j];
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        for (int q = 14; q >= 0; q--) s = __fadd_rn(__fmul_rn(As[ty][kb + q], Bs[kb + q][tx]), s);
+        acc = __fadd_rn(acc, s);
+      }
     }
-    __syncthreads();
   }
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const uint32_t gm = m0 + ty + 16 * i;
-    if (gm >= M) continue;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint32_t gn = n0 + tx + 16 * j;
-      if (gn < N) C[(size_t)gm * N + gn] = BIAS ? __fadd_rn(bias[gn], acc[i][j]) : acc[i][j];
-    }
+  if (row >= M || col >= N) return;
+  uint64_t at;
+  if (lim_mode == LIM_INDEX) at = (uint64_t)row * N + col;
+  else if (lim_mode == LIM_BLOCK4) at = (uint64_t)(row / 4) * ((N + 3) / 4) + col / 4;
+  else at = (uint64_t)(row / 16) * ((N + 15) / 16) + col / 16;
+  if (at < lim) C[(size_t)row * N + col] = acc;
+}
+
+template <int ORDER>
+static void mm_go(const float *A, const float *B, const float *bias, float *C, uint32_t M, uint32_t N, uint32_t K,
+                  bool trans_b, int lim_mode, uint64_t lim, hipStream_t st) {
+  const dim3 g(nlg_blocks(N, MM_T), nlg_blocks(M, MM_T)), b(256);
+  if (trans_b) {
+    if (bias) hipLaunchKernelGGL((k_mm<ORDER, true, true>), g, b, 0, st, A, B, bias, C, M, N, K, lim_mode, lim);
+    else hipLaunchKernelGGL((k_mm<ORDER, true, false>), g, b, 0, st, A, B, bias, C, M, N, K, lim_mode, lim);
+  } else {
+    hipLaunchKernelGGL((k_mm<ORDER, false, false>), g, b, 0, st, A, B, bias, C, M, N, K, lim_mode, lim);
   }
 }
 
-static int sgemm(const float *A, const float *B, const float *bias, float *C, uint32_t M, uint32_t N,
-                 uint32_t K, bool trans_b, hipStream_t st, const char *name) {
-  if (!M || !N) return NLG_OK;
-  dim3 g(nlg_blocks(N, 64), nlg_blocks(M, 64)), b(256);
-  if (trans_b) {
-    if (bias) hipLaunchKernelGGL((k_sgemm<true, true>), g, b, 0, st, A, B, bias, C, M, N, K);
-    else hipLaunchKernelGGL((k_sgemm<true, false>), g, b, 0, st, A, B, bias, C, M, N, K);
-  } else {
-    hipLaunchKernelGGL((k_sgemm<false, false>), g, b, 0, st, A, B, bias, C, M, N, K);
-  }
+static int mm(const float *A, const float *B, const float *bias, float *C, uint32_t M, uint32_t N, uint32_t K,
+              bool trans_b, int order, int lim_mode, uint64_t lim, hipStream_t st, const char *name) {
+  if (!M || !N || !lim) return NLG_OK;
+  if (nlg_blocks(M, MM_T) > 65535) return nlg_fail("%s: M = %u is too large", name, M);
+  if (order == MM_TILE16) mm_go<MM_TILE16>(A, B, bias, C, M, N, K, trans_b, lim_mode, lim, st);
+  else mm_go<MM_SERIAL>(A, B, bias, C, M, N, K, trans_b, lim_mode, lim, st);
   NLG_LAUNCHED(name);
   return NLG_OK;
 }
@@ -96,45 +117,41 @@ static int mm_check(const nlg_buffer *b, uint32_t M, uint32_t K, uint32_t N, con
   return NLG_OK;
 }
 
-// matmul (kernels.el:17-27): A B C; push (M K N); one invocation per C element
+// matmul (kernels.el:17-27): A B C; push (M K N); invocation idx < M*N
+// writes C[idx]
 int L_matmul(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
   const uint32_t M = p[0], K = p[1], N = p[2];
-  if (nlg_domain((uint64_t)M * N, groups) < (uint64_t)M * N)
-    return nlg_fail("matmul: %u groups do not cover %u x %u outputs", groups, M, N);
   if (mm_check(b, M, K, N, "matmul")) return NLG_ERR;
-  return sgemm((const float *)b[0].ptr, (const float *)b[1].ptr, nullptr, (float *)b[2].ptr, M, N, K,
-               false, st, "matmul");
+  return mm((const float *)b[0].ptr, (const float *)b[1].ptr, nullptr, (float *)b[2].ptr, M, N, K, false,
+            MM_SERIAL, LIM_INDEX, nlg_domain((uint64_t)M * N, groups), st, "matmul");
 }
-// matmul-tiled (kernels.el:82-107): one 16x16 workgroup per C tile
+// matmul-tiled (kernels.el:82-107): workgroup wg (of groups) writes C tile wg
 int L_matmul_tiled(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
   const uint32_t M = p[0], K = p[1], N = p[2];
-  const uint64_t tiles = (uint64_t)((M + 15) / 16) * ((N + 15) / 16);
-  if (groups < tiles) return nlg_fail("matmul-tiled: %u groups do not cover %llu tiles", groups,
-                                      (unsigned long long)tiles);
   if (mm_check(b, M, K, N, "matmul-tiled")) return NLG_ERR;
-  return sgemm((const float *)b[0].ptr, (const float *)b[1].ptr, nullptr, (float *)b[2].ptr, M, N, K,
-               false, st, "matmul-tiled");
+  return mm((const float *)b[0].ptr, (const float *)b[1].ptr, nullptr, (float *)b[2].ptr, M, N, K, false,
+            MM_TILE16, LIM_TILE16, groups, st, "matmul-tiled");
 }
-// matmul-reg (kernels.el:129): a 4x4 micro-tile per invocation; the
-// reference writes past row ends unless M and N are multiples of 4.
+// matmul-reg (kernels.el:129): invocation idx writes the 4x4 block idx (row
+// block idx / ceil(N/4)); the reference writes past row ends unless M and N
+// are multiples of 4, so other shapes are refused.
 int L_matmul_reg(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
   const uint32_t M = p[0], K = p[1], N = p[2];
   if (M % 4 || N % 4) return nlg_fail("matmul-reg: M and N must be multiples of 4 (got %u, %u)", M, N);
-  const uint64_t blocks = (uint64_t)(M / 4) * (N / 4);
-  if (nlg_domain(blocks, groups) < blocks) return nlg_fail("matmul-reg: groups do not cover the output");
   if (mm_check(b, M, K, N, "matmul-reg")) return NLG_ERR;
-  return sgemm((const float *)b[0].ptr, (const float *)b[1].ptr, nullptr, (float *)b[2].ptr, M, N, K,
-               false, st, "matmul-reg");
+  const uint64_t blocks = (uint64_t)(M / 4) * (N / 4);
+  return mm((const float *)b[0].ptr, (const float *)b[1].ptr, nullptr, (float *)b[2].ptr, M, N, K, false,
+            MM_SERIAL, LIM_BLOCK4, nlg_domain(blocks, groups), st, "matmul-reg");
 }
-// linear (kernels.el:71-81): X W B C; push (M IN OUT); C = X.W^T + B
+// linear (kernels.el:71-81): X W B C; push (M IN OUT); C = B + X.W^T,
+// invocation idx < M*OUT writes C[idx]
 int L_linear(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
   const uint32_t M = p[0], IN = p[1], OUT = p[2];
-  if (nlg_domain((uint64_t)M * OUT, groups) < (uint64_t)M * OUT)
-    return nlg_fail("linear: groups do not cover the output");
   const char *k = "linear";
   if (nlg_need(b, 0, (uint64_t)M * IN, k) || nlg_need(b, 1, (uint64_t)OUT * IN, k) ||
       nlg_need(b, 2, OUT, k) || nlg_need(b, 3, (uint64_t)M * OUT, k))
     return NLG_ERR;
-  return sgemm((const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr,
-               (float *)b[3].ptr, M, OUT, IN, true, st, k);
+  if ((uint64_t)M * OUT > 0xffffffffull) return nlg_fail("linear: M*OUT exceeds 2^32");
+  return mm((const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (float *)b[3].ptr, M,
+            OUT, IN, true, MM_SERIAL, LIM_INDEX, nlg_domain((uint64_t)M * OUT, groups), st, k);
 }

@@ -523,24 +523,37 @@ extern "C" int nlg_ternary_linear(const float *x, const uint32_t *w2, const floa
 
 // "ternary-i8" by name (an extension with no reference counterpart: the
 // composite the reference expresses as pack-act-rows + bitlinear-dp4a-1f on
-// unpacked weights).  AP WP BIAS BETA GAMMA Y; push (seq out cols).
+// unpacked weights).  AP WP BIAS BETA GAMMA Y; push (seq out cols).  One
+// invocation per output, idx = s*out + o < min(seq*out, 64*groups): a partial
+// grid is the whole rows s < n/out, then the first n%out outputs of row n/out.
 int L_ternary_i8(const nlg_buffer *b, const uint32_t *p, uint32_t groups, hipStream_t st) {
   const uint32_t seq = p[0], out = p[1], cols = p[2];
   const uint32_t ng = (cols + 3) / 4, wng = (cols + 15) / 16;
-  const uint64_t n = nlg_domain((uint64_t)seq * out, groups);
-  if (n != (uint64_t)seq * out)
-    return nlg_fail("ternary-i8: groups must cover seq*out (partial grids unsupported)");
   const char *k = "ternary-i8";
   if (nlg_need(b, 0, (uint64_t)seq * ng, k) || nlg_need(b, 1, (uint64_t)out * wng, k) ||
       nlg_need(b, 2, out, k) || nlg_need(b, 3, 1, k) || nlg_need(b, 4, seq, k) ||
       nlg_need(b, 5, (uint64_t)seq * out, k))
     return NLG_ERR;
-  TernArgs a{(const uint32_t *)b[0].ptr, (const float *)b[4].ptr, (const uint32_t *)b[1].ptr,
-             (const float *)b[2].ptr, (const float *)b[3].ptr, (float *)b[5].ptr, seq, out, cols,
-             ng, wng, 0};
+  if (!seq || !out) return NLG_OK;
+  const uint64_t n = nlg_domain((uint64_t)seq * out, groups);
+  const uint32_t full = (uint32_t)(n / out), part = (uint32_t)(n % out);
+  const uint32_t *xq = (const uint32_t *)b[0].ptr;
+  const float *gamma = (const float *)b[4].ptr;
+  float *y = (float *)b[5].ptr;
   int rpw, wpb;
-  tern_default_geometry(out, seq, &rpw, &wpb);
-  return tern_launch(a, rpw, wpb, st);
+  if (full) {
+    TernArgs a{xq, gamma, (const uint32_t *)b[1].ptr, (const float *)b[2].ptr, (const float *)b[3].ptr, y, full,
+               out, cols, ng, wng, 0};
+    tern_default_geometry(out, full, &rpw, &wpb);
+    if (tern_launch(a, rpw, wpb, st)) return NLG_ERR;
+  }
+  if (part) {  // row `full`, outputs 0..part-1
+    TernArgs a{xq + (size_t)full * ng, gamma + full, (const uint32_t *)b[1].ptr, (const float *)b[2].ptr,
+               (const float *)b[3].ptr, y + (size_t)full * out, 1, part, cols, ng, wng, 0};
+    tern_default_geometry(part, 1, &rpw, &wpb);
+    if (tern_launch(a, rpw, wpb, st)) return NLG_ERR;
+  }
+  return NLG_OK;
 }
 
 // ------------------------------------------------------ int8-lane linears

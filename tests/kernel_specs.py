@@ -150,16 +150,29 @@ def cases(seed: int = 1234) -> list[Case]:
     for nm, nbeta in (("bitlinear-packed", 1), ("bitlinear-packed-v", out)):
         cs.append(Case(nm, [_f(rng, seq * inn), wpk, _f(rng, out), np.abs(_f(rng, nbeta)) * 0.1,
                             _z(seq * out)], [seq, inn, out, pk, fcount], g64(seq * out), 1e-5))
-    for (M, K, N) in ((20, 24, 12), (64, 80, 72)):
+    # The f32 GEMMs sum in the reference's order (serial k; matmul-tiled's
+    # right-nested 16-term tile sums), so they are bit-exact.  K = 300 and
+    # 520 cross the device's 256-deep LDS stages; the 256^3 case is config 1.
+    # Fewer groups than the domain needs: only the covered outputs change.
+    for (M, K, N) in ((20, 24, 12), (64, 80, 72), (36, 300, 20), (256, 256, 256), (16, 520, 32)):
         A, Bm = _f(rng, M * K), _f(rng, K * N)
-        cs.append(Case("matmul", [A, Bm, _z(M * N)], [M, K, N], g64(M * N), 1e-5, label=f"{M}x{K}x{N}"))
-        cs.append(Case("matmul-tiled", [A, Bm, _z(M * N)], [M, K, N], ((M + 15) // 16) * ((N + 15) // 16),
-                       1e-5, label=f"{M}x{K}x{N}"))
-        cs.append(Case("matmul-reg", [A, Bm, _z(M * N)], [M, K, N], g64(((M + 3) // 4) * ((N + 3) // 4)),
-                       1e-5, label=f"{M}x{K}x{N}"))
-    M, IN, OUT = 20, 12, 16
-    cs.append(Case("linear", [_f(rng, M * IN), _f(rng, OUT * IN), _f(rng, OUT), _z(M * OUT)], [M, IN, OUT],
-                   g64(M * OUT), 1e-5))
+        C0 = _f(rng, M * N)
+        lab = f"{M}x{K}x{N}"
+        cs.append(Case("matmul", [A, Bm, _z(M * N)], [M, K, N], g64(M * N), label=lab))
+        cs.append(Case("matmul", [A, Bm, C0], [M, K, N], max(1, g64(M * N) // 3), label=lab + "/partial"))
+        tiles = ((M + 15) // 16) * ((N + 15) // 16)
+        cs.append(Case("matmul-tiled", [A, Bm, _z(M * N)], [M, K, N], tiles, label=lab))
+        cs.append(Case("matmul-tiled", [A, Bm, C0], [M, K, N], max(1, tiles - 2), label=lab + "/partial"))
+        if M % 4 == 0 and N % 4 == 0:
+            blocks = (M // 4) * (N // 4)
+            cs.append(Case("matmul-reg", [A, Bm, _z(M * N)], [M, K, N], g64(blocks), label=lab))
+            if blocks > 64:
+                cs.append(Case("matmul-reg", [A, Bm, C0], [M, K, N], g64(blocks) - 1, label=lab + "/partial"))
+    for (M, IN, OUT) in ((20, 12, 16), (9, 300, 70)):
+        X, W, Bv = _f(rng, M * IN), _f(rng, OUT * IN), _f(rng, OUT)
+        cs.append(Case("linear", [X, W, Bv, _z(M * OUT)], [M, IN, OUT], g64(M * OUT), label=f"{M}x{IN}x{OUT}"))
+        cs.append(Case("linear", [X, W, Bv, _f(rng, M * OUT)], [M, IN, OUT], max(1, g64(M * OUT) // 2),
+                       label=f"{M}x{IN}x{OUT}/partial"))
     seq, dim, heads, kvh = 9, 64, 4, 2
     cs.append(Case("attn-scores", [_f(rng, seq * dim), _f(rng, seq * kvh * 16), _z(heads * seq * seq)],
                    [seq, dim, heads, kvh], g64(heads * seq * seq)))

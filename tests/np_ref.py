@@ -190,12 +190,24 @@ def ref(case):
         be = b[3][:out] if nm.endswith("-v") else np.full(out, b[3][0])
         x = b[0].reshape(seq, inn).astype(np.float64)
         return {4: (b[2][None, :] + (x @ tern.T) * be[None, :]).ravel()}
-    if nm in ("matmul", "matmul-tiled", "matmul-reg"):
-        M, K, N = p
-        return {2: (b[0].reshape(M, K).astype(np.float64) @ b[1].reshape(K, N)).ravel()}
-    if nm == "linear":
-        M, IN, OUT = p
-        return {3: (b[0].reshape(M, IN).astype(np.float64) @ b[1].reshape(OUT, IN).T + b[2]).ravel()}
+    if nm in ("matmul", "matmul-tiled", "matmul-reg", "linear"):
+        if nm == "linear":
+            M, IN, N = p
+            full = b[0].reshape(M, IN).astype(np.float64) @ b[1].reshape(N, IN).T + b[2]
+            cidx = 3
+        else:
+            M, K, N = p
+            full = b[0].reshape(M, K).astype(np.float64) @ b[1].reshape(K, N)
+            cidx = 2
+        # a partial grid writes only the outputs of the invocations it runs
+        r, c = np.meshgrid(np.arange(M), np.arange(N), indexing="ij")
+        if nm == "matmul-tiled":
+            covered = (r // 16) * ((N + 15) // 16) + c // 16 < case.groups  # workgroup = tile
+        elif nm == "matmul-reg":
+            covered = (r // 4) * ((N + 3) // 4) + c // 4 < 64 * case.groups  # invocation = 4x4 block
+        else:
+            covered = r * N + c < 64 * case.groups  # invocation = output
+        return {cidx: np.where(covered, full, b[cidx].reshape(M, N).astype(np.float64)).ravel()}
     if nm == "attn-scores":
         seq, dim, heads, kvh = p
         hd = dim // heads

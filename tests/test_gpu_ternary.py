@@ -81,6 +81,26 @@ def test_named_ternary_i8_matches_typed_entry():
     assert np.array_equal(dy.download(np.float32, seq * out).view(np.uint32), y_ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("groups", [1, 7, 15])
+def test_named_ternary_i8_partial_grid(groups):
+    """groups*64 < seq*out: invocations idx = s*out + o < 64*groups write
+    their outputs, the rest of Y keeps its contents (whole rows, then part of
+    the next row)."""
+    seq, out, cols = 4, 300, 1024
+    t, w2, x, bias, beta = make(6, seq, out, cols)
+    xq, g = orc.pack_act_rows(x, seq, cols)
+    y_ref = orc.ternary_linear_i8(xq, g, w2, bias, beta, seq, out, cols)
+    y0 = np.full(seq * out, -3.5, np.float32)
+    dy = nlgpu.to_device(y0)
+    bufs = [nlgpu.to_device(xq), nlgpu.to_device(w2), nlgpu.to_device(bias), nlgpu.to_device(beta),
+            nlgpu.to_device(g), dy]
+    nlgpu.dispatch("ternary-i8", bufs, [seq, out, cols], groups)
+    n = min(seq * out, 64 * groups)
+    got = dy.download(np.float32, seq * out)
+    assert np.array_equal(got[:n].view(np.uint32), y_ref[:n].view(np.uint32))
+    assert np.all(got[n:] == -3.5)
+
+
 def test_int32_accumulator_extremes():
     # every weight -2 (code 10) against x = +-127 lanes: the largest partial sums
     seq, out, cols = 2, 64, 8192
