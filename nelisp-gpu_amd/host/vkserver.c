@@ -38,6 +38,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "nlg_deferred.h"
 #include "nlg_host.h"
 
 #define OP_RUN 0
@@ -183,12 +184,7 @@ static int res_slot(void) {
 static int res_valid(uint32_t h) { return h < (uint32_t)g_nres && g_res[h].used; }
 
 /* pointers freed by the client while a compiled batch still binds them */
-typedef struct {
-  void *p;
-  int live;
-} Deferred;
-static Deferred g_deferred[MAXRES];
-static int g_ndeferred = 0;
+static nlg_deferred g_deferred;
 
 /* -------------------------------------------------------------- batches */
 
@@ -282,6 +278,8 @@ typedef struct {
 } Comp;
 static Comp g_comp[MAXCOMP];
 
+static void free_device(void *p) { nlg_free(p); }
+
 static int comp_binds(const void *p) {
   for (int c = 0; c < MAXCOMP; c++)
     if (g_comp[c].used)
@@ -300,12 +298,7 @@ static void comp_release(Comp *C) {
   batch_free(&C->b);
   memset(C, 0, sizeof *C);
   /* deferred frees no batch binds any more */
-  for (int i = 0; i < g_ndeferred; i++)
-    if (g_deferred[i].live && !comp_binds(g_deferred[i].p)) {
-      nlg_free(g_deferred[i].p);
-      g_deferred[i].live = 0;
-    }
-  while (g_ndeferred && !g_deferred[g_ndeferred - 1].live) g_ndeferred--;
+  nlg_deferred_sweep(&g_deferred, comp_binds, free_device);
 }
 
 /* Zero this batch's tmp/out slots then run its dispatches. */
@@ -411,12 +404,11 @@ static void release_resident(uint32_t h) {
   void *p = g_res[h].p;
   g_res[h].used = 0;
   g_res[h].p = NULL;
-  if (comp_binds(p) && g_ndeferred < MAXRES) {
-    g_deferred[g_ndeferred].p = p;
-    g_deferred[g_ndeferred].live = 1;
-    g_ndeferred++;
-  } else {
+  if (!comp_binds(p)) {
     nlg_free(p);
+  } else if (nlg_deferred_add(&g_deferred, p)) {
+    /* out of host memory: leak the buffer rather than free one a graph binds */
+    fprintf(stderr, "vkserver: cannot park a bound resident; it stays allocated\n");
   }
 }
 
