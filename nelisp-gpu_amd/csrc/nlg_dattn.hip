@@ -48,6 +48,9 @@ struct AttnArgs {
   // [0, trows) as zero rotations
   const int32_t *ent;
   uint32_t nslots, trows;
+  // one query head per workgroup (G == 1): units (row, kv head, chunk) on a
+  // 1-D grid, the grp workgroups of a unit on one XCD (see attn_unit)
+  uint32_t nunits;
 };
 
 // how k_attn_part finds position p's K/V row; AM_NT added to a mode: K and V
@@ -130,7 +133,22 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
                "s"(a.kvheads), "s"(a.max_seq), "s"(a.nchunk), "s"(a.coef));
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   // workgroup: chunk c, query heads h0 .. h0+G-1 (all of one kv head), query row qr
-  const uint32_t c = blockIdx.x, h0 = blockIdx.y * G, qr = blockIdx.z, kvh = h0 / a.grp;
+  uint32_t c, h0, qr;
+  if (G == 1) {
+    // Workgroups are dealt to the 8 XCDs round-robin by id, and each XCD
+    // has its own L2: the grp query heads of one (row, kv head, chunk) unit
+    // get ids u%8 + 8(q + grp*(u/8)), all on XCD u%8, so the unit's K/V rows
+    // come from HBM once and from that L2 for the other heads.
+    const uint32_t id = blockIdx.x, rest = id >> 3, q = rest % a.grp, u = (id & 7u) + 8u * (rest / a.grp);
+    if (u >= a.nunits) return;
+    c = u % a.nchunk;
+    const uint32_t r2 = u / a.nchunk;
+    h0 = (r2 % a.kvheads) * a.grp + q;
+    qr = r2 / a.kvheads;
+  } else {
+    c = blockIdx.x; h0 = blockIdx.y * G; qr = blockIdx.z;
+  }
+  const uint32_t kvh = h0 / a.grp;
   const uint32_t b = a.qper ? qr / a.qper : qr;                         // its sequence
   const size_t cb = (size_t)qr * a.nchunk + c;
   float *pctx = a.pctx + cb * a.heads * HD + (size_t)h0 * HD;
@@ -459,7 +477,9 @@ static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, int
   const uint64_t seqs = a.qper ? (rows + a.qper - 1) / a.qper : rows;
   if (mode != AM_ENTRIES && seqs * a.kvheads * a.max_seq * head_dim * 4 >= ATTN_NT_BYTES) mode |= AM_NT;
   constexpr int AM_CONTIG_NT_ = AM_CONTIG | AM_NT;
-  const dim3 grid(a.nchunk, a.heads / G, rows), blk(ATTN_WAVES * 64);
+  a.nunits = rows * a.kvheads * a.nchunk;
+  const dim3 grid = G == 1 ? dim3((a.nunits + 7) / 8 * 8 * a.grp) : dim3(a.nchunk, a.heads / G, rows);
+  const dim3 blk(ATTN_WAVES * 64);
 #define AT1(HD, GG, PGV)                                                                   \
   do {                                                                                     \
     if (ni == 8) hipLaunchKernelGGL((k_attn_part<HD, GG, 8, PGV>), grid, blk, 0, st, a);   \
