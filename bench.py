@@ -225,29 +225,13 @@ def _per_launch_us(fn, n, stream):
     return us
 
 
-def decode_bench(batch: int, stream):
-    """Config 5: prefill 512 random ids (teacher-forced token steps), then 256
-    greedy steps, one captured graph per step; then each kernel of a step
-    timed on its own over the 30 layers' weights."""
+def _decode_kernels(s, batch, stream):
+    """The five kernels of one decoder layer at the last cache position
+    (767), each a function of the launch index i that rotates over the 30
+    layers' weights, with its algorithmic bytes per launch."""
     import nlgpu
     c = STACK
     max_seq = PROMPT + DECODE
-    s = nlgpu.Stack(**c, max_seq=max_seq, batch=batch, seed=20260921 + 5)
-    ids = (nlgpu.uniform(20260921 + 55, batch * PROMPT) * c["vocab"]).astype(np.int32).reshape(batch, PROMPT)
-    e0, e1, e2 = nlgpu.Event(), nlgpu.Event(), nlgpu.Event()
-    s.prefill(ids)  # warm: allocates the prefill rows and scratch
-    e0.record(stream)
-    s.prefill(ids)  # all 512 prompt tokens at once, then the first greedy token
-    e1.record(stream)
-    prefill_ms = e0.elapsed_ms(e1)
-    s.step(1)  # first decode step: captures the step graph
-    e1.record(stream)
-    s.step(DECODE - 1)
-    e2.record(stream)
-    decode_ms = e1.elapsed_ms(e2) * DECODE / (DECODE - 1)
-    toks, _ = s.tokens()
-    assert (toks[:, :max_seq] >= 0).all()
-    # per-kernel, at the last position (768 cached), rotating over the layers
     L, d, f = c["layers"], c["d_model"], c["d_ff"]
     nq, nkv = c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"]
     T = lambda n, l=-1: _tensor(s, n, l)
@@ -279,6 +263,36 @@ def decode_bench(batch: int, stream):
             h, ly[i % L]["wd"], None, ly[i % L]["bd"], x, x, batch, d, f, stream=stream),
             d * f // 4 + batch * (f * 4 + d * 8)),
     }
+    return kern, L
+
+
+def decode_bench(batch: int, stream):
+    """Config 5: prefill 512 random ids (teacher-forced token steps), then 256
+    greedy steps, one captured graph per step; then each kernel of a step
+    timed on its own over the 30 layers' weights."""
+    import nlgpu
+    c = STACK
+    max_seq = PROMPT + DECODE
+    s = nlgpu.Stack(**c, max_seq=max_seq, batch=batch, seed=20260921 + 5)
+    ids = (nlgpu.uniform(20260921 + 55, batch * PROMPT) * c["vocab"]).astype(np.int32).reshape(batch, PROMPT)
+    e0, e1, e2 = nlgpu.Event(), nlgpu.Event(), nlgpu.Event()
+    s.prefill(ids)  # warm: allocates the prefill rows and scratch
+    e0.record(stream)
+    s.prefill(ids)  # all 512 prompt tokens at once, then the first greedy token
+    e1.record(stream)
+    prefill_ms = e0.elapsed_ms(e1)
+    s.step(1)  # first decode step: captures the step graph
+    e1.record(stream)
+    s.step(DECODE - 1)
+    e2.record(stream)
+    decode_ms = e1.elapsed_ms(e2) * DECODE / (DECODE - 1)
+    toks, _ = s.tokens()
+    assert (toks[:, :max_seq] >= 0).all()
+    # per-kernel, at the last position (768 cached), rotating over the layers
+    kern, L = _decode_kernels(s, batch, stream)
+    n = 4 * L
+    d, f = c["d_model"], c["d_ff"]
+    nq, nkv = c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"]
     per = {}
     for name, (fn, nbytes) in kern.items():
         us = _per_launch_us(fn, n, stream)
@@ -697,9 +711,13 @@ def cpu_baseline(x, w_one, seconds: float):
 
 
 def pmc_probe():
-    """Launches for rocprofv3 --pmc runs: 64 config-2 steps (eager, one
-    dispatch each, rotating weight copies) and 4 device-to-device copies of
-    64 MiB, whose FETCH_SIZE / WRITE_SIZE calibrate the counters' scale."""
+    """Eager launches for rocprofv3 --pmc and --kernel-trace runs, in this
+    order: 64 config-2 steps (rotating weight copies), 4 launches of the
+    same GEMV kernel over all 128 copies stacked (long dispatches that
+    calibrate GRBM_GUI_ACTIVE's clock), 4 device-to-device copies of 64 MiB
+    (calibrating FETCH_SIZE / WRITE_SIZE), then the five decoder-layer
+    kernels at batch 1 and at batch 32 (30 launches each, one per layer, at
+    cache position 767) and one full-size config-3 softmax."""
     import nlgpu
     nlgpu.init()
     seed = 20260921 + 1
@@ -716,11 +734,34 @@ def pmc_probe():
         L.nlg_ternary_linear_cfg(dx.ptr, dW.ptr + (i % COPIES) * wbytes, None, dbeta.ptr, 0, dy.ptr, None, 1,
                                  OUT, COLS, 0, None, 0, None)
     nlgpu.sync()
+    dxq, dg, dY = nlgpu.DeviceArray(COLS), nlgpu.DeviceArray(4), nlgpu.DeviceArray(OUT * COPIES * 4)
+    L.nlg_pack_act_rows(dx.ptr, dxq.ptr, dg.ptr, 1, COLS, None)
+    for _ in range(4):
+        L.nlg_ternary_linear_i8_cfg(dxq.ptr, dg.ptr, dW.ptr, None, dbeta.ptr, 0, dY.ptr, 1, OUT * COPIES, COLS, 4, 4,
+                                    None)
+    nlgpu.sync()
     a, b = nlgpu.DeviceArray(64 << 20), nlgpu.DeviceArray(64 << 20)
     for _ in range(4):
         L.nlg_copy_d2d(b.ptr, a.ptr, 64 << 20, None)
     nlgpu.sync()
-    print("pmc probe: 64 steps of k_tern_fused (4096x4096), 4 copies of 64 MiB", flush=True)
+    print("pmc probe: 64 config-2 steps, 4 stacked GEMVs, 4 copies of 64 MiB", flush=True)
+    del dW, dY, a, b
+    stream = L.nlg_default_stream()
+    for batch in (1, 32):
+        st = nlgpu.Stack(**STACK, max_seq=PROMPT + DECODE, batch=batch, seed=20260921 + 5)
+        kern, nl = _decode_kernels(st, batch, stream)
+        for name, (fn, _) in kern.items():
+            for i in range(nl):
+                fn(i)
+            nlgpu.sync()
+        st.close()
+        print(f"pmc probe: decoder-layer kernels at batch {batch}, {nl} launches each", flush=True)
+    n = SM_HEADS * SM_N * SM_N
+    sm = nlgpu.DeviceArray(n * 4)
+    nlgpu.fill_normal(sm, n, 20260921 + 3, 3.0, SM_N)
+    nlgpu.softmax_rows(sm, sm, SM_HEADS * SM_N, SM_N)
+    nlgpu.sync()
+    print("pmc probe: one config-3 softmax", flush=True)
 
 
 def profile_eager(stack=True):

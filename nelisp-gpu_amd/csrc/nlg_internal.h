@@ -271,6 +271,10 @@ uint32_t nlg_argmax_parts(uint32_t seq, uint32_t cols, uint32_t out);
 // Grow-only device scratch owned by the library, one per stream (NULL on
 // failure).  It cannot grow while `st` is being captured into a graph.
 void *nlg_scratch(size_t bytes, hipStream_t st);
+// The same for another purpose (slot 1: zero-filled when allocated); NULL,
+// with no error set, when it would have to grow inside a graph capture or
+// cannot be allocated.
+void *nlg_scratch_try(size_t bytes, hipStream_t st, int slot);
 // The active device's fixed scratch array (NLG_NOALLOC_SCRATCH_BYTES), or
 // null with the error set.
 void *nlg_noalloc_scratch(void);

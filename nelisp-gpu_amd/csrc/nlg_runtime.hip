@@ -97,30 +97,42 @@ struct StreamScratch {
   std::vector<void *> bufs;
   size_t bytes = 0;
 };
-static std::map<hipStream_t, StreamScratch> g_scratch;
+static std::map<std::pair<hipStream_t, int>, StreamScratch> g_scratch;
 static std::mutex g_scratch_mu;
 
-void *nlg_scratch(size_t bytes, hipStream_t st) {
+// Slot 0: the batched linears' int8 activations.  Slot 1: the column-split
+// GEMM's partial sums and arrival counters, zero-filled when allocated (the
+// GEMM leaves its counters at zero).
+static void *scratch_get(size_t bytes, hipStream_t st, int slot, bool quiet) {
   std::lock_guard<std::mutex> lk(g_scratch_mu);
-  StreamScratch &e = g_scratch[st];
+  StreamScratch &e = g_scratch[{st, slot}];
   if (bytes <= e.bytes) return e.bufs.back();
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
-    nlg_fail("batched linear: its %zu-byte scratch must be reserved on this stream before graph capture "
-             "(run the call once on it outside the capture first)", bytes);
+    if (!quiet)
+      nlg_fail("batched linear: its %zu-byte scratch must be reserved on this stream before graph capture "
+               "(run the call once on it outside the capture first)", bytes);
     return nullptr;
   }
   size_t want = e.bytes ? e.bytes : (1u << 20);
   while (want < bytes) want *= 2;
   void *p = nullptr;
   if (hipMalloc(&p, want) != hipSuccess) {
-    nlg_fail("scratch: hipMalloc(%zu) failed", want);
+    if (!quiet) nlg_fail("scratch: hipMalloc(%zu) failed", want);
+    return nullptr;
+  }
+  if (slot == 1 && hipMemsetAsync(p, 0, want, st) != hipSuccess) {
+    (void)hipFree(p);
+    if (!quiet) nlg_fail("scratch: zero fill failed");
     return nullptr;
   }
   e.bufs.push_back(p);
   e.bytes = want;
   return p;
 }
+
+void *nlg_scratch(size_t bytes, hipStream_t st) { return scratch_get(bytes, st, 0, false); }
+void *nlg_scratch_try(size_t bytes, hipStream_t st, int slot) { return scratch_get(bytes, st, slot, true); }
 
 extern "C" int nlg_shutdown(void) {
   if (!g_inited) return NLG_OK;

@@ -190,6 +190,14 @@ struct GemmArgs {
   float *pval;
   int32_t *pidx;
   uint32_t nparts;
+  // k_tgemm_l split over the columns: gridDim.z slices of the chunks, each
+  // slice's int32 accumulators to ksum (one block of registers per
+  // (slice, tile, thread)), tile arrivals counted in kctr (zero between
+  // launches); the last slice of a tile to arrive adds the others' and
+  // runs the epilogue
+  int32_t *ksum;
+  uint32_t *kctr;
+  bool allow_split;  // the launcher may take split workspace from the library
 };
 
 // One output element of the batched linear (every lane calls it: the SwiGLU
@@ -574,7 +582,7 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
 
 #define TL_PITCH (TG_KC + 16)   // LDS row pitch (bytes) of the activation stage
 
-template <int NB, int WR, int EPI>
+template <int NB, int WR, int EPI, bool SPLIT = false>
 __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   typedef int v16i __attribute__((ext_vector_type(16)));
   typedef uint32_t wvec __attribute__((ext_vector_type(8 * NB)));
@@ -588,7 +596,9 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   const int li = lane & 31, lg = lane >> 5;
   const uint32_t rbase = blockIdx.x * (32 * NB * WR) + wn * (32 * NB);
   const uint32_t tok0 = blockIdx.y * 128;
-  const uint32_t nchunks = a.cols / TG_KC;
+  // this slice's chunks: [cfirst, nchunks)
+  const uint32_t ntot = a.cols / TG_KC, ks = SPLIT ? gridDim.z : 1;
+  const uint32_t cfirst = SPLIT ? blockIdx.z * ntot / ks : 0, nchunks = SPLIT ? (blockIdx.z + 1) * ntot / ks : ntot;
   // weight rows of this lane: rbase + 32 nt + li (clamped; dead rows masked at the store)
   uint32_t rw[NB], rc[NB];
   const uint4 *wp[NB];
@@ -633,9 +643,9 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   // on the loads still in flight); activations run one chunk ahead.
   wvec wA, wB, wC;
   avec aX;
-  const uint32_t c1 = nchunks > 1 ? 1 : 0;
-  TL_LOADW(0, wA);
-  TL_LOADA(0, aX);
+  const uint32_t c1 = nchunks > cfirst + 1 ? cfirst + 1 : cfirst;
+  TL_LOADW(cfirst, wA);
+  TL_LOADA(cfirst, aX);
   TL_LOADW(c1, wB);
   float bo[NB], be[NB];
 #pragma unroll
@@ -643,7 +653,7 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
     bo[nt] = a.bias ? a.bias[rc[nt]] : 0.0f;
     be[nt] = a.beta[a.beta_per_row ? rc[nt] : 0];
   }
-  TL_STOREA(0, aX);
+  TL_STOREA(cfirst & 1, aX);
   v16i acc[2][NB];  // [token block][row block]
 #pragma unroll
   for (int mt = 0; mt < 2; mt++)
@@ -680,7 +690,7 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   }
   // whole groups of three chunks without branches (a conditional step would
   // merge register sets at its join and copy them), then the last one or two
-  uint32_t c0 = 0;
+  uint32_t c0 = cfirst;
   for (; c0 + 3 <= nchunks; c0 += 3) {
     TL_STEP(0, wA, wC)
     TL_STEP(1, wB, wA)
@@ -693,6 +703,51 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
 #undef TL_LOADW
 #undef TL_LOADA
 #undef TL_STOREA
+  if (SPLIT) {
+    // Column slices meet here.  Every slice leaves its accumulators in its
+    // own block of ksum with agent-coherent (write-through) stores, waits
+    // for them to complete, and counts itself in; the last to arrive reads
+    // the other slices' blocks (agent-coherent loads, past any stale L2
+    // copy), adds them -- integer sums, the same in any order -- and goes
+    // on to the epilogue.  It also re-zeros the tile's counter for the next
+    // launch, which the stream orders after this one.
+    constexpr int NR = 2 * NB * 16;  // accumulators per thread
+    const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x, ntile = gridDim.x * gridDim.y;
+    const size_t nthr = blockDim.x;
+    // register j of every thread side by side: each store and load of a
+    // wave covers 256 contiguous bytes
+    int32_t *mine = a.ksum + ((size_t)blockIdx.z * ntile + tile) * NR * nthr + threadIdx.x;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+      for (int nt = 0; nt < NB; nt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          __hip_atomic_store(mine + ((mt * NB + nt) * 16 + r) * nthr, acc[mt][nt][r], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ uint32_t s_last;
+    if (threadIdx.x == 0) {
+      const uint32_t n = __hip_atomic_fetch_add(a.kctr + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = n + 1 == ks;
+      if (n + 1 == ks) __hip_atomic_store(a.kctr + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    for (uint32_t z = 0; z < ks; z++) {
+      if (z == blockIdx.z) continue;
+      const int32_t *other = a.ksum + ((size_t)z * ntile + tile) * NR * nthr + threadIdx.x;
+#pragma unroll
+      for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NB; nt++)
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            acc[mt][nt][r] += __hip_atomic_load(other + ((mt * NB + nt) * 16 + r) * nthr, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
   // epilogue: acc[mt][nt] register r is token tok0 + 64 wm + 32 mt + (r%4) + 8 (r/4) + 4 lg,
   // row rbase + 32 nt + li
   if (EPI == NLG_EPI_SWIGLU) {
@@ -781,12 +836,39 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
     const int tile = (uint64_t)nlg_blocks(a.out, 256) * ty >= 256   ? 256
                      : (uint64_t)nlg_blocks(a.out, 128) * ty >= 256 ? 128
                                                                     : 64;
-    const dim3 grid(nlg_blocks(a.out, tile), ty), blk(tile == 256 ? 512 : 256);
+    // Too few 64-row tiles to fill the CUs (e.g. 2560 rows x 512 tokens):
+    // split the columns into slices of at least 4 chunks, about 384
+    // workgroups in all, when the per-stream split workspace is to be had
+    // (measured: down projection 2560 x 6912 at 512 tokens 29.5 -> 24.5 us
+    // with 3 slices, at 128 tokens 25 -> 15 us with 6; 216 tiles gain
+    // nothing from 2)
+    const uint32_t ntile = nlg_blocks(a.out, tile) * ty, nch = a.cols / TG_KC;
+    uint32_t ks = 1;
+    if (a.allow_split && tile == 64 && ntile < 192 && nch >= 8) {
+      ks = (384 + ntile - 1) / ntile;
+      if (ks > nch / 4) ks = nch / 4;
+      if (ks > 8) ks = 8;
+    }
+    if (ks > 1) {
+      const uint32_t nthr = tile == 256 ? 512 : 256, nr = tile == 256 ? 64 : (tile == 128 ? 64 : 32);
+      // the counters' region is the same for every launch (a split grid has
+      // fewer than 256 tiles), so partial sums never land on a counter
+      const size_t ctr_bytes = 256 * 4;
+      uint8_t *w = (uint8_t *)nlg_scratch_try(ctr_bytes + (size_t)ks * ntile * nthr * nr * 4, st, 1);
+      if (w) {
+        a.kctr = (uint32_t *)w;
+        a.ksum = (int32_t *)(w + ctr_bytes);
+      } else {
+        ks = 1;
+      }
+    }
+    const dim3 grid(nlg_blocks(a.out, tile), ty, ks), blk(tile == 256 ? 512 : 256);
     if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
     const size_t lds = (size_t)2 * 128 * TL_PITCH;
 #define TLG(E)                                                                            \
   do {                                                                                    \
-    if (tile == 256) hipLaunchKernelGGL((k_tgemm_l<2, 4, E>), grid, blk, lds, st, a);     \
+    if (ks > 1) hipLaunchKernelGGL((k_tgemm_l<1, 2, E, true>), grid, blk, lds, st, a);    \
+    else if (tile == 256) hipLaunchKernelGGL((k_tgemm_l<2, 4, E>), grid, blk, lds, st, a); \
     else if (tile == 128) hipLaunchKernelGGL((k_tgemm_l<2, 2, E>), grid, blk, lds, st, a); \
     else hipLaunchKernelGGL((k_tgemm_l<1, 2, E>), grid, blk, lds, st, a);                 \
   } while (0)
@@ -911,5 +993,6 @@ int nlg_batched_launch(const FusedArgs &f, int pro, int epi, hipStream_t st) {
   g.rstride = f.rstride; g.nq = f.nq; g.nkv = f.nkv; g.hd = f.hd; g.kvheads = f.kvheads; g.max_seq = f.max_seq;
   g.co = f.co; g.si = f.si; g.pos = f.pos; g.kc = f.kc; g.vc = f.vc; g.qper = f.qper;
   g.pval = f.pval; g.pidx = f.pidx;
+  g.allow_split = !f.act_scratch;  // caller-provided scratch: no library allocation
   return nlg_tgemm_launch(g, epi, st);
 }
