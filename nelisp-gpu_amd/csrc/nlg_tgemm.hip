@@ -575,10 +575,12 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
 // (r % 4) + 8 (r / 4) + 4 (l / 32), column l % 32).  Columns go in chunks
 // of 256 (8 MFMA steps): lane group g at step t covers 2-bit word 8g + t
 // of the chunk, so a lane's weights for a chunk are 8 consecutive words
-// (32 bytes) of its row.  Loads run two chunks ahead of the matrix cores:
-// chunk c+2's weights and activations are fetched while chunk c computes
-// and chunk c+1's wait in registers to go to LDS.  Every decoded B operand
-// feeds two MFMAs.
+// (32 bytes) of its row.  Weights run two chunks ahead of the matrix
+// cores, activations one: chunk c+2's weights and chunk c+1's activations
+// are fetched while chunk c computes.  (Activations two chunks ahead, in
+// three more register sets, measured slower: 16,384-token gate|up 746 ->
+// 760 us, 512 tokens 28.6 -> 33.8 us.)  Every decoded B operand feeds two
+// MFMAs.
 
 #define TL_PITCH (TG_KC + 16)   // LDS row pitch (bytes) of the activation stage
 
@@ -646,6 +648,10 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   const uint32_t c1 = nchunks > cfirst + 1 ? cfirst + 1 : cfirst;
   TL_LOADW(cfirst, wA);
   TL_LOADA(cfirst, aX);
+  // gamma of the workgroup's 128 tokens, for the epilogue (to LDS below,
+  // ordered before the epilogue by the main loop's barriers)
+  __shared__ float s_gm[128];
+  const float gm_t = a.gamma[tok0 + (threadIdx.x & 127u) < a.seq ? tok0 + (threadIdx.x & 127u) : a.seq - 1];
   TL_LOADW(c1, wB);
   float bo[NB], be[NB];
 #pragma unroll
@@ -654,6 +660,7 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
     be[nt] = a.beta[a.beta_per_row ? rc[nt] : 0];
   }
   TL_STOREA(cfirst & 1, aX);
+  if (threadIdx.x < 128) s_gm[threadIdx.x] = gm_t;
   v16i acc[2][NB];  // [token block][row block]
 #pragma unroll
   for (int mt = 0; mt < 2; mt++)
@@ -749,7 +756,12 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
     }
   }
   // epilogue: acc[mt][nt] register r is token tok0 + 64 wm + 32 mt + (r%4) + 8 (r/4) + 4 lg,
-  // row rbase + 32 nt + li
+  // row rbase + 32 nt + li.  gamma comes from LDS; the residual and RoPE
+  // operands of a (token block, row block) are all fetched before its first
+  // result is stored.  (y may be the residual itself, so the compiler keeps
+  // every load behind the stores before it: fetched beside its own store,
+  // each operand cost a memory round trip.  Measured at 16,384 tokens: the
+  // gate|up GEMM 813 -> 746 us, its STORE form 881 -> 712 us.)
   if (EPI == NLG_EPI_SWIGLU) {
     // Gate row 2j and up row 2j+1 sit in lanes l, l^1.  Each lane of a pair
     // finishes half of the pair's tokens: the even lane registers 0..7, the
@@ -765,8 +777,7 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
         for (int k = 0; k < 8; k++) {
           const uint32_t tlo = tok0 + 64 * wm + 32 * mt + (k % 4) + 8 * (k / 4) + 4 * lg;
           const uint32_t thi = tlo + 16;  // register k + 8
-          const float glo = a.gamma[tlo < a.seq ? tlo : a.seq - 1];
-          const float ghi = a.gamma[thi < a.seq ? thi : a.seq - 1];
+          const float glo = s_gm[tlo - tok0], ghi = s_gm[thi - tok0];
           // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
           const float vlo = __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], glo), (float)(q[k] >> 6)));
           const float vhi = __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], ghi), (float)(q[k + 8] >> 6)));
@@ -786,15 +797,18 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
 #pragma unroll
   for (int mt = 0; mt < 2; mt++) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const uint32_t tk = tok0 + 64 * wm + 32 * mt + (r % 4) + 8 * (r / 4) + 4 * lg;
-      const uint32_t tkc = tk < a.seq ? tk : a.seq - 1;
-      const float gm = a.gamma[tkc];
+    for (int nt = 0; nt < NB; nt++) {
+      TgPre pre[16];
 #pragma unroll
-      for (int nt = 0; nt < NB; nt++) {
+      for (int r = 0; r < 16; r++)
+        pre[r] = tg_prefetch<EPI>(a, rc[nt], tok0 + 64 * wm + 32 * mt + (r % 4) + 8 * (r / 4) + 4 * lg);
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const uint32_t tk = tok0 + 64 * wm + 32 * mt + (r % 4) + 8 * (r / 4) + 4 * lg;
         // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
-        const float v = __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], gm), (float)(acc[mt][nt][r] >> 6)));
-        tg_store<EPI>(a, lane, rw[nt], tk, rw[nt] < a.out && tk < a.seq, v);
+        const float v =
+            __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], s_gm[tk - tok0]), (float)(acc[mt][nt][r] >> 6)));
+        tg_store_pre<EPI>(a, lane, rw[nt], tk, rw[nt] < a.out && tk < a.seq, v, pre[r]);
       }
     }
   }
