@@ -46,7 +46,7 @@ COPIES = 128
 STEP_BYTES = OUT * COLS // 4 + COLS * 4 + 4 + OUT * 4          # 4,227,076
 GEMV_BYTES = OUT * COLS // 4 + COLS + 4 + 4 + OUT * 4          # 4,214,792
 # HBM bytes per step measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-STEP_TRAFFIC = 4520462 + 16384
+STEP_TRAFFIC = 4511247 + 16384
 METRIC = "ternary GEMV GB/s (% HBM peak) at 4096²; decode tok/s, 2B ternary model, batch 1"
 
 
