@@ -19,7 +19,9 @@
 // the order the score layout gives them; V^T is read from a transposed LDS
 // copy in the same order).  Q and P enter the f16 matrix cores as hi + lo
 // halves (x = hi + lo exactly to 22 bits), so the products carry f32-grade
-// precision; K and V are fp16 already.
+// precision; K and V are fp16 already.  Scores are kept in base 2 (log2 e
+// folded into the 1/sqrt(hd) scale), so every exponential is one v_exp_f32
+// instead of a correctly rounded expf.
 
 #include "nlg_internal.h"
 
@@ -36,15 +38,22 @@ struct PrefillArgs {
   const int32_t *pos;
   float *ctx;
   uint32_t qper, heads, kvheads, max_seq, nq;
-  float coef;  // 1/sqrt(head_dim)
+  float coef;  // log2(e)/sqrt(head_dim): scores in base 2
+  // key-range split (SPLIT kernels): workgroup x = query block x / maxp,
+  // piece x % maxp of kps key blocks; each piece leaves its unnormalised
+  // context [piece][row][nq] and (max, sum) [piece][row][heads][2] for
+  // k_prefill_merge
+  float *part_o, *part_ml;
+  uint32_t kps, maxp;
 };
 
 #define PA_KB 32  // keys per block
 #define PA_QB 32  // query positions per workgroup
+#define PA_KPS 4  // key blocks per piece of a split launch
 
 __device__ __forceinline__ v8h f16x8(uint4 u) { return __builtin_bit_cast(v8h, u); }
 
-template <int HD, int GRP>
+template <int HD, int GRP, bool SPLIT>
 __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_attn(PrefillArgs a) {
   constexpr int NT = 64 * GRP;
   constexpr int KP = HD + 8;       // K row pitch in halves (staggers the banks)
@@ -58,16 +67,21 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int li = lane & 31, lg = lane >> 5;
   const uint32_t kvh = blockIdx.y, sq = blockIdx.z, head = kvh * GRP + w;
+  const uint32_t qb = SPLIT ? blockIdx.x / a.maxp : blockIdx.x, piece = SPLIT ? blockIdx.x % a.maxp : 0;
   const int32_t pos0 = a.pos[0];
   // this lane's query: prompt row i (clamped for the tail block)
-  const uint32_t i = blockIdx.x * PA_QB + li;
+  const uint32_t i = qb * PA_QB + li;
   const bool live = i < a.qper;
   const uint32_t ic = live ? i : a.qper - 1;
   const uint32_t row = sq * a.qper + ic;
   const int32_t pj = pos0 + (int32_t)ic;
-  const uint32_t ilast = min(blockIdx.x * PA_QB + PA_QB - 1, a.qper - 1);
+  const uint32_t ilast = min(qb * PA_QB + PA_QB - 1, a.qper - 1);
   const int32_t plast = min(pos0 + (int32_t)ilast, (int32_t)a.max_seq - 1);
-  const uint32_t nkb = plast < 0 ? 0u : (uint32_t)plast / PA_KB + 1;
+  const uint32_t nkb_all = plast < 0 ? 0u : (uint32_t)plast / PA_KB + 1;
+  // this workgroup's key blocks: [kbf, nkb)
+  const uint32_t kbf = SPLIT ? min(piece * a.kps, nkb_all) : 0u;
+  const uint32_t nkb = SPLIT ? min(kbf + a.kps, nkb_all) : nkb_all;
+  if (SPLIT && kbf >= nkb && piece) return;  // past the causal range (piece 0 always reports)
   const size_t cache0 = (size_t)(sq * a.kvheads + kvh) * a.max_seq * HD;
   const uint16_t *kb0 = a.kc + cache0, *vb0 = a.vc + cache0;
   const uint32_t klast = a.max_seq - 1;
@@ -145,11 +159,11 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
 #pragma unroll
   for (int t = 0; t < HD / 32; t++) o[t] = (v16f){};
   float m = -1.0e30f, l = 0.0f;
-  if (nkb) {
-    PA_LOAD(0u);
-    PA_STORE(0);
+  if (nkb > kbf) {
+    PA_LOAD(kbf);
+    PA_STORE(kbf & 1);
   }
-  for (uint32_t kb = 0; kb < nkb; kb++) {
+  for (uint32_t kb = kbf; kb < nkb; kb++) {
     const int buf = kb & 1;
     if (kb + 1 < nkb) PA_LOAD(kb + 1);
     __syncthreads();
@@ -165,16 +179,16 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int32_t key = (int32_t)(kb * PA_KB + 8 * (r / 4) + 4 * lg + r % 4);
-      sc[r] = key <= pj ? sc[r] * a.coef : -INFINITY;
+      sc[r] = key <= pj ? sc[r] * a.coef : -INFINITY;  // (q.k / sqrt(hd)) * log2(e)
       mb = fmaxf(mb, sc[r]);
     }
     mb = fmaxf(mb, __shfl_xor(mb, 32));
     const float mn = fmaxf(m, mb);
-    const float al = expf(m - mn);
+    const float al = nlg_exp2(m - mn);
     float ls = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      sc[r] = expf(sc[r] - mn);
+      sc[r] = nlg_exp2(sc[r] - mn);
       ls += sc[r];
     }
     ls += __shfl_xor(ls, 32);
@@ -207,6 +221,20 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
 #undef PA_LOAD
 #undef PA_STORE
   // O^T tile t, register r: dim 32 t + 8 (r/4) + 4 lg + r%4 of query li
+  if (SPLIT) {
+    if (live) {
+      const size_t pr = (size_t)piece * gridDim.z * a.qper + row;
+      float *po = a.part_o + pr * a.nq + (size_t)head * HD + 4 * lg;
+#pragma unroll
+      for (int t = 0; t < HD / 32; t++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++)
+          *(float4 *)(po + 32 * t + 8 * rq) =
+              make_float4(o[t][4 * rq], o[t][4 * rq + 1], o[t][4 * rq + 2], o[t][4 * rq + 3]);
+      if (lg == 0) *(float2 *)(a.part_ml + (pr * a.heads + head) * 2) = make_float2(m, l);
+    }
+    return;
+  }
   if (live) {
     float *cp = a.ctx + (size_t)row * a.nq + (size_t)head * HD + 4 * lg;
 #pragma unroll
@@ -222,6 +250,46 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
       }
     }
   }
+}
+
+// The pieces of a split prompt attention merged: per (row, head), M = max
+// of the pieces' maxima, L = sum l_p 2^(m_p - M), ctx = sum o_p 2^(m_p - M)
+// / L over the pieces that row's query block has; one thread per 4 dims.
+__global__ __launch_bounds__(256) void k_prefill_merge(PrefillArgs a, uint32_t hd, uint32_t nrows) {
+  const uint32_t per = hd / 4;
+  const uint64_t gid = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (uint64_t)nrows * a.heads * per) return;
+  const uint32_t d4 = (uint32_t)(gid % per);
+  const uint64_t rh = gid / per;
+  const uint32_t head = (uint32_t)(rh % a.heads), row = (uint32_t)(rh / a.heads);
+  // the pieces this row's query block was split into (as k_prefill_attn counts them)
+  const uint32_t qb = (row % a.qper) / PA_QB;
+  const int32_t pos0 = a.pos[0];
+  const uint32_t ilast = min(qb * PA_QB + PA_QB - 1, a.qper - 1);
+  const int32_t plast = min(pos0 + (int32_t)ilast, (int32_t)a.max_seq - 1);
+  const uint32_t nkb_all = plast < 0 ? 0u : (uint32_t)plast / PA_KB + 1;
+  const uint32_t np = nkb_all ? (nkb_all + a.kps - 1) / a.kps : 1;
+  float mm = -1.0e30f;
+  for (uint32_t p = 0; p < np; p++) {
+    const float mp = a.part_ml[(((size_t)p * nrows + row) * a.heads + head) * 2];
+    mm = mp > mm ? mp : mm;
+  }
+  float ll = 0.0f;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (uint32_t p = 0; p < np; p++) {
+    const size_t pr = (size_t)p * nrows + row;
+    const float2 ml = *(const float2 *)(a.part_ml + (pr * a.heads + head) * 2);
+    const float sc = nlg_exp2(ml.x - mm);
+    ll = fmaf(ml.y, sc, ll);
+    const float4 v = *(const float4 *)(a.part_o + pr * a.nq + (size_t)head * hd + 4 * d4);
+    acc.x = fmaf(v.x, sc, acc.x);
+    acc.y = fmaf(v.y, sc, acc.y);
+    acc.z = fmaf(v.z, sc, acc.z);
+    acc.w = fmaf(v.w, sc, acc.w);
+  }
+  const float4 out = ll > 0.0f ? make_float4(acc.x / ll, acc.y / ll, acc.z / ll, acc.w / ll)
+                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  *(float4 *)(a.ctx + (size_t)row * a.nq + (size_t)head * hd + 4 * d4) = out;
 }
 
 }  // namespace
@@ -242,14 +310,50 @@ int nlg_prefill_attn(const float *q, const uint16_t *kc, const uint16_t *vc, con
   const uint32_t nseq = rows / qper;
   if (nseq > 65535 || kvheads > 65535) return nlg_fail("prefill attn: too many sequences or kv heads");
   PrefillArgs a{q, kc, vc, pos, ctx, qper, heads, kvheads, max_seq, heads * head_dim,
-                1.0f / sqrtf((float)head_dim)};  // (/ 1.0 (sqrt (float hd)))
-  const dim3 grid((qper + PA_QB - 1) / PA_QB, kvheads, nseq), blk(64 * grp);
+                (1.0f / sqrtf((float)head_dim)) * NLG_LOG2E,  // (/ 1.0 (sqrt (float hd))), in base 2
+                nullptr, nullptr, 0, 0};
+  const uint32_t nqb = (qper + PA_QB - 1) / PA_QB;
+  // Too few workgroups to fill the CUs (one prompt: 16 query blocks x kv
+  // heads), and the last query block walks every key block while the first
+  // walks one: split each block's keys into pieces of PA_KPS key blocks,
+  // merged by a second launch.  The pieces' partials go to a per-stream
+  // workspace; without one (a capture that would have to grow it) the
+  // launch stays unsplit.
+  const uint32_t kblocks = (max_seq + PA_KB - 1) / PA_KB;
+  if ((uint64_t)nqb * kvheads * nseq < 256 && kblocks > PA_KPS) {
+    const uint32_t maxp = (kblocks + PA_KPS - 1) / PA_KPS;
+    const size_t o_bytes = (size_t)maxp * rows * a.nq * 4, ml_bytes = (size_t)maxp * rows * heads * 2 * 4;
+    uint8_t *ws = (uint8_t *)nlg_scratch_try((o_bytes + 255) / 256 * 256 + ml_bytes, st, 2);
+    if (ws && (uint64_t)nqb * maxp <= 0x7fffffffu) {
+      a.part_o = (float *)ws;
+      a.part_ml = (float *)(ws + (o_bytes + 255) / 256 * 256);
+      a.kps = PA_KPS;
+      a.maxp = maxp;
+      const dim3 grid(nqb * maxp, kvheads, nseq), blk(64 * grp);
+#define PAS(HD)                                                                              \
+  do {                                                                                       \
+    if (grp == 1) hipLaunchKernelGGL((k_prefill_attn<HD, 1, true>), grid, blk, 0, st, a);    \
+    else if (grp == 2) hipLaunchKernelGGL((k_prefill_attn<HD, 2, true>), grid, blk, 0, st, a); \
+    else if (grp == 4) hipLaunchKernelGGL((k_prefill_attn<HD, 4, true>), grid, blk, 0, st, a); \
+    else hipLaunchKernelGGL((k_prefill_attn<HD, 8, true>), grid, blk, 0, st, a);             \
+  } while (0)
+      if (head_dim == 128) PAS(128); else PAS(64);
+#undef PAS
+      NLG_LAUNCHED("prefill attention (fp16 KV, MFMA, split keys)");
+      const uint64_t nthr = (uint64_t)rows * heads * (head_dim / 4);
+      hipLaunchKernelGGL(k_prefill_merge, dim3((uint32_t)((nthr + 255) / 256)), dim3(256), 0, st, a, head_dim,
+                         rows);
+      NLG_LAUNCHED("prefill attention merge");
+      return NLG_OK;
+    }
+  }
+  const dim3 grid(nqb, kvheads, nseq), blk(64 * grp);
 #define PA(HD)                                                                             \
   do {                                                                                     \
-    if (grp == 1) hipLaunchKernelGGL((k_prefill_attn<HD, 1>), grid, blk, 0, st, a);        \
-    else if (grp == 2) hipLaunchKernelGGL((k_prefill_attn<HD, 2>), grid, blk, 0, st, a);   \
-    else if (grp == 4) hipLaunchKernelGGL((k_prefill_attn<HD, 4>), grid, blk, 0, st, a);   \
-    else hipLaunchKernelGGL((k_prefill_attn<HD, 8>), grid, blk, 0, st, a);                 \
+    if (grp == 1) hipLaunchKernelGGL((k_prefill_attn<HD, 1, false>), grid, blk, 0, st, a);        \
+    else if (grp == 2) hipLaunchKernelGGL((k_prefill_attn<HD, 2, false>), grid, blk, 0, st, a);   \
+    else if (grp == 4) hipLaunchKernelGGL((k_prefill_attn<HD, 4, false>), grid, blk, 0, st, a);   \
+    else hipLaunchKernelGGL((k_prefill_attn<HD, 8, false>), grid, blk, 0, st, a);                 \
   } while (0)
   if (head_dim == 128) PA(128); else PA(64);
 #undef PA
