@@ -845,22 +845,31 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   if (((uintptr_t)a.w2 & 15) || ((uintptr_t)a.xq & 15)) return nlg_fail("ternary GEMM: 16-byte alignment");
   a.wng = a.cols / 16;
   if (a.seq >= 128 && epi != NLG_EPI_ARGMAX) {
-    // the largest row tile (256, 128 or 64 rows) whose grid still fills the CUs
+    // Row tile: 256 rows once that grid has 128 workgroups (one 8-wave
+    // workgroup per CU: fewer, larger tiles re-read the activations less),
+    // else 128 rows once that grid has 192, else 64.  Measured at 512 and
+    // 2048 tokens over the config-5 linears (STORE epilogue): gate|up at 512
+    // tokens 256-row tiles (216 workgroups) 27.2 us against 29.4 with 128;
+    // QKV, O and down at 2048 tokens (160..240 workgroups) 28.2 / 26.6 /
+    // 50.5 us against 30.6 / 28.4 / 54.7; QKV at 512 tokens 64-row tiles
+    // 13.8 us against 17.4 / 23.2.  (Gate|up at 2048 tokens, 864 256-row
+    // workgroups, is the exception: 98.3 us against 91.7 with 128.)
     const uint32_t ty = (a.seq + 127) / 128;
-    const int tile = (uint64_t)nlg_blocks(a.out, 256) * ty >= 256   ? 256
-                     : (uint64_t)nlg_blocks(a.out, 128) * ty >= 256 ? 128
+    const int tile = (uint64_t)nlg_blocks(a.out, 256) * ty >= 128   ? 256
+                     : (uint64_t)nlg_blocks(a.out, 128) * ty >= 192 ? 128
                                                                     : 64;
     // Too few 64-row tiles to fill the CUs (e.g. 2560 rows x 512 tokens):
-    // split the columns into slices of at least 4 chunks, about 384
+    // split the columns into slices of at least 3 chunks, about 384
     // workgroups in all, when the per-stream split workspace is to be had
     // (measured: down projection 2560 x 6912 at 512 tokens 29.5 -> 24.5 us
-    // with 3 slices, at 128 tokens 25 -> 15 us with 6; 216 tiles gain
-    // nothing from 2)
+    // with 3 slices, at 128 tokens 25 -> 15 us with 6; the O projection
+    // 2560 x 2560 at 512 tokens 15.6 us with 2 slices, 14.8 with 3; 216
+    // tiles gain nothing from 2)
     const uint32_t ntile = nlg_blocks(a.out, tile) * ty, nch = a.cols / TG_KC;
     uint32_t ks = 1;
     if (a.allow_split && tile == 64 && ntile < 192 && nch >= 8) {
       ks = (384 + ntile - 1) / ntile;
-      if (ks > nch / 4) ks = nch / 4;
+      if (ks > nch / 3) ks = nch / 3;
       if (ks > 8) ks = 8;
     }
     if (ks > 1) {

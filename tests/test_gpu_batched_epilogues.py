@@ -58,14 +58,16 @@ def same_bits(a, b, what=""):
 def row_tile(seq, out):
     """The GEMM's row tile for seq >= 128 tokens (nlg_tgemm.hip's choice)."""
     ty = (seq + 127) // 128
-    for t in (256, 128):
-        if (out + t - 1) // t * ty >= 256:
-            return t
+    if (out + 255) // 256 * ty >= 128:
+        return 256
+    if (out + 127) // 128 * ty >= 192:
+        return 128
     return 64
 
 
-SWIGLU = [(128, 6912, 2560, True, 64), (512, 6912, 2560, True, 128), (600, 6912, 2560, True, 256),
-          (512, 640, 2560, False, 64), (400, 4096, 1024, True, 128)]
+SWIGLU = [(128, 6912, 2560, True, 64), (512, 6912, 2560, True, 256), (600, 6912, 2560, True, 256),
+          (512, 640, 2560, False, 64), (400, 4096, 1024, True, 256), (512, 3072, 1024, True, 128),
+          (300, 3840, 2560, False, 64)]
 
 
 @pytest.mark.parametrize("seq,dff,cols,rms,tile", SWIGLU)
@@ -87,8 +89,8 @@ def test_batched_swiglu(seq, dff, cols, rms, tile):
     assert np.all(err <= 1e-5 * np.abs(want) + 1e-7 * np.abs(want).max())
 
 
-RESID = [(128, 2560, 6912, 64), (512, 2560, 6912, 64), (512, 8192, 2560, 128), (600, 13824, 2560, 256),
-         (200, 1000, 512, 64)]
+RESID = [(128, 2560, 6912, 64), (512, 2560, 6912, 64), (512, 8192, 2560, 256), (600, 13824, 2560, 256),
+         (200, 1000, 512, 64), (512, 6144, 2560, 128), (512, 2560, 2560, 64)]
 
 
 @pytest.mark.parametrize("inplace", [False, True])
@@ -115,7 +117,8 @@ def rope_tables(max_seq, hd, theta=500000.0):
 
 # rows, qper (0: decode rows), heads, kvheads, head_dim, cols, max_seq, pos0, tile
 QKV = [(512, 512, 20, 5, 128, 2560, 768, 0, 64),      # config 5's prompt at B = 1
-       (600, 200, 64, 16, 128, 2560, 256, 40, 128),   # three prompts
+       (600, 200, 64, 16, 128, 2560, 256, 40, 256),   # three prompts
+       (512, 256, 32, 8, 128, 2560, 320, 40, 128),    # two prompts
        (512, 128, 64, 32, 128, 2560, 160, 20, 256),   # four prompts
        (128, 64, 8, 2, 64, 1024, 100, 50, 64),        # positions run past max_seq: no cache store there
        (128, 0, 20, 5, 128, 2560, 16, 5, 64)]         # 128 decode rows at one position
