@@ -380,8 +380,14 @@ int nlg_attn_ternary_linear_residual(const void *workspace, size_t workspace_byt
  * [rows/qper][kvheads][max_seq][head_dim] that nlg_rms_ternary_qkv_rope
  * fills.  q and ctx are [rows][heads*head_dim] f32; row r is sequence
  * r / qper at position pos[0] + r % qper.  head_dim 64 or 128, heads/kvheads
- * in {1,2,4,8}, rows a multiple of qper; one launch, f16 matrix cores with
- * q and the probabilities split into hi + lo halves (f32-grade products). */
+ * in {1,2,4,8}, rows a multiple of qper; f16 matrix cores with q and the
+ * probabilities split into hi + lo halves (f32-grade products).  One launch,
+ * or -- when the grid would have fewer than 256 workgroups (a single prompt)
+ * -- two: the keys of each query block in pieces, then their merge, with the
+ * pieces' partials in a scratch of the library kept per stream (grown on the
+ * first such call; a call being captured that would have to grow it runs as
+ * one launch instead).  Calls on one stream share that scratch, in stream
+ * order. */
 int nlg_prefill_attn_f16(const float *q, const uint16_t *kcache, const uint16_t *vcache,
                          const int32_t *pos, uint32_t rows, uint32_t qper, uint32_t heads,
                          uint32_t kvheads, uint32_t head_dim, uint32_t max_seq, float *ctx,
