@@ -67,7 +67,9 @@ __global__ __launch_bounds__(256) void k_mm(const float *__restrict__ A, const f
     }
     __syncthreads();
     if (ORDER == MM_SERIAL) {
-      // acc = acc + a*b, k ascending (kernels.el:24-26, :78-80)
+      // acc = acc + a*b, k ascending (kernels.el:24-26, :78-80); unrolled so
+      // the LDS reads run well ahead of the dependent adds
+#pragma unroll 32
       for (uint32_t k = 0; k < kc; k++) acc = __fadd_rn(acc, __fmul_rn(As[ty][k], Bs[k][tx]));
     } else {
       // kernels.el:99-104: acc + (p0 + (p1 + ... (p14 + p15))) per tile of 16
