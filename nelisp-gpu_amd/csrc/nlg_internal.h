@@ -278,6 +278,12 @@ void *nlg_scratch_try(size_t bytes, hipStream_t st, int slot);
 // The active device's fixed scratch array (NLG_NOALLOC_SCRATCH_BYTES), or
 // null with the error set.
 void *nlg_noalloc_scratch(void);
+// The registered tiled copy of 2-bit weights w2 of rows x cols (the prefill
+// GEMM's load order, nlg_repack.hip), or null; its size; and the release of
+// every copy at shutdown.
+const uint32_t *nlg_tiled_find(const uint32_t *w2, uint32_t rows, uint32_t cols);
+size_t nlg_tiled_bytes(uint32_t rows, uint32_t cols);
+void nlg_tiled_release_all(void);
 // Bytes the batched form needs for seq tokens of cols columns.
 size_t nlg_batched_scratch_bytes(uint32_t seq, uint32_t cols);
 // The rows-per-wave the launcher uses for `out` rows in mode `epi`.

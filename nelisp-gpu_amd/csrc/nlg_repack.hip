@@ -18,6 +18,9 @@
 
 #include "nlg_internal.h"
 
+#include <mutex>
+#include <unordered_map>
+
 namespace {
 
 __device__ __forceinline__ uint32_t code2(int32_t v) { return (uint32_t)v & 3u; }
@@ -190,5 +193,108 @@ extern "C" int nlg_repack_packed_to_2bit(const float *wpk, uint32_t out, uint32_
   else
     hipLaunchKernelGGL(k_repack_packed<16>, grid, blk, 0, nlg_stream(stream), wpk, out, cols, pk, fcount, wng, w2, nbad);
   NLG_LAUNCHED("repack base-4 codes to 2-bit");
+  return NLG_OK;
+}
+
+// ------------------------------------------------------------ tiled copies
+//
+// The prefill GEMM (k_tgemm_l) hands lane 32g + i of a wave the words
+// 8g..8g+7 of row i's 256-column chunk: 32 bytes of each of 32 rows, so a
+// load instruction over the row layout touches 32 cache lines and uses a
+// quarter of each.  The tiled copy stores each (32-row block, chunk) as one
+// 2 KiB tile in exactly that order: 16-byte unit u = 64h + 32g + i of tile
+// (b, c) is words 16c + 8g + 4h .. +3 of row 32b + i (zero past the last
+// row), and the tiles of a row block follow each other chunk by chunk.  The
+// wave's two loads of a chunk then read units lane and 64 + lane: 1 KiB
+// each, contiguous.  Same bits as the row layout, reordered.
+
+namespace {
+
+__global__ __launch_bounds__(256) void k_tile_2bit(const uint32_t *w2, uint32_t rows, uint32_t wng, uint32_t nch,
+                                                   uint64_t nunits, uint4 *wt) {
+  const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= nunits) return;
+  const uint32_t u = (uint32_t)idx & 127u;
+  const uint64_t tile = idx >> 7;
+  const uint32_t c = (uint32_t)(tile % nch), b = (uint32_t)(tile / nch);
+  const uint32_t i = u & 31u, g = (u >> 5) & 1u, h = u >> 6;
+  const uint32_t row = 32 * b + i;
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (row < rows) v = *(const uint4 *)(w2 + (size_t)row * wng + 16 * c + 8 * g + 4 * h);
+  wt[idx] = v;
+}
+
+struct TiledCopy {
+  uint32_t rows, cols;
+  uint32_t *wt;
+};
+std::mutex g_tiled_mu;
+std::unordered_map<const uint32_t *, TiledCopy> g_tiled;
+size_t g_tiled_n = 0;  // entries, read without the lock as a fast "none" test
+
+}  // namespace
+
+size_t nlg_tiled_bytes(uint32_t rows, uint32_t cols) { return (size_t)((rows + 31) / 32) * 32 * (cols / 4); }
+
+const uint32_t *nlg_tiled_find(const uint32_t *w2, uint32_t rows, uint32_t cols) {
+  if (!__atomic_load_n(&g_tiled_n, __ATOMIC_RELAXED)) return nullptr;
+  std::lock_guard<std::mutex> lk(g_tiled_mu);
+  const auto it = g_tiled.find(w2);
+  return it != g_tiled.end() && it->second.rows == rows && it->second.cols == cols ? it->second.wt : nullptr;
+}
+
+void nlg_tiled_release_all(void) {
+  std::lock_guard<std::mutex> lk(g_tiled_mu);
+  for (auto &kv : g_tiled) (void)hipFree(kv.second.wt);
+  g_tiled.clear();
+  __atomic_store_n(&g_tiled_n, 0, __ATOMIC_RELAXED);
+}
+
+extern "C" int nlg_ternary_tiled_register(const uint32_t *w2, uint32_t rows, uint32_t cols, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!w2) return nlg_fail("tiled weights: null weights");
+  if (!rows || !cols || cols % 256) return nlg_fail("tiled weights: rows must be nonzero, cols a multiple of 256");
+  if ((uintptr_t)w2 & 15) return nlg_fail("tiled weights: w2 must be 16-byte aligned");
+  const size_t bytes = nlg_tiled_bytes(rows, cols);
+  uint32_t *wt = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_tiled_mu);
+    auto it = g_tiled.find(w2);
+    if (it != g_tiled.end() && it->second.rows == rows && it->second.cols == cols) wt = it->second.wt;
+  }
+  const bool fresh = !wt;
+  if (fresh) {
+    const hipError_t e = hipMalloc((void **)&wt, bytes);
+    if (e != hipSuccess) return nlg_fail("tiled weights: hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+  }
+  const uint32_t nch = cols / 256;
+  const uint64_t nunits = bytes / 16;
+  hipStream_t st = nlg_stream(stream);
+  hipLaunchKernelGGL(k_tile_2bit, dim3((unsigned)((nunits + 255) / 256)), dim3(256), 0, st, w2, rows, cols / 16,
+                     nch, nunits, (uint4 *)wt);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) {
+    if (fresh) (void)hipFree(wt);
+    return nlg_fail("tiled weights: %s", hipGetErrorString(e));
+  }
+  if (fresh) {
+    std::lock_guard<std::mutex> lk(g_tiled_mu);
+    auto it = g_tiled.find(w2);
+    if (it != g_tiled.end()) (void)hipFree(it->second.wt);  // another shape before
+    g_tiled[w2] = TiledCopy{rows, cols, wt};
+    __atomic_store_n(&g_tiled_n, g_tiled.size(), __ATOMIC_RELAXED);
+  }
+  return NLG_OK;
+}
+
+extern "C" int nlg_ternary_tiled_unregister(const uint32_t *w2) {
+  std::lock_guard<std::mutex> lk(g_tiled_mu);
+  auto it = g_tiled.find(w2);
+  if (it == g_tiled.end()) return NLG_OK;
+  const hipError_t e = hipFree(it->second.wt);
+  g_tiled.erase(it);
+  __atomic_store_n(&g_tiled_n, g_tiled.size(), __ATOMIC_RELAXED);
+  if (e != hipSuccess) return nlg_fail("tiled weights: hipFree failed: %s", hipGetErrorString(e));
   return NLG_OK;
 }

@@ -137,6 +137,7 @@ void *nlg_scratch_try(size_t bytes, hipStream_t st, int slot) { return scratch_g
 extern "C" int nlg_shutdown(void) {
   if (!g_inited) return NLG_OK;
   (void)hipDeviceSynchronize();
+  nlg_tiled_release_all();
   {
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     for (auto &kv : g_scratch)

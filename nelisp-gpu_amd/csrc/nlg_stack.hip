@@ -219,6 +219,7 @@ struct nlg_stack {
   void *pattn_ws;
   size_t pattn_ws_bytes;
   uint32_t pcap;
+  bool tiled;  // prompt-order copies of the layer weights registered
   void *graph;
   uint32_t host_pos;
   bool started;
@@ -263,6 +264,9 @@ static int gen_normal(float *d, uint64_t n, uint64_t seed) {
 extern "C" void nlg_stack_destroy(nlg_stack *s) {
   if (!s) return;
   if (s->graph) nlg_graph_destroy(s->graph);
+  if (s->tiled)
+    for (Layer &y : s->L)
+      for (const uint32_t *w : {y.wqkv, y.wo, y.wgu, y.wd}) (void)nlg_ternary_tiled_unregister(w);
   for (void *p : s->allocs) nlg_free(p);
   for (void *p : {(void *)s->px, (void *)s->pq, (void *)s->ph, s->pattn_ws})
     if (p) nlg_free(p);
@@ -528,6 +532,19 @@ extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t 
     s->pattn_ws = nlg_malloc(s->pattn_ws_bytes);
     if (!s->px || !s->pq || !s->ph || !s->pattn_ws) return NLG_ERR;
     s->pcap = T;
+  }
+  if (T >= 128 && !s->tiled) {
+    // the matrix-core GEMMs of 128+ rows read tiled copies of the layer
+    // weights (one more copy of them, made once)
+    const uint32_t qkv = s->nq + 2 * s->nkv;
+    s->tiled = true;
+    for (Layer &y : s->L) {
+      if ((d % 256 == 0 && (nlg_ternary_tiled_register(y.wqkv, qkv, d, nullptr) ||
+                            nlg_ternary_tiled_register(y.wgu, 2 * f, d, nullptr))) ||
+          (s->nq % 256 == 0 && nlg_ternary_tiled_register(y.wo, d, s->nq, nullptr)) ||
+          (f % 256 == 0 && nlg_ternary_tiled_register(y.wd, d, f, nullptr)))
+        return NLG_ERR;
+    }
   }
   hipLaunchKernelGGL(k_embed_prompt, dim3(nlg_blocks(d, 256), T), dim3(256), 0, st, s->emb, s->prompt,
                      c.max_seq, P, s->px, d);

@@ -584,7 +584,7 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
 
 #define TL_PITCH (TG_KC + 16)   // LDS row pitch (bytes) of the activation stage
 
-template <int NB, int WR, int EPI, bool SPLIT = false>
+template <int NB, int WR, int EPI, bool SPLIT = false, bool TILED = false>
 __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   typedef int v16i __attribute__((ext_vector_type(16)));
   typedef uint32_t wvec __attribute__((ext_vector_type(8 * NB)));
@@ -601,14 +601,23 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   // this slice's chunks: [cfirst, nchunks)
   const uint32_t ntot = a.cols / TG_KC, ks = SPLIT ? gridDim.z : 1;
   const uint32_t cfirst = SPLIT ? blockIdx.z * ntot / ks : 0, nchunks = SPLIT ? (blockIdx.z + 1) * ntot / ks : ntot;
-  // weight rows of this lane: rbase + 32 nt + li (clamped; dead rows masked at the store)
+  // weight rows of this lane: rbase + 32 nt + li (clamped; dead rows masked
+  // at the store).  Row layout: the lane's 32 bytes of a chunk are 16-byte
+  // units 4c, 4c + 1 from word 8 lg of its row.  Tiled layout (a.w2 is the
+  // tiled copy): units 128c + lane and 128c + 64 + lane of its row block's
+  // run of 2 KiB tiles, so each load of the wave is 1 KiB contiguous.
   uint32_t rw[NB], rc[NB];
   const uint4 *wp[NB];
 #pragma unroll
   for (int nt = 0; nt < NB; nt++) {
     rw[nt] = rbase + 32 * nt + li;
     rc[nt] = rw[nt] < a.out ? rw[nt] : a.out - 1;
-    wp[nt] = (const uint4 *)(a.w2 + (size_t)rc[nt] * a.wng) + 2 * lg;
+    if (TILED) {
+      const uint32_t nrb = (a.out + 31) / 32, rb = rbase / 32 + nt < nrb ? rbase / 32 + nt : nrb - 1;
+      wp[nt] = (const uint4 *)a.w2 + (size_t)rb * ntot * 128 + lane;
+    } else {
+      wp[nt] = (const uint4 *)(a.w2 + (size_t)rc[nt] * a.wng) + 2 * lg;
+    }
   }
   // activation staging: thread t copies token t/16 + 8 WR i (i < AI), slot t % 16
   const uint32_t slot = threadIdx.x % 16u, tsub = threadIdx.x / 16u;
@@ -621,7 +630,8 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
 #define TL_LOADW(c, dst)                                                                   \
   do {                                                                                     \
     _Pragma("unroll") for (int nt = 0; nt < NB; nt++) {                                    \
-      const uint4 u0 = wp[nt][4 * (c)], u1 = wp[nt][4 * (c) + 1];                          \
+      const uint4 u0 = TILED ? wp[nt][128 * (c)] : wp[nt][4 * (c)];                         \
+      const uint4 u1 = TILED ? wp[nt][128 * (c) + 64] : wp[nt][4 * (c) + 1];                \
       dst[8 * nt + 0] = u0.x; dst[8 * nt + 1] = u0.y; dst[8 * nt + 2] = u0.z;               \
       dst[8 * nt + 3] = u0.w; dst[8 * nt + 4] = u1.x; dst[8 * nt + 5] = u1.y;               \
       dst[8 * nt + 6] = u1.z; dst[8 * nt + 7] = u1.w;                                       \
@@ -845,6 +855,10 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   if (((uintptr_t)a.w2 & 15) || ((uintptr_t)a.xq & 15)) return nlg_fail("ternary GEMM: 16-byte alignment");
   a.wng = a.cols / 16;
   if (a.seq >= 128 && epi != NLG_EPI_ARGMAX) {
+    // a registered tiled copy of the weights (nlg_ternary_tiled_register)
+    // replaces the row layout: the same words, in load order
+    const uint32_t *wt = nlg_tiled_find(a.w2, a.out, a.cols);
+    if (wt) a.w2 = wt;
     // Row tile: 256 rows once that grid has 128 workgroups (one 8-wave
     // workgroup per CU: fewer, larger tiles re-read the activations less),
     // else 128 rows once that grid has 192, else 64.  Measured at 512 and
@@ -888,12 +902,17 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
     const dim3 grid(nlg_blocks(a.out, tile), ty, ks), blk(tile == 256 ? 512 : 256);
     if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
     const size_t lds = (size_t)2 * 128 * TL_PITCH;
-#define TLG(E)                                                                            \
-  do {                                                                                    \
-    if (ks > 1) hipLaunchKernelGGL((k_tgemm_l<1, 2, E, true>), grid, blk, lds, st, a);    \
-    else if (tile == 256) hipLaunchKernelGGL((k_tgemm_l<2, 4, E>), grid, blk, lds, st, a); \
-    else if (tile == 128) hipLaunchKernelGGL((k_tgemm_l<2, 2, E>), grid, blk, lds, st, a); \
-    else hipLaunchKernelGGL((k_tgemm_l<1, 2, E>), grid, blk, lds, st, a);                 \
+#define TLT(E, T)                                                                                \
+  do {                                                                                           \
+    if (ks > 1) hipLaunchKernelGGL((k_tgemm_l<1, 2, E, true, T>), grid, blk, lds, st, a);        \
+    else if (tile == 256) hipLaunchKernelGGL((k_tgemm_l<2, 4, E, false, T>), grid, blk, lds, st, a); \
+    else if (tile == 128) hipLaunchKernelGGL((k_tgemm_l<2, 2, E, false, T>), grid, blk, lds, st, a); \
+    else hipLaunchKernelGGL((k_tgemm_l<1, 2, E, false, T>), grid, blk, lds, st, a);              \
+  } while (0)
+#define TLG(E)                                                                                   \
+  do {                                                                                           \
+    if (wt) TLT(E, true);                                                                        \
+    else TLT(E, false);                                                                          \
   } while (0)
     switch (epi) {
       case NLG_EPI_STORE: TLG(NLG_EPI_STORE); break;
@@ -903,6 +922,7 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
       default: return nlg_fail("ternary GEMM: unknown epilogue %d", epi);
     }
 #undef TLG
+#undef TLT
     NLG_LAUNCHED("ternary GEMM (int8 MFMA, 128 x 128 tiles)");
     return NLG_OK;
   }

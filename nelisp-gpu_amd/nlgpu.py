@@ -121,6 +121,8 @@ def lib() -> C.CDLL:
         "nlg_attn_entries_f16_workspace": (sz, [u32, u32, u32, u32, u32]),
         "nlg_block_copy_f16": (i32, [vp, vp, vp, u32, u32, u32, u32, vp]),
         "nlg_repack_packed_to_2bit": (i32, [vp, u32, u32, u32, u32, vp, vp, vp]),
+        "nlg_ternary_tiled_register": (i32, [vp, u32, u32, vp]),
+        "nlg_ternary_tiled_unregister": (i32, [vp]),
         "nlg_fill_normal": (i32, [vp, C.c_uint64, C.c_uint64, C.c_float, u32, vp]),
         "nlg_stack_create": (i32, [C.POINTER(StackConfig), C.POINTER(vp)]),
         "nlg_stack_destroy": (None, [vp]),
@@ -435,6 +437,16 @@ def repack_packed_to_2bit(wpk, out, cols, pk, fcount, w2, nbad=None, stream=None
     """base-4 codes in f32 [out x fcount] -> 2-bit words [out x ceil(cols/16)]."""
     _check(lib().nlg_repack_packed_to_2bit(wpk.ptr, out, cols, pk, fcount, w2.ptr, _ptr(nbad), stream),
            "repack_packed_to_2bit")
+
+
+def ternary_tiled_register(w2, rows, cols, stream=None) -> None:
+    """Keep a copy of 2-bit weights [rows x cols/16] in the prompt GEMM's load order."""
+    _check(lib().nlg_ternary_tiled_register(w2.ptr, rows, cols, stream), "ternary_tiled_register")
+
+
+def ternary_tiled_unregister(w2) -> None:
+    """Drop the tiled copy of w2 (a no-op when there is none)."""
+    _check(lib().nlg_ternary_tiled_unregister(w2.ptr), "ternary_tiled_unregister")
 
 
 def attn_ternary_linear_residual(workspace, batch, heads, kvheads, head_dim, max_seq, w2, bias, beta,

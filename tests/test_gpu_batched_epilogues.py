@@ -12,7 +12,9 @@ kernels on the CPU (tests/layer_ref.py):
   pos0 + r % qper).
 
 Each shape is chosen so the GEMM runs a given row tile: 256, 128 or 64 rows
-per workgroup (the largest whose grid still gives 256 workgroups).  The
+per workgroup (the largest whose grid still gives 256 workgroups).  Every
+case runs twice: with the weights' row layout, then with a registered tiled
+copy of them (nlg_ternary_tiled_register), which must give the same bits.  The
 activations of the RMSNorm cases are small integers, so the sum of squares
 is exact in any order and everything but SiLU's exp is bit-exact; SwiGLU's
 gate uses the device exp and is held to 1e-5 relative (the north star's
@@ -55,6 +57,15 @@ def same_bits(a, b, what=""):
     assert bad.size == 0, f"{what}: {bad.size} differ, first {bad[:4]}: {a[bad[:3]]} vs {b[bad[:3]]}"
 
 
+def with_tiled_copy(dw, rows, cols, run):
+    """run() again with a tiled copy of dw registered, then drop the copy."""
+    nlgpu.ternary_tiled_register(dw, rows, cols)
+    try:
+        return run()
+    finally:
+        nlgpu.ternary_tiled_unregister(dw)
+
+
 def row_tile(seq, out):
     """The GEMM's row tile for seq >= 128 tokens (nlg_tgemm.hip's choice)."""
     ty = (seq + 127) // 128
@@ -78,15 +89,21 @@ def test_batched_swiglu(seq, dff, cols, rms, tile):
     g = gains(cols + 2, cols)
     w2, beta = weights(dff + 11, 2 * dff, cols, per_row=True)
     dh = nlgpu.DeviceArray(seq * dff * 4)
-    nlgpu.rms_ternary_swiglu(nlgpu.to_device(x), nlgpu.to_device(g) if rms else None, 1e-5, nlgpu.to_device(w2),
-                             nlgpu.to_device(beta), dh, seq, dff, cols)
+    dx, dg, dw, db = nlgpu.to_device(x), nlgpu.to_device(g) if rms else None, nlgpu.to_device(w2), nlgpu.to_device(beta)
+
+    def run():
+        dh.zero()
+        nlgpu.rms_ternary_swiglu(dx, dg, 1e-5, dw, db, dh, seq, dff, cols)
+        return dh.download(f32, seq * dff)
+
+    got = run()
     xn = ref.rms(x, g, 1e-5, seq, cols) if rms else x
     gu = ref.linear(xn, w2, beta, seq, 2 * dff, cols, per_row=True).reshape(seq, 2 * dff)
     want = ref.silu_mul(gu[:, 0::2].ravel(), gu[:, 1::2].ravel())
-    got = dh.download(f32, seq * dff)
     err = np.abs(got - want)
     print(f"  max rel err {np.max(err / np.maximum(np.abs(want), 1e-30)):.2e}", flush=True)
     assert np.all(err <= 1e-5 * np.abs(want) + 1e-7 * np.abs(want).max())
+    same_bits(with_tiled_copy(dw, 2 * dff, cols, run), got, "tiled copy")
 
 
 RESID = [(128, 2560, 6912, 64), (512, 2560, 6912, 64), (512, 8192, 2560, 256), (600, 13824, 2560, 256),
@@ -103,10 +120,19 @@ def test_batched_residual(seq, out, cols, tile, inplace):
     bias = (nlgpu.normal(out + 1, out) * f32(0.1)).astype(f32)
     dres = nlgpu.to_device(res)
     dy = dres if inplace else nlgpu.DeviceArray(seq * out * 4)
-    nlgpu.ternary_linear_residual(nlgpu.to_device(x), nlgpu.to_device(w2), nlgpu.to_device(bias),
-                                  nlgpu.to_device(beta), dres, dy, seq, out, cols, beta_per_row=bool(out % 3))
+    dx, dw, dbias, db = nlgpu.to_device(x), nlgpu.to_device(w2), nlgpu.to_device(bias), nlgpu.to_device(beta)
+
+    def run():
+        dres.upload(res)
+        if not inplace:
+            dy.zero()
+        nlgpu.ternary_linear_residual(dx, dw, dbias, db, dres, dy, seq, out, cols, beta_per_row=bool(out % 3))
+        return dy.download(f32, seq * out)
+
+    got = run()
     want = (res + ref.linear(x, w2, beta, seq, out, cols, bias=bias, per_row=bool(out % 3))).astype(f32)
-    same_bits(dy.download(f32, seq * out), want, "residual")
+    same_bits(got, want, "residual")
+    same_bits(with_tiled_copy(dw, out, cols, run), got, "tiled copy")
 
 
 def rope_tables(max_seq, hd, theta=500000.0):
@@ -138,16 +164,27 @@ def test_batched_qkv_rope_append(rows, qper, heads, kvh, hd, cols, max_seq, pos0
     sentinel = np.full(nseq * kvh * max_seq * hd, 0x7BCD, np.uint16)
     dkc, dvc = nlgpu.to_device(sentinel), nlgpu.to_device(sentinel)
     dq = nlgpu.DeviceArray(rows * nq * 4)
-    args = (nlgpu.to_device(x), nlgpu.to_device(g), 1e-5, nlgpu.to_device(w2), nlgpu.to_device(beta), dq, dkc,
+    dw = nlgpu.to_device(w2)
+    args = (nlgpu.to_device(x), nlgpu.to_device(g), 1e-5, dw, nlgpu.to_device(beta), dq, dkc,
             dvc, nlgpu.to_device(co), nlgpu.to_device(si), nlgpu.to_device(np.array([pos0], np.int32)))
-    if qper:
-        nlgpu.rms_ternary_qkv_rope_prompt(*args, rows, qper, heads, kvh, hd, max_seq, cols)
-    else:
-        nlgpu.rms_ternary_qkv_rope(*args, rows, heads, kvh, hd, max_seq, cols)
+
+    def run():
+        dq.zero()
+        dkc.upload(sentinel)
+        dvc.upload(sentinel)
+        if qper:
+            nlgpu.rms_ternary_qkv_rope_prompt(*args, rows, qper, heads, kvh, hd, max_seq, cols)
+        else:
+            nlgpu.rms_ternary_qkv_rope(*args, rows, heads, kvh, hd, max_seq, cols)
+        return (dq.download(f32, rows * nq).reshape(rows, nq),
+                dkc.download(np.uint16).reshape(nseq, kvh, max_seq, hd),
+                dvc.download(np.uint16).reshape(nseq, kvh, max_seq, hd))
+
+    gq, kc, vc = run()
+    tq, tk, tv = with_tiled_copy(dw, out, cols, run)
+    same_bits(tq, gq, "tiled copy: q")
+    assert np.array_equal(tk, kc) and np.array_equal(tv, vc), "tiled copy: caches"
     qkv = ref.linear(ref.rms(x, g, 1e-5, rows, cols), w2, beta, rows, out, cols, per_row=True).reshape(rows, -1)
-    gq = dq.download(f32, rows * nq).reshape(rows, nq)
-    kc = dkc.download(np.uint16).reshape(nseq, kvh, max_seq, hd)
-    vc = dvc.download(np.uint16).reshape(nseq, kvh, max_seq, hd)
     if not qper:  # every row at pos0: decode-rope-b over the whole batch at once
         q = ref.rope_b(qkv[:, :nq].ravel(), co, si, pos0, rows, nq, heads).reshape(rows, nq)
         k = ref.rope_b(qkv[:, nq:nq + nkv].ravel(), co, si, pos0, rows, nkv, kvh).reshape(rows, kvh, hd)
@@ -178,3 +215,42 @@ def test_qkv_prompt_rejects_ragged_rows():
         nlgpu.rms_ternary_qkv_rope_prompt(d, d, 1e-5, d, d, d, d, d, d, d, pos, 10, 4, 4, 2, 64, 16, 256)
     with pytest.raises(nlgpu.NlgError, match="qper"):
         nlgpu.rms_ternary_qkv_rope_prompt(d, d, 1e-5, d, d, d, d, d, d, d, pos, 10, 0, 4, 2, 64, 16, 256)
+
+
+def test_tiled_copy_registration():
+    """A tiled copy is taken at registration: changed weights need a new
+    registration (which refreshes the copy in place); after unregistering,
+    the row layout is read again.  Shapes the copy cannot serve are refused."""
+    seq, out, cols = 256, 512, 1024
+    x = nlgpu.normal(7, seq * cols)
+    w_a, beta = weights(31, out, cols, per_row=False)
+    w_b, _ = weights(32, out, cols, per_row=False)
+    dx, dw, db = nlgpu.to_device(x), nlgpu.to_device(w_a), nlgpu.to_device(beta)
+    dy = nlgpu.DeviceArray(seq * out * 4)
+
+    def run():
+        dy.zero()
+        nlgpu.ternary_linear(dx, dw, None, db, dy, seq, out, cols)
+        return dy.download(f32, seq * out)
+
+    want_a = ref.linear(x, w_a, beta, seq, out, cols)
+    want_b = ref.linear(x, w_b, beta, seq, out, cols)
+    nlgpu.ternary_tiled_register(dw, out, cols)
+    try:
+        same_bits(run(), want_a, "tiled copy of A")
+        dw.upload(w_b)
+        same_bits(run(), want_a, "stale copy still A")  # the copy, not the rows, is read
+        nlgpu.ternary_tiled_register(dw, out, cols)
+        same_bits(run(), want_b, "refreshed copy of B")
+        # another shape over the same pointer is not served by the copy
+        dy.zero()
+        nlgpu.ternary_linear(dx, dw, None, db, dy, seq, out - 32, cols)
+        same_bits(dy.download(f32, seq * (out - 32)), ref.linear(x, w_b[:out - 32], beta, seq, out - 32, cols),
+                  "other rows: row layout")
+    finally:
+        nlgpu.ternary_tiled_unregister(dw)
+    dw.upload(w_a)
+    same_bits(run(), want_a, "unregistered: row layout")
+    nlgpu.ternary_tiled_unregister(dw)  # no copy: a no-op
+    with pytest.raises(nlgpu.NlgError, match="multiple of 256"):
+        nlgpu.ternary_tiled_register(dw, out, 1000)
