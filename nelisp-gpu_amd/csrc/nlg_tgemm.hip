@@ -566,7 +566,122 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
 }
 
 // ------------------------------------------------------------ k_tgemm_l
-//
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// Column slices of one tile meet here (k_tgemm_l's split form).  Every slice leaves its accumulators in its own block of
+// ksum with agent-coherent (write-through) stores, waits for them to
+// complete, and counts itself in; the last to arrive reads the other
+// slices' blocks (agent-coherent loads, past any stale L2 copy), adds them
+// -- integer sums, the same in any order -- and returns true to run the
+// epilogue.  It also re-zeros the tile's counter for the next launch,
+// which the stream orders after this one.  s_last: one LDS word.
+template <int NB>
+__device__ __forceinline__ bool tl_split_meet(const GemmArgs &a, v16i (&acc)[2][NB], uint32_t *s_last) {
+  constexpr int NR = 2 * NB * 16;  // accumulators per thread
+  const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x, ntile = gridDim.x * gridDim.y, ks = gridDim.z;
+  const size_t nthr = blockDim.x;
+  // register j of every thread side by side: each store and load of a
+  // wave covers 256 contiguous bytes
+  int32_t *mine = a.ksum + ((size_t)blockIdx.z * ntile + tile) * NR * nthr + threadIdx.x;
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int nt = 0; nt < NB; nt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+        __hip_atomic_store(mine + ((mt * NB + nt) * 16 + r) * nthr, acc[mt][nt][r], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t n = __hip_atomic_fetch_add(a.kctr + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_last = n + 1 == ks;
+    if (n + 1 == ks) __hip_atomic_store(a.kctr + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!*s_last) return false;
+  for (uint32_t z = 0; z < ks; z++) {
+    if (z == blockIdx.z) continue;
+    const int32_t *other = a.ksum + ((size_t)z * ntile + tile) * NR * nthr + threadIdx.x;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+      for (int nt = 0; nt < NB; nt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          acc[mt][nt][r] += __hip_atomic_load(other + ((mt * NB + nt) * 16 + r) * nthr, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return true;
+}
+
+// The epilogue of k_tgemm_l: acc[mt][nt] of lane (li, lg) of the
+// wave at token half wm, rows rw[nt] (clamped rc[nt]), with bias bo and
+// beta be per row block and the workgroup's 128 gammas in s_gm.
+template <int NB, int EPI>
+__device__ __forceinline__ void tl_epilogue(const GemmArgs &a, const v16i (&acc)[2][NB], const uint32_t (&rw)[NB],
+                                            const uint32_t (&rc)[NB], const float (&bo)[NB], const float (&be)[NB],
+                                            const float *s_gm, int lane, int wm, int lg, uint32_t tok0) {
+  // acc[mt][nt] register r is token tok0 + 64 wm + 32 mt + (r%4) + 8 (r/4) + 4 lg,
+  // row rw[nt].  gamma comes from LDS; the residual and RoPE
+  // operands of a (token block, row block) are all fetched before its first
+  // result is stored.  (y may be the residual itself, so the compiler keeps
+  // every load behind the stores before it: fetched beside its own store,
+  // each operand cost a memory round trip.  Measured at 16,384 tokens: the
+  // gate|up GEMM 813 -> 746 us, its STORE form 881 -> 712 us.)
+  if (EPI == NLG_EPI_SWIGLU) {
+    // Gate row 2j and up row 2j+1 sit in lanes l, l^1.  Each lane of a pair
+    // finishes half of the pair's tokens: the even lane registers 0..7, the
+    // odd lane 8..15, after swapping the other half's value with its partner.
+    const bool odd = lane & 1;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+#pragma unroll
+      for (int nt = 0; nt < NB; nt++) {
+        const v16i q = acc[mt][nt];
+        const bool lr = rw[nt] < a.out;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          const uint32_t tlo = tok0 + 64 * wm + 32 * mt + (k % 4) + 8 * (k / 4) + 4 * lg;
+          const uint32_t thi = tlo + 16;  // register k + 8
+          const float glo = s_gm[tlo - tok0], ghi = s_gm[thi - tok0];
+          // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
+          const float vlo = __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], glo), (float)(q[k] >> 6)));
+          const float vhi = __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], ghi), (float)(q[k + 8] >> 6)));
+          const float keep = odd ? vhi : vlo, give = odd ? vlo : vhi;
+          const float got = __int_as_float(nlg_dpp<0xB1>(__float_as_int(give)));  // from lane ^ 1
+          const float g = odd ? got : keep, u = odd ? keep : got;
+          const uint32_t tk = odd ? thi : tlo;
+          if (lr && tk < a.seq) {
+            const float sg = nlg_silu_gate(g);
+            a.y[(size_t)tk * a.ystride + (rw[nt] >> 1)] = (g * sg) * u;
+          }
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++) {
+#pragma unroll
+    for (int nt = 0; nt < NB; nt++) {
+      TgPre pre[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+        pre[r] = tg_prefetch<EPI>(a, rc[nt], tok0 + 64 * wm + 32 * mt + (r % 4) + 8 * (r / 4) + 4 * lg);
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const uint32_t tk = tok0 + 64 * wm + 32 * mt + (r % 4) + 8 * (r / 4) + 4 * lg;
+        // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
+        const float v =
+            __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], s_gm[tk - tok0]), (float)(acc[mt][nt][r] >> 6)));
+        tg_store_pre<EPI>(a, lane, rw[nt], tk, rw[nt] < a.out && tk < a.seq, v, pre[r]);
+      }
+    }
+  }
+}
+
 // Many tokens (prefill): a workgroup owns 32 NB WR output rows x 128 tokens;
 // its 2 WR waves 32 NB rows x 64 tokens each (NB x 2 blocks of
 // v_mfma_i32_32x32x32_i8, whose layout, checked on gfx950, is
@@ -586,7 +701,6 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
 
 template <int NB, int WR, int EPI, bool SPLIT = false, bool TILED = false>
 __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
-  typedef int v16i __attribute__((ext_vector_type(16)));
   typedef uint32_t wvec __attribute__((ext_vector_type(8 * NB)));
   constexpr int AI = 16 / WR;  // 16-byte activation pieces per thread and chunk
   typedef uint32_t avec __attribute__((ext_vector_type(4 * AI)));
@@ -721,107 +835,10 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
 #undef TL_LOADA
 #undef TL_STOREA
   if (SPLIT) {
-    // Column slices meet here.  Every slice leaves its accumulators in its
-    // own block of ksum with agent-coherent (write-through) stores, waits
-    // for them to complete, and counts itself in; the last to arrive reads
-    // the other slices' blocks (agent-coherent loads, past any stale L2
-    // copy), adds them -- integer sums, the same in any order -- and goes
-    // on to the epilogue.  It also re-zeros the tile's counter for the next
-    // launch, which the stream orders after this one.
-    constexpr int NR = 2 * NB * 16;  // accumulators per thread
-    const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x, ntile = gridDim.x * gridDim.y;
-    const size_t nthr = blockDim.x;
-    // register j of every thread side by side: each store and load of a
-    // wave covers 256 contiguous bytes
-    int32_t *mine = a.ksum + ((size_t)blockIdx.z * ntile + tile) * NR * nthr + threadIdx.x;
-#pragma unroll
-    for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-      for (int nt = 0; nt < NB; nt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++)
-          __hip_atomic_store(mine + ((mt * NB + nt) * 16 + r) * nthr, acc[mt][nt][r], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
     __shared__ uint32_t s_last;
-    if (threadIdx.x == 0) {
-      const uint32_t n = __hip_atomic_fetch_add(a.kctr + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = n + 1 == ks;
-      if (n + 1 == ks) __hip_atomic_store(a.kctr + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    for (uint32_t z = 0; z < ks; z++) {
-      if (z == blockIdx.z) continue;
-      const int32_t *other = a.ksum + ((size_t)z * ntile + tile) * NR * nthr + threadIdx.x;
-#pragma unroll
-      for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-        for (int nt = 0; nt < NB; nt++)
-#pragma unroll
-          for (int r = 0; r < 16; r++)
-            acc[mt][nt][r] += __hip_atomic_load(other + ((mt * NB + nt) * 16 + r) * nthr, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (!tl_split_meet<NB>(a, acc, &s_last)) return;
   }
-  // epilogue: acc[mt][nt] register r is token tok0 + 64 wm + 32 mt + (r%4) + 8 (r/4) + 4 lg,
-  // row rbase + 32 nt + li.  gamma comes from LDS; the residual and RoPE
-  // operands of a (token block, row block) are all fetched before its first
-  // result is stored.  (y may be the residual itself, so the compiler keeps
-  // every load behind the stores before it: fetched beside its own store,
-  // each operand cost a memory round trip.  Measured at 16,384 tokens: the
-  // gate|up GEMM 813 -> 746 us, its STORE form 881 -> 712 us.)
-  if (EPI == NLG_EPI_SWIGLU) {
-    // Gate row 2j and up row 2j+1 sit in lanes l, l^1.  Each lane of a pair
-    // finishes half of the pair's tokens: the even lane registers 0..7, the
-    // odd lane 8..15, after swapping the other half's value with its partner.
-    const bool odd = lane & 1;
-#pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
-#pragma unroll
-      for (int nt = 0; nt < NB; nt++) {
-        const v16i q = acc[mt][nt];
-        const bool lr = rw[nt] < a.out;
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-          const uint32_t tlo = tok0 + 64 * wm + 32 * mt + (k % 4) + 8 * (k / 4) + 4 * lg;
-          const uint32_t thi = tlo + 16;  // register k + 8
-          const float glo = s_gm[tlo - tok0], ghi = s_gm[thi - tok0];
-          // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
-          const float vlo = __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], glo), (float)(q[k] >> 6)));
-          const float vhi = __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], ghi), (float)(q[k + 8] >> 6)));
-          const float keep = odd ? vhi : vlo, give = odd ? vlo : vhi;
-          const float got = __int_as_float(nlg_dpp<0xB1>(__float_as_int(give)));  // from lane ^ 1
-          const float g = odd ? got : keep, u = odd ? keep : got;
-          const uint32_t tk = odd ? thi : tlo;
-          if (lr && tk < a.seq) {
-            const float sg = nlg_silu_gate(g);
-            a.y[(size_t)tk * a.ystride + (rw[nt] >> 1)] = (g * sg) * u;
-          }
-        }
-      }
-    }
-    return;
-  }
-#pragma unroll
-  for (int mt = 0; mt < 2; mt++) {
-#pragma unroll
-    for (int nt = 0; nt < NB; nt++) {
-      TgPre pre[16];
-#pragma unroll
-      for (int r = 0; r < 16; r++)
-        pre[r] = tg_prefetch<EPI>(a, rc[nt], tok0 + 64 * wm + 32 * mt + (r % 4) + 8 * (r / 4) + 4 * lg);
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const uint32_t tk = tok0 + 64 * wm + 32 * mt + (r % 4) + 8 * (r / 4) + 4 * lg;
-        // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
-        const float v =
-            __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], s_gm[tk - tok0]), (float)(acc[mt][nt][r] >> 6)));
-        tg_store_pre<EPI>(a, lane, rw[nt], tk, rw[nt] < a.out && tk < a.seq, v, pre[r]);
-      }
-    }
-  }
+  tl_epilogue<NB, EPI>(a, acc, rw, rc, bo, be, s_gm, lane, wm, lg, tok0);
 }
 
 // ------------------------------------------------------------ launchers
