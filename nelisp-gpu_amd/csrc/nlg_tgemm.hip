@@ -43,14 +43,20 @@ struct ActQArgs {
   uint32_t seq, cols;
 };
 
-// G16: 16-column groups per thread (cols <= 4096 * G16).
+// 256 threads per token row; thread t holds the row's float4s t + 256 j
+// (j < 4 G16, cols <= 4096 G16), so every load of a wave reads 1 KiB
+// contiguous.  A 16-column group's four float4s sit in the four lanes of a
+// quad; each lane quantises its own word and the 4x4 byte transpose into
+// matrix-core order runs across the quad (DPP broadcasts), each lane then
+// storing one word of the group (256 contiguous bytes per wave store).
 template <int G16, int PRO>
 __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
+  constexpr int J = 4 * G16;
   __shared__ float red[4], red2[4];  // the two reductions' own scratch: no reuse barrier
   asm volatile("" ::"s"(a.x), "s"(a.gain), "s"(a.xq), "s"(a.gamma), "s"(a.cols));
   const uint32_t tok = blockIdx.x;
-  const uint32_t ngrp = a.cols >> 4, nf4 = a.cols >> 2;
-  float4 v[G16][4];
+  const uint32_t nf4 = a.cols >> 2;
+  float4 v[J];
   // PRO_ATTN3: exactly three chunks (see k_tern_fused's prologue)
   constexpr bool ATT = PRO == NLG_PRO_ATTN || PRO == NLG_PRO_ATTN3;
   constexpr int NC = PRO == NLG_PRO_ATTN3 ? 3 : NLG_ATTN_MAX_CHUNKS;
@@ -59,110 +65,100 @@ __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
     const uint32_t heads = a.cols / a.hd;
     const float4 *c4 = (const float4 *)a.x;
 #pragma unroll
-    for (int k = 0; k < G16; k++) {
-      const uint32_t gi = threadIdx.x + 256u * k, gc = gi < ngrp ? gi : ngrp - 1;
+    for (int j = 0; j < J; j++) {
+      const uint32_t f0 = threadIdx.x + 256u * j, f = f0 < nf4 ? f0 : nf4 - 1, h = (4 * f) / a.hd;
+      float4 cx[NC];
+      float2 mz[NC];
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint32_t f = 4 * gc + q, h = (4 * f) / a.hd;
-        float4 cx[NC];
-        float2 mz[NC];
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-          const uint32_t cc = (uint32_t)c < a.attn_nc ? (uint32_t)c : a.attn_nc - 1;
-          const size_t tc = (size_t)tok * a.attn_nc + cc;
-          cx[c] = c4[tc * nf4 + f];
-          mz[c] = *(const float2 *)(a.attn_mz + (tc * heads + h) * 2);
-        }
-        float mm = -1.0e30f;
-#pragma unroll
-        for (int c = 0; c < NC; c++) mm = mz[c].x > mm ? mz[c].x : mm;
-        float zz = 0.0f;
-        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-          const float sc = (uint32_t)c < a.attn_nc ? nlg_exp2(mz[c].x - mm) : 0.0f;  // base-2 maxima
-          zz = fmaf(mz[c].y, sc, zz);
-          acc.x = fmaf(cx[c].x, sc, acc.x);
-          acc.y = fmaf(cx[c].y, sc, acc.y);
-          acc.z = fmaf(cx[c].z, sc, acc.z);
-          acc.w = fmaf(cx[c].w, sc, acc.w);
-        }
-        v[k][q] = make_float4(acc.x / zz, acc.y / zz, acc.z / zz, acc.w / zz);
+      for (int c = 0; c < NC; c++) {
+        const uint32_t cc = (uint32_t)c < a.attn_nc ? (uint32_t)c : a.attn_nc - 1;
+        const size_t tc = (size_t)tok * a.attn_nc + cc;
+        cx[c] = c4[tc * nf4 + f];
+        mz[c] = *(const float2 *)(a.attn_mz + (tc * heads + h) * 2);
       }
+      float mm = -1.0e30f;
+#pragma unroll
+      for (int c = 0; c < NC; c++) mm = mz[c].x > mm ? mz[c].x : mm;
+      float zz = 0.0f;
+      float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const float sc = (uint32_t)c < a.attn_nc ? nlg_exp2(mz[c].x - mm) : 0.0f;  // base-2 maxima
+        zz = fmaf(mz[c].y, sc, zz);
+        acc.x = fmaf(cx[c].x, sc, acc.x);
+        acc.y = fmaf(cx[c].y, sc, acc.y);
+        acc.z = fmaf(cx[c].z, sc, acc.z);
+        acc.w = fmaf(cx[c].w, sc, acc.w);
+      }
+      v[j] = make_float4(acc.x / zz, acc.y / zz, acc.z / zz, acc.w / zz);
     }
   } else {
     const float4 *x4 = (const float4 *)(a.x + (size_t)tok * a.cols);
 #pragma unroll
-    for (int k = 0; k < G16; k++) {
-      const uint32_t gi = threadIdx.x + 256u * k, gc = gi < ngrp ? gi : ngrp - 1;
-#pragma unroll
-      for (int q = 0; q < 4; q++) v[k][q] = x4[4 * gc + q];
+    for (int j = 0; j < J; j++) {
+      const uint32_t f0 = threadIdx.x + 256u * j;
+      v[j] = x4[f0 < nf4 ? f0 : nf4 - 1];
     }
   }
-  float4 gv[G16][4];
+  float4 gv[J];
   if (PRO == NLG_PRO_RMS) {
     const float4 *g4 = (const float4 *)a.gain;
 #pragma unroll
-    for (int k = 0; k < G16; k++) {
-      const uint32_t gi = threadIdx.x + 256u * k, gc = gi < ngrp ? gi : ngrp - 1;
-#pragma unroll
-      for (int q = 0; q < 4; q++) gv[k][q] = g4[4 * gc + q];
+    for (int j = 0; j < J; j++) {
+      const uint32_t f0 = threadIdx.x + 256u * j;
+      gv[j] = g4[f0 < nf4 ? f0 : nf4 - 1];
     }
   }
 #pragma unroll
-  for (int k = 0; k < G16; k++)
-    if (threadIdx.x + 256u * k >= ngrp)
-#pragma unroll
-      for (int q = 0; q < 4; q++) v[k][q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int j = 0; j < J; j++)
+    if (threadIdx.x + 256u * j >= nf4) v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (PRO == NLG_PRO_RMS) {
     float sq = 0.0f;
 #pragma unroll
-    for (int k = 0; k < G16; k++)
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        sq = sq + v[k][q].x * v[k][q].x;
-        sq = sq + v[k][q].y * v[k][q].y;
-        sq = sq + v[k][q].z * v[k][q].z;
-        sq = sq + v[k][q].w * v[k][q].w;
-      }
+    for (int j = 0; j < J; j++) {
+      sq = sq + v[j].x * v[j].x;
+      sq = sq + v[j].y * v[j].y;
+      sq = sq + v[j].z * v[j].z;
+      sq = sq + v[j].w * v[j].w;
+    }
     sq = nlg_block_sum_f32<4, true>(sq, red);
     sq = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq)));
     const float istd = 1.0f / sqrtf(sq / (float)a.cols + a.eps);
 #pragma unroll
-    for (int k = 0; k < G16; k++)
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        v[k][q].x = (v[k][q].x * istd) * gv[k][q].x;
-        v[k][q].y = (v[k][q].y * istd) * gv[k][q].y;
-        v[k][q].z = (v[k][q].z * istd) * gv[k][q].z;
-        v[k][q].w = (v[k][q].w * istd) * gv[k][q].w;
-      }
+    for (int j = 0; j < J; j++) {
+      v[j].x = (v[j].x * istd) * gv[j].x;
+      v[j].y = (v[j].y * istd) * gv[j].y;
+      v[j].z = (v[j].z * istd) * gv[j].z;
+      v[j].w = (v[j].w * istd) * gv[j].w;
+    }
   }
   float amax = 0.0f;
 #pragma unroll
-  for (int k = 0; k < G16; k++)
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      float t;
-      t = dsl_abs(v[k][q].x); amax = t > amax ? t : amax;
-      t = dsl_abs(v[k][q].y); amax = t > amax ? t : amax;
-      t = dsl_abs(v[k][q].z); amax = t > amax ? t : amax;
-      t = dsl_abs(v[k][q].w); amax = t > amax ? t : amax;
-    }
+  for (int j = 0; j < J; j++) {
+    float t;
+    t = dsl_abs(v[j].x); amax = t > amax ? t : amax;
+    t = dsl_abs(v[j].y); amax = t > amax ? t : amax;
+    t = dsl_abs(v[j].z); amax = t > amax ? t : amax;
+    t = dsl_abs(v[j].w); amax = t > amax ? t : amax;
+  }
   amax = nlg_block_max_f32<4, true>(amax, red2);
   const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
   const float ginv = 1.0f / g;
   const bool fast = g > 0.0f && ginv < INFINITY;
   if (threadIdx.x == 0) a.gamma[tok] = g;
-  uint4 *dst = (uint4 *)(a.xq + (size_t)tok * a.cols);
+  // Lane i of a quad holds the group's word n_i (its columns 4i..4i+3) and
+  // writes y_i = (n0.b_i, n1.b_i, n2.b_i, n3.b_i): byte i of each word.
+  const uint32_t i = threadIdx.x & 3u;
+  const uint32_t sel_lo = 0x0c0c0000u | ((4u + i) << 8) | i, sel_hi = 0x00000c0cu | ((4u + i) << 24) | (i << 16);
+  uint32_t *dst = (uint32_t *)(a.xq + (size_t)tok * a.cols);
 #pragma unroll
-  for (int k = 0; k < G16; k++) {
-    const uint32_t gi = threadIdx.x + 256u * k;
-    const uint32_t n0 = quant_word(v[k][0], g, ginv, fast), n1 = quant_word(v[k][1], g, ginv, fast);
-    const uint32_t n2 = quant_word(v[k][2], g, ginv, fast), n3 = quant_word(v[k][3], g, ginv, fast);
-    uint32_t y0, y1, y2, y3;
-    xpose4(n0, n1, n2, n3, y0, y1, y2, y3);
-    if (gi < ngrp) dst[gi] = make_uint4(y0, y1, y2, y3);
+  for (int j = 0; j < J; j++) {
+    const uint32_t f = threadIdx.x + 256u * j;
+    const int n = (int)quant_word(v[j], g, ginv, fast);
+    const uint32_t n0 = (uint32_t)nlg_dpp<0x00>(n), n1 = (uint32_t)nlg_dpp<0x55>(n);
+    const uint32_t n2 = (uint32_t)nlg_dpp<0xAA>(n), n3 = (uint32_t)nlg_dpp<0xFF>(n);
+    const uint32_t y = __builtin_amdgcn_perm(n1, n0, sel_lo) | __builtin_amdgcn_perm(n3, n2, sel_hi);
+    if (f < nf4) dst[f] = y;
   }
 }
 
