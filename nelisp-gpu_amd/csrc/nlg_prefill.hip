@@ -49,7 +49,6 @@ struct PrefillArgs {
 
 #define PA_KB 32  // keys per block
 #define PA_QB 32  // query positions per workgroup
-#define PA_KPS 4  // key blocks per piece of a split launch
 
 __device__ __forceinline__ v8h f16x8(uint4 u) { return __builtin_bit_cast(v8h, u); }
 
@@ -315,19 +314,23 @@ int nlg_prefill_attn(const float *q, const uint16_t *kc, const uint16_t *vc, con
   const uint32_t nqb = (qper + PA_QB - 1) / PA_QB;
   // Too few workgroups to fill the CUs (one prompt: 16 query blocks x kv
   // heads), and the last query block walks every key block while the first
-  // walks one: split each block's keys into pieces of PA_KPS key blocks,
-  // merged by a second launch.  The pieces' partials go to a per-stream
-  // workspace; without one (a capture that would have to grow it) the
-  // launch stays unsplit.
-  const uint32_t kblocks = (max_seq + PA_KB - 1) / PA_KB;
-  if ((uint64_t)nqb * kvheads * nseq < 256 && kblocks > PA_KPS) {
-    const uint32_t maxp = (kblocks + PA_KPS - 1) / PA_KPS;
+  // walks one: split each block's keys into pieces of kps key blocks,
+  // merged by a second launch.  kps is half the key blocks a prompt
+  // starting at position 0 spans (at least 4), so the longest query blocks
+  // take two equal pieces (measured at 512 tokens, 20/5 heads: pieces of 8
+  // blocks 24.5 us with the merge, of 4 27.2, 6 29.2, 12 28.5, 1 39.8;
+  // unsplit 27.2).  The pieces' partials go to a per-stream workspace;
+  // without one (a capture that would have to grow it) the launch stays
+  // unsplit.
+  const uint32_t kblocks = (max_seq + PA_KB - 1) / PA_KB, kps = nqb / 2 + nqb % 2 > 4 ? nqb / 2 + nqb % 2 : 4;
+  if ((uint64_t)nqb * kvheads * nseq < 256 && kblocks > kps) {
+    const uint32_t maxp = (kblocks + kps - 1) / kps;
     const size_t o_bytes = (size_t)maxp * rows * a.nq * 4, ml_bytes = (size_t)maxp * rows * heads * 2 * 4;
     uint8_t *ws = (uint8_t *)nlg_scratch_try((o_bytes + 255) / 256 * 256 + ml_bytes, st, 2);
     if (ws && (uint64_t)nqb * maxp <= 0x7fffffffu) {
       a.part_o = (float *)ws;
       a.part_ml = (float *)(ws + (o_bytes + 255) / 256 * 256);
-      a.kps = PA_KPS;
+      a.kps = kps;
       a.maxp = maxp;
       const dim3 grid(nqb * maxp, kvheads, nseq), blk(64 * grp);
 #define PAS(HD)                                                                              \
