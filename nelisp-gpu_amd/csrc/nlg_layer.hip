@@ -296,7 +296,10 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
 // at the decode shapes (graph-timed, weights streamed from HBM): 4 rows per
 // wave for 2560..4096 outputs, 8 for the 13824-row gate|up and the LM head.
 int nlg_fused_rows_per_wave(uint32_t out, int epi) {
-  if (epi == NLG_EPI_ARGMAX) return out >= 32768 ? 8 : 4;
+  // the LM head: 16 rows per wave (128,256 x 2,560, one row, graph-timed with
+  // the argmax: 8 rows 34.9 us, 16 30.6, 32 34.0; the quantisation as its
+  // own launch in front of a prologue-free GEMV measured 32.0)
+  if (epi == NLG_EPI_ARGMAX) return out >= 32768 ? 16 : 4;
   if (epi == NLG_EPI_SWIGLU || epi == NLG_EPI_QKV) return out >= 8192 ? 8 : (out >= 2048 ? 4 : 2);
   return out >= 8192 ? 8 : (out >= 2048 ? 4 : (out >= 1024 ? 2 : 1));
 }
@@ -346,14 +349,18 @@ int nlg_fused_launch(const FusedArgs &a0, int pro, int epi, int rpw, hipStream_t
       default: fused_go<P, E, 4>(a, grid, lds, st); break; \
     }                                                     \
   } while (0)
-  if (rpw != 1 && rpw != 2 && rpw != 4 && rpw != 8) return nlg_fail("rows_per_wave must be 1, 2, 4 or 8");
+  if (rpw != 1 && rpw != 2 && rpw != 4 && rpw != 8 && !(rpw == 16 && epi == NLG_EPI_ARGMAX))
+    return nlg_fail("rows_per_wave must be 1, 2, 4 or 8 (or 16 for an argmax)");
   if (pro == NLG_PRO_NONE && epi == NLG_EPI_STORE) PE(NLG_PRO_NONE, NLG_EPI_STORE);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_STORE) PE(NLG_PRO_RMS, NLG_EPI_STORE);
   else if (pro == NLG_PRO_NONE && epi == NLG_EPI_RESID) PE(NLG_PRO_NONE, NLG_EPI_RESID);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_SWIGLU) PE(NLG_PRO_RMS, NLG_EPI_SWIGLU);
   else if (pro == NLG_PRO_NONE && epi == NLG_EPI_SWIGLU) PE(NLG_PRO_NONE, NLG_EPI_SWIGLU);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_QKV) PE(NLG_PRO_RMS, NLG_EPI_QKV);
-  else if (pro == NLG_PRO_RMS && epi == NLG_EPI_ARGMAX) PE(NLG_PRO_RMS, NLG_EPI_ARGMAX);
+  else if (pro == NLG_PRO_RMS && epi == NLG_EPI_ARGMAX) {
+    if (rpw == 16) fused_go<NLG_PRO_RMS, NLG_EPI_ARGMAX, 16>(a, grid, lds, st);
+    else PE(NLG_PRO_RMS, NLG_EPI_ARGMAX);
+  }
   else if (pro == NLG_PRO_ATTN && epi == NLG_EPI_RESID) {
     if (!a.hd || a.hd % 4 || a.cols % a.hd || !a.attn_nc || a.attn_nc > NLG_ATTN_MAX_CHUNKS || !a.attn_mz)
       return nlg_fail("fused ternary linear: bad attention partials (hd %u, chunks %u)", a.hd, a.attn_nc);

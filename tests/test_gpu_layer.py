@@ -154,9 +154,13 @@ def test_qkv_rope_and_fp16_append(B, heads, kvh, hd, cols, max_seq, pos):
     assert np.all(kc == 0x7BCD) and np.all(vc == 0x7BCD)  # nothing else written
 
 
+# vocabularies of 32,768 rows and more at under 8 rows take the LM-head form
+# (one quantisation launch, then the streaming GEMV at 1, 2 or 4 chunks per lane)
 @pytest.mark.parametrize("seq,vocab,cols,dup", [(1, 128256, 2560, False), (2, 1000, 256, True), (1, 37, 64, True),
                                                 (32, 128256, 2560, False), (8, 1000, 256, True),
-                                                (16, 9000, 2560, False), (32, 9000, 2560, True)])
+                                                (16, 9000, 2560, False), (32, 9000, 2560, True),
+                                                (2, 40000, 1024, True), (1, 33000, 6144, True),
+                                                (3, 32800, 9216, False)])
 def test_lm_head_argmax(seq, vocab, cols, dup):
     print(f"[gpu] argmax seq={seq} vocab={vocab} cols={cols}", flush=True)
     x, g = int_rows(vocab, seq * cols), gains(cols + 9, cols)
