@@ -181,20 +181,35 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
       sc[r] = key <= pj ? sc[r] * a.coef : -INFINITY;  // (q.k / sqrt(hd)) * log2(e)
       mb = fmaxf(mb, sc[r]);
     }
-    mb = fmaxf(mb, __shfl_xor(mb, 32));
-    const float mn = fmaxf(m, mb);
-    const float al = nlg_exp2(m - mn);
+    // lanes l and l ^ 32 hold the same query: v_permlane32_swap hands each
+    // the other's value (the pair it returns is {x[l], x[l ^ 32]})
+    {
+      const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(mb), __float_as_uint(mb), false, false);
+      mb = fmaxf(__uint_as_float(pr[0]), __uint_as_float(pr[1]));
+    }
+    // The running reference m moves only when a block beats it by more than
+    // 2^8 (probabilities then stay <= 256, which the fp16 hi + lo split
+    // carries exactly), so most blocks skip rescaling the context: the
+    // multiplies run only when some query of the wave moved.
+    const bool up = mb > m + 8.0f;
+    const float mn = up ? mb : m;
+    const float al = nlg_exp2(m - mn);  // 1 where m stays
     float ls = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       sc[r] = nlg_exp2(sc[r] - mn);
       ls += sc[r];
     }
-    ls += __shfl_xor(ls, 32);
+    {
+      const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(ls), __float_as_uint(ls), false, false);
+      ls = __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
+    }
     l = l * al + ls;
     m = mn;
+    if (__builtin_amdgcn_ballot_w64(up) != 0ull) {
 #pragma unroll
-    for (int t = 0; t < HD / 32; t++) o[t] *= al;
+      for (int t = 0; t < HD / 32; t++) o[t] *= al;
+    }
     // O^T += V^T P^T over two steps of 16 keys; element e of step s2 is key
     // 16 s2 + 8 (e/4) + 4 lg + e%4 in both operands
 #pragma unroll
