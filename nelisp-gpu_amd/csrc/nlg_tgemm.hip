@@ -886,18 +886,30 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
                      : (uint64_t)nlg_blocks(a.out, 128) * ty >= 192 ? 128
                                                                     : 64;
     // Too few 64-row tiles to fill the CUs (e.g. 2560 rows x 512 tokens):
-    // split the columns into slices of at least 3 chunks, about 384
-    // workgroups in all, when the per-stream split workspace is to be had
-    // (measured: down projection 2560 x 6912 at 512 tokens 29.5 -> 24.5 us
-    // with 3 slices, at 128 tokens 25 -> 15 us with 6; the O projection
-    // 2560 x 2560 at 512 tokens 15.6 us with 2 slices, 14.8 with 3; 216
-    // tiles gain nothing from 2)
+    // split the columns over gridDim.z slices (about 384 workgroups in all),
+    // when the per-stream split workspace is to be had.  Row layout: slices
+    // of at least 3 chunks, at most 8 (measured: down projection 2560 x 6912
+    // at 512 tokens 29.5 -> 24.5 us with 3 slices, at 128 tokens 25 -> 15
+    // us with 6; the O projection 2560 x 2560 at 512 tokens 15.6 us with 2
+    // slices, 14.8 with 3; 216 tiles gain nothing from 2).  Tiled copies,
+    // whose chunks cost less: only rows of 16+ chunks, in 2..4 slices
+    // (config-5 shapes: the down projection, 27 chunks, at 128 / 256 / 512
+    // tokens 23.9 / 24.5 / 26.1 us unsplit, 14.9 in 4 slices / 16.9 in 3 /
+    // 21.7 in 3, 17.4 in 8 at 128; QKV and O, 10 chunks, no faster split:
+    // QKV at 256 tokens 13.5 us unsplit, 15.4 in 3 slices, O at 512 14.6
+    // against 15.4).  Split 128- and 256-row tiles lose (the last slice to
+    // arrive reads every other slice's 64 KB of partials).
     const uint32_t ntile = nlg_blocks(a.out, tile) * ty, nch = a.cols / TG_KC;
     uint32_t ks = 1;
-    if (a.allow_split && tile == 64 && ntile < 192 && nch >= 8) {
+    if (a.allow_split && tile == 64 && ntile < 192 && nch >= (wt ? 16u : 8u)) {
       ks = (384 + ntile - 1) / ntile;
-      if (ks > nch / 3) ks = nch / 3;
-      if (ks > 8) ks = 8;
+      if (wt) {
+        if (ks < 2) ks = 2;
+        if (ks > 4) ks = 4;
+      } else {
+        if (ks > nch / 3) ks = nch / 3;
+        if (ks > 8) ks = 8;
+      }
     }
     if (ks > 1) {
       const uint32_t nthr = tile == 256 ? 512 : 256, nr = tile == 256 ? 64 : (tile == 128 ? 64 : 32);
