@@ -276,7 +276,18 @@ __device__ __forceinline__ void tg_store(const GemmArgs &a, int lane, uint32_t r
 // arrays stay in registers) of PH chunks: cols <= 256 * PH * NPH.  The
 // epilogue's operands (gamma, the residual, RoPE entries) are fetched
 // before the first phase, not after the last.
-template <int MB, int NPH, int PH, int EPI>
+// With TILED, a.w2 is the registered tiled copy (k_tgemm_l): lane (lg, lr)'s
+// 16 bytes of chunk c (words 4 lg .. 4 lg + 3 of its row, the row layout's
+// wrow[4 c + lg]) are unit 128 c + 64 (lg % 2) + 32 (lg / 2) + row % 32 of its
+// 32-row block's tiles, so a load instruction reads four 256-byte runs.
+__device__ __forceinline__ const uint4 *tg_wbase(const GemmArgs &a, uint32_t rowc, int lg, bool tiled) {
+  if (tiled)
+    return (const uint4 *)a.w2 + (size_t)(rowc / 32) * (a.cols / TG_KC) * 128 + 64 * (lg & 1) + 32 * (lg >> 1) +
+           rowc % 32;
+  return (const uint4 *)(a.w2 + (size_t)rowc * a.wng) + lg;
+}
+
+template <int MB, int NPH, int PH, int EPI, bool TILED = false>
 __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
   constexpr int MT = 16 * MB;
   constexpr int PITCH = PH * TG_KC + 16;  // LDS row pitch in bytes (staggers the banks)
@@ -291,7 +302,8 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
   const uint32_t rowc = row < a.out ? row : a.out - 1;
   const uint32_t tok0 = blockIdx.y * MT;
   const uint32_t nchunks = a.cols / TG_KC;
-  const uint4 *wrow = (const uint4 *)(a.w2 + (size_t)rowc * a.wng);
+  const uint4 *wrow = tg_wbase(a, rowc, lg, TILED);
+  constexpr uint32_t WCS = TILED ? 128 : 4;  // uint4s from one chunk to the next
   // activation staging: piece p = threadIdx.x + 256 i is token p / SL,
   // 16-byte slot p % SL of the phase's 256 PH columns
   constexpr int SL = PH * TG_KC / 16;          // slots per token row
@@ -326,7 +338,7 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < PH; i++) {
       const uint32_t cc = c0 + i < nchunks ? c0 + i : nchunks - 1;
-      const uint4 u = wrow[4 * cc + lg];
+      const uint4 u = wrow[WCS * cc];
       // chunks past the end contribute zero
       const uint32_t keep = c0 + i < nchunks ? 0xffffffffu : 0u;
       wv[4 * i + 0] = u.x & keep;
@@ -436,7 +448,7 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
 #define TK_D 3  // activation chunks in flight
 #define TK_PITCH 68  // LDS row pitch (words) of a wave's activation tile: 256 bytes + 16
 
-template <int MB, int EPI, int PM>
+template <int MB, int EPI, int PM, bool TILED = false>
 __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
   constexpr int NA = 4 * MB;  // 16-byte activation pieces per lane and chunk
   constexpr int D = PM < TK_D ? PM : TK_D;
@@ -455,7 +467,8 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
   const uint32_t nchunks = a.cols / TG_KC;
   const uint32_t per = (nchunks + 3) / 4, cb = w * per;
   const uint32_t ce = min(cb + per, nchunks);
-  const uint4 *wrow = (const uint4 *)(a.w2 + (size_t)rowc * a.wng) + lg;
+  const uint4 *wrow = tg_wbase(a, rowc, lg, TILED);
+  constexpr uint32_t WCS = TILED ? 128 : 4;  // uint4s from one chunk to the next
   // Activations are fetched whole rows at a time -- load u of block m brings
   // token 16 m + 4 u + lane / 16, bytes 16 (lane % 16) of a chunk, so each
   // instruction reads four full 256-byte row chunks -- and reach the matrix
@@ -476,7 +489,7 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
 #pragma unroll
   for (int j = 0; j < PM; j++) {
     const uint32_t c = cb + j;
-    wq[j] = nlg_ld_stream(&wrow[4 * (c < ce ? c : nchunks - 1)]);
+    wq[j] = nlg_ld_stream(&wrow[WCS * (c < ce ? c : nchunks - 1)]);
   }
   // 2. the first D chunks' activations, whole rows per load (see above)
   avec av[PM];
@@ -867,11 +880,11 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   if (a.cols % TG_KC || !a.cols) return nlg_fail("ternary GEMM: cols must be a multiple of %d", TG_KC);
   if (((uintptr_t)a.w2 & 15) || ((uintptr_t)a.xq & 15)) return nlg_fail("ternary GEMM: 16-byte alignment");
   a.wng = a.cols / 16;
+  // a registered tiled copy of the weights (nlg_ternary_tiled_register)
+  // replaces the row layout: the same words, in load order
+  const uint32_t *wt = epi != NLG_EPI_ARGMAX ? nlg_tiled_find(a.w2, a.out, a.cols) : nullptr;
+  if (wt) a.w2 = wt;
   if (a.seq >= 128 && epi != NLG_EPI_ARGMAX) {
-    // a registered tiled copy of the weights (nlg_ternary_tiled_register)
-    // replaces the row layout: the same words, in load order
-    const uint32_t *wt = nlg_tiled_find(a.w2, a.out, a.cols);
-    if (wt) a.w2 = wt;
     // Row tile: 256 rows once that grid has 128 workgroups (one 8-wave
     // workgroup per CU: fewer, larger tiles re-read the activations less),
     // else 128 rows once that grid has 192, else 64.  Measured at 512 and
@@ -964,13 +977,18 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
     // weight chunks per wave: the smallest instantiated count >= ceil(chunks / 4)
     const uint32_t per = (a.cols / TG_KC + 3) / 4;
     const int pm = per <= 2 ? 2 : per <= 3 ? 3 : per <= 4 ? 4 : per <= 7 ? 7 : 16;
+#define TKT(M, E, T)                                                                      \
+  do {                                                                                    \
+    if (pm == 2) hipLaunchKernelGGL((k_tgemm_k<M, E, 2, T>), grid, blk, 0, st, a);        \
+    else if (pm == 3) hipLaunchKernelGGL((k_tgemm_k<M, E, 3, T>), grid, blk, 0, st, a);   \
+    else if (pm == 4) hipLaunchKernelGGL((k_tgemm_k<M, E, 4, T>), grid, blk, 0, st, a);   \
+    else if (pm == 7) hipLaunchKernelGGL((k_tgemm_k<M, E, 7, T>), grid, blk, 0, st, a);   \
+    else hipLaunchKernelGGL((k_tgemm_k<M, E, 16, T>), grid, blk, 0, st, a);               \
+  } while (0)
 #define TKP(M, E)                                                                         \
   do {                                                                                    \
-    if (pm == 2) hipLaunchKernelGGL((k_tgemm_k<M, E, 2>), grid, blk, 0, st, a);           \
-    else if (pm == 3) hipLaunchKernelGGL((k_tgemm_k<M, E, 3>), grid, blk, 0, st, a);      \
-    else if (pm == 4) hipLaunchKernelGGL((k_tgemm_k<M, E, 4>), grid, blk, 0, st, a);      \
-    else if (pm == 7) hipLaunchKernelGGL((k_tgemm_k<M, E, 7>), grid, blk, 0, st, a);      \
-    else hipLaunchKernelGGL((k_tgemm_k<M, E, 16>), grid, blk, 0, st, a);                  \
+    if (wt) TKT(M, E, true);                                                              \
+    else TKT(M, E, false);                                                                \
   } while (0)
 #define TKG(E)                                                                            \
   do {                                                                                    \
@@ -986,6 +1004,7 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
     }
 #undef TKG
 #undef TKP
+#undef TKT
     NLG_LAUNCHED("ternary GEMM (int8 MFMA, split columns)");
     return NLG_OK;
   }
@@ -999,13 +1018,18 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   const bool ph10 = nch > TG_PH && nch <= 10 && (uint64_t)grid.x * grid.y <= 256;
   const size_t lds = (size_t)MT * (ph10 ? 10 * TG_KC + 16 : TG_PITCH);
   const int nph = a.cols <= 2048 ? 1 : (a.cols <= 4096 ? 2 : (a.cols <= 8192 ? 4 : 8));
+#define TGT(M, E, T)                                                                              \
+  do {                                                                                            \
+    if (ph10) hipLaunchKernelGGL((k_tgemm<M, 1, 10, E, T>), grid, blk, lds, st, a);               \
+    else if (nph == 1) hipLaunchKernelGGL((k_tgemm<M, 1, TG_PH, E, T>), grid, blk, lds, st, a);   \
+    else if (nph == 2) hipLaunchKernelGGL((k_tgemm<M, 2, TG_PH, E, T>), grid, blk, lds, st, a);   \
+    else if (nph == 4) hipLaunchKernelGGL((k_tgemm<M, 4, TG_PH, E, T>), grid, blk, lds, st, a);   \
+    else hipLaunchKernelGGL((k_tgemm<M, 8, TG_PH, E, T>), grid, blk, lds, st, a);                 \
+  } while (0)
 #define TGP(M, E)                                                                                 \
   do {                                                                                            \
-    if (ph10) hipLaunchKernelGGL((k_tgemm<M, 1, 10, E>), grid, blk, lds, st, a);                  \
-    else if (nph == 1) hipLaunchKernelGGL((k_tgemm<M, 1, TG_PH, E>), grid, blk, lds, st, a);      \
-    else if (nph == 2) hipLaunchKernelGGL((k_tgemm<M, 2, TG_PH, E>), grid, blk, lds, st, a);      \
-    else if (nph == 4) hipLaunchKernelGGL((k_tgemm<M, 4, TG_PH, E>), grid, blk, lds, st, a);      \
-    else hipLaunchKernelGGL((k_tgemm<M, 8, TG_PH, E>), grid, blk, lds, st, a);                    \
+    if (wt) TGT(M, E, true);                                                                      \
+    else TGT(M, E, false);                                                                        \
   } while (0)
 #define TG(E)                                                                                     \
   do {                                                                                            \
@@ -1017,11 +1041,15 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
     case NLG_EPI_RESID: TG(NLG_EPI_RESID); break;
     case NLG_EPI_SWIGLU: TG(NLG_EPI_SWIGLU); break;
     case NLG_EPI_QKV: TG(NLG_EPI_QKV); break;
-    case NLG_EPI_ARGMAX: TG(NLG_EPI_ARGMAX); break;
+    case NLG_EPI_ARGMAX:  // never a tiled copy (the lookup skips ARGMAX)
+      if (MB == 1) TGT(1, NLG_EPI_ARGMAX, false);
+      else TGT(2, NLG_EPI_ARGMAX, false);
+      break;
     default: return nlg_fail("ternary GEMM: unknown epilogue %d", epi);
   }
 #undef TG
 #undef TGP
+#undef TGT
   NLG_LAUNCHED("ternary GEMM (int8 MFMA)");
   return NLG_OK;
 }

@@ -254,3 +254,29 @@ def test_tiled_copy_registration():
     nlgpu.ternary_tiled_unregister(dw)  # no copy: a no-op
     with pytest.raises(nlgpu.NlgError, match="multiple of 256"):
         nlgpu.ternary_tiled_register(dw, out, 1000)
+
+
+# 8..127 tokens: the 16x16x64 GEMM with 64-row workgroups (many rows) or the
+# 16-row column-split form (few rows), each on the row layout and on a tiled copy
+SMALL = [(8, 13824, 2560), (32, 13824, 2560), (100, 6912, 1024), (32, 2560, 6912), (16, 3840, 2560),
+         (32, 2560, 2560), (77, 1000, 512)]
+
+
+@pytest.mark.parametrize("seq,out,cols", SMALL)
+def test_small_batch_tiled_copy(seq, out, cols):
+    print(f"[gpu] small batch seq={seq} out={out} cols={cols}", flush=True)
+    x, res = nlgpu.normal(cols + seq + 1, seq * cols), nlgpu.normal(out + seq + 1, seq * out)
+    w2, beta = weights(cols + out + 1, out, cols, per_row=True)
+    bias = (nlgpu.normal(out + 2, out) * f32(0.1)).astype(f32)
+    dx, dw, dbias, db = nlgpu.to_device(x), nlgpu.to_device(w2), nlgpu.to_device(bias), nlgpu.to_device(beta)
+    dres, dy = nlgpu.to_device(res), nlgpu.DeviceArray(seq * out * 4)
+
+    def run():
+        dy.zero()
+        nlgpu.ternary_linear_residual(dx, dw, dbias, db, dres, dy, seq, out, cols, beta_per_row=True)
+        return dy.download(f32, seq * out)
+
+    got = run()
+    want = (res + ref.linear(x, w2, beta, seq, out, cols, bias=bias, per_row=True)).astype(f32)
+    same_bits(got, want, "residual")
+    same_bits(with_tiled_copy(dw, out, cols, run), got, "tiled copy")
