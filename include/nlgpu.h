@@ -407,14 +407,14 @@ int nlg_repack_i8_to_2bit(const uint32_t *wp, uint32_t out, uint32_t cols, uint3
 int nlg_repack_packed_to_2bit(const float *wpk, uint32_t out, uint32_t cols, uint32_t pk, uint32_t fcount,
                               uint32_t *w2, uint32_t *nbad, void *stream);
 
-/* Tiled copies for prompts.  No counterpart in the reference, which reads
- * the row layout of ternary-rows (kernels.el:700-746) at every batch size;
- * for callers that run the batched linears above at 128 or more tokens.
+/* Tiled weight copies.  No counterpart in the reference, which reads the
+ * row layout of ternary-rows (kernels.el:700-746) at every batch size; for
+ * callers that run the batched linears above (8 or more tokens).
  * Registering 2-bit weights w2 [rows x cols/16] (cols a multiple of 256,
  * 16-byte aligned) makes a library-owned copy of them in the matrix-core
  * GEMM's load order (the same words; each wave then loads 1 KiB runs
  * instead of 32-byte pieces of 32 rows), which every linear given this w2
- * pointer with the same rows and cols at 128+ tokens reads instead.  The
+ * pointer with the same rows and cols at 8+ tokens reads instead.  The
  * copy is taken when this is called (it waits for `stream`): register
  * again after changing the weights, and unregister before freeing w2.
  * Results are bit-identical to the row layout's.  Costs rows (rounded up

@@ -393,7 +393,7 @@ extern "C" int nlg_stack_create(const nlg_stack_config *cfg, nlg_stack **out) {
   s->c = c;
   s->nq = c.heads * c.head_dim;
   s->nkv = c.kv_heads * c.head_dim;
-  if (stack_alloc(s) || stack_generate(s)) {
+  if (stack_alloc(s) || stack_generate(s) || (c.batch >= NLG_BATCHED_MIN && stack_tile(s))) {
     nlg_stack_destroy(s);
     return NLG_ERR;
   }
@@ -418,6 +418,23 @@ static int stack_attention(nlg_stack *s, Layer &y) {
 }
 
 static int stack_head(nlg_stack *s);
+
+// The matrix-core GEMMs (8+ rows: prompts, and every step at batch >= 8)
+// read tiled copies of the layer weights: one more copy of them, made once.
+static int stack_tile(nlg_stack *s) {
+  if (s->tiled) return NLG_OK;
+  const nlg_stack_config &c = s->c;
+  const uint32_t d = c.d_model, f = c.d_ff, qkv = s->nq + 2 * s->nkv;
+  s->tiled = true;
+  for (Layer &y : s->L) {
+    if ((d % 256 == 0 && (nlg_ternary_tiled_register(y.wqkv, qkv, d, nullptr) ||
+                          nlg_ternary_tiled_register(y.wgu, 2 * f, d, nullptr))) ||
+        (s->nq % 256 == 0 && nlg_ternary_tiled_register(y.wo, d, s->nq, nullptr)) ||
+        (f % 256 == 0 && nlg_ternary_tiled_register(y.wd, d, f, nullptr)))
+      return NLG_ERR;
+  }
+  return NLG_OK;
+}
 static int upload_prompt(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt, bool all_hist);
 
 // One token step for the whole batch, enqueued on the library stream.
@@ -533,19 +550,7 @@ extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t 
     if (!s->px || !s->pq || !s->ph || !s->pattn_ws) return NLG_ERR;
     s->pcap = T;
   }
-  if (T >= 128 && !s->tiled) {
-    // the matrix-core GEMMs of 128+ rows read tiled copies of the layer
-    // weights (one more copy of them, made once)
-    const uint32_t qkv = s->nq + 2 * s->nkv;
-    s->tiled = true;
-    for (Layer &y : s->L) {
-      if ((d % 256 == 0 && (nlg_ternary_tiled_register(y.wqkv, qkv, d, nullptr) ||
-                            nlg_ternary_tiled_register(y.wgu, 2 * f, d, nullptr))) ||
-          (s->nq % 256 == 0 && nlg_ternary_tiled_register(y.wo, d, s->nq, nullptr)) ||
-          (f % 256 == 0 && nlg_ternary_tiled_register(y.wd, d, f, nullptr)))
-        return NLG_ERR;
-    }
-  }
+  if (T >= NLG_BATCHED_MIN && stack_tile(s)) return NLG_ERR;
   hipLaunchKernelGGL(k_embed_prompt, dim3(nlg_blocks(d, 256), T), dim3(256), 0, st, s->emb, s->prompt,
                      c.max_seq, P, s->px, d);
   NLG_LAUNCHED("embed prompt");
