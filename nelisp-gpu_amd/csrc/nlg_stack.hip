@@ -267,6 +267,7 @@ extern "C" void nlg_stack_destroy(nlg_stack *s) {
   if (s->tiled)
     for (Layer &y : s->L)
       for (const uint32_t *w : {y.wqkv, y.wo, y.wgu, y.wd}) (void)nlg_ternary_tiled_unregister(w);
+  if (s->tiled) (void)nlg_ternary_tiled_unregister(s->wlm);
   for (void *p : s->allocs) nlg_free(p);
   for (void *p : {(void *)s->px, (void *)s->pq, (void *)s->ph, s->pattn_ws})
     if (p) nlg_free(p);
@@ -420,7 +421,8 @@ static int stack_attention(nlg_stack *s, Layer &y) {
 static int stack_head(nlg_stack *s);
 
 // The matrix-core GEMMs (8+ rows: prompts, and every step at batch >= 8)
-// read tiled copies of the layer weights: one more copy of them, made once.
+// read tiled copies of the layer weights, and of the LM head when it runs
+// on 8+ rows (batch >= 8): one more copy of them, made once.
 static int stack_tile(nlg_stack *s) {
   if (s->tiled) return NLG_OK;
   const nlg_stack_config &c = s->c;
@@ -433,6 +435,8 @@ static int stack_tile(nlg_stack *s) {
         (f % 256 == 0 && nlg_ternary_tiled_register(y.wd, d, f, nullptr)))
       return NLG_ERR;
   }
+  if (c.batch >= NLG_BATCHED_MIN && d % 256 == 0 && nlg_ternary_tiled_register(s->wlm, c.vocab, d, nullptr))
+    return NLG_ERR;
   return NLG_OK;
 }
 static int upload_prompt(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt, bool all_hist);

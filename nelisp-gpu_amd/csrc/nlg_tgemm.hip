@@ -882,7 +882,7 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   a.wng = a.cols / 16;
   // a registered tiled copy of the weights (nlg_ternary_tiled_register)
   // replaces the row layout: the same words, in load order
-  const uint32_t *wt = epi != NLG_EPI_ARGMAX ? nlg_tiled_find(a.w2, a.out, a.cols) : nullptr;
+  const uint32_t *wt = nlg_tiled_find(a.w2, a.out, a.cols);
   if (wt) a.w2 = wt;
   if (a.seq >= 128 && epi != NLG_EPI_ARGMAX) {
     // Row tile: 256 rows once that grid has 128 workgroups (one 8-wave
@@ -1041,10 +1041,7 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
     case NLG_EPI_RESID: TG(NLG_EPI_RESID); break;
     case NLG_EPI_SWIGLU: TG(NLG_EPI_SWIGLU); break;
     case NLG_EPI_QKV: TG(NLG_EPI_QKV); break;
-    case NLG_EPI_ARGMAX:  // never a tiled copy (the lookup skips ARGMAX)
-      if (MB == 1) TGT(1, NLG_EPI_ARGMAX, false);
-      else TGT(2, NLG_EPI_ARGMAX, false);
-      break;
+    case NLG_EPI_ARGMAX: TG(NLG_EPI_ARGMAX); break;
     default: return nlg_fail("ternary GEMM: unknown epilogue %d", epi);
   }
 #undef TG

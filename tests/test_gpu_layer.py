@@ -171,12 +171,21 @@ def test_lm_head_argmax(seq, vocab, cols, dup):
     beta = np.array([1.0 / np.sqrt(cols)], f32)
     dl, da = nlgpu.DeviceArray(seq * vocab * 4), nlgpu.DeviceArray(seq * 4)
     ws = nlgpu.DeviceArray(nlgpu.rms_ternary_argmax_workspace(seq, vocab))
-    nlgpu.rms_ternary_argmax(nlgpu.to_device(x), nlgpu.to_device(g), 1e-5, nlgpu.to_device(w2),
-                             nlgpu.to_device(beta), dl, da, seq, vocab, cols, ws)
+    dx, dg, dw, db = nlgpu.to_device(x), nlgpu.to_device(g), nlgpu.to_device(w2), nlgpu.to_device(beta)
+    nlgpu.rms_ternary_argmax(dx, dg, 1e-5, dw, db, dl, da, seq, vocab, cols, ws)
     want = ref.linear(ref.rms(x, g, 1e-5, seq, cols), w2, beta, seq, vocab, cols)
     got = dl.download(f32, seq * vocab)
     same_bits(got, want)
     assert np.array_equal(da.download(np.int32, seq), np.argmax(want.reshape(seq, vocab), axis=1))
+    if seq >= 8 and cols % 256 == 0:  # the batched form again, on a registered tiled copy
+        nlgpu.ternary_tiled_register(dw, vocab, cols)
+        try:
+            dl.zero()
+            nlgpu.rms_ternary_argmax(dx, dg, 1e-5, dw, db, dl, da, seq, vocab, cols, ws)
+        finally:
+            nlgpu.ternary_tiled_unregister(dw)
+        same_bits(dl.download(f32, seq * vocab), want)
+        assert np.array_equal(da.download(np.int32, seq), np.argmax(want.reshape(seq, vocab), axis=1))
 
 
 ATTN = [(1, 20, 5, 128, 768, [0, 1, 63, 64, 65, 200, 767]), (3, 8, 8, 64, 130, [0, 129, 77]),
