@@ -212,9 +212,14 @@ int nlg_attn_chunks(const float *q, const uint16_t *kc, const uint16_t *vc, cons
 // Causal attention of `rows` prompt rows (row r = sequence r / qper at
 // position pos[0] + r % qper) over the fp16 caches on the matrix cores;
 // ctx [rows][heads * head_dim] f32, normalised.
+// With xq, gamma and quantized given, a launch that splits the keys leaves
+// the merged context quantised for the output projection in xq ([rows x
+// heads*head_dim] int8 in matrix-core order) and gamma ([rows]) instead of
+// ctx, and sets *quantized; otherwise ctx is written as without them.
 int nlg_prefill_attn(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *pos, uint32_t rows,
                      uint32_t qper, uint32_t heads, uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
-                     float *ctx, hipStream_t st);
+                     float *ctx, hipStream_t st, uint8_t *xq = nullptr, float *gamma = nullptr,
+                     bool *quantized = nullptr);
 enum {
   NLG_EPI_STORE = 0,   // y = bias + (beta*gamma)*acc
   NLG_EPI_RESID = 1,   // y = res + that
@@ -266,6 +271,9 @@ int nlg_fused_launch(const FusedArgs &a, int pro, int epi, int rows_per_wave, hi
 #define NLG_BATCHED_MIN 8
 bool nlg_batched(uint32_t seq, uint32_t cols);
 int nlg_batched_launch(const FusedArgs &a, int pro, int epi, hipStream_t st);
+// Its GEMM alone, over activations already quantised into xq / gamma (as
+// k_act_q leaves them); f's x, gain and prologue fields are not used.
+int nlg_batched_gemm(const FusedArgs &f, const uint8_t *xq, const float *gamma, int epi, hipStream_t st);
 // (max, index) partials per token an ARGMAX launch of `out` rows writes.
 uint32_t nlg_argmax_parts(uint32_t seq, uint32_t cols, uint32_t out);
 // Grow-only device scratch owned by the library, one per stream (NULL on

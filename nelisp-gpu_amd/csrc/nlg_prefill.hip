@@ -24,6 +24,7 @@
 // instead of a correctly rounded expf.
 
 #include "nlg_internal.h"
+#include "nlg_quant.h"
 
 #include <math.h>
 
@@ -306,11 +307,84 @@ __global__ __launch_bounds__(256) void k_prefill_merge(PrefillArgs a, uint32_t h
   *(float4 *)(a.ctx + (size_t)row * a.nq + (size_t)head * hd + 4 * d4) = out;
 }
 
+// The same merge for whole rows (one workgroup per row), then the per-token
+// quantisation of k_act_q (amax, gamma = amax / 127, the exact quantiser,
+// matrix-core byte order across each quad) straight into the int8 rows the
+// output projection's GEMM reads: the merged context never goes to memory.
+// Thread t takes float4s t + 256 j of the row; the merge runs in
+// k_prefill_merge's operation order and the quantisation in k_act_q's, so
+// the int8 rows and gammas are the ones the two launches would leave.
+template <int J>
+__global__ __launch_bounds__(256) void k_prefill_merge_q(PrefillArgs a, uint32_t hd, uint32_t nrows, uint8_t *xq,
+                                                         float *gamma) {
+  __shared__ float red[4];
+  const uint32_t row = blockIdx.x, nf4 = a.nq >> 2, per = hd / 4;
+  const uint32_t qb = (row % a.qper) / PA_QB;
+  const int32_t pos0 = a.pos[0];
+  const uint32_t ilast = min(qb * PA_QB + PA_QB - 1, a.qper - 1);
+  const int32_t plast = min(pos0 + (int32_t)ilast, (int32_t)a.max_seq - 1);
+  const uint32_t nkb_all = plast < 0 ? 0u : (uint32_t)plast / PA_KB + 1;
+  const uint32_t np = nkb_all ? (nkb_all + a.kps - 1) / a.kps : 1;
+  float4 v[J];
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const uint32_t f0 = threadIdx.x + 256u * j, f = f0 < nf4 ? f0 : nf4 - 1;
+    const uint32_t head = f / per, d4 = f % per;
+    float mm = -1.0e30f;
+    for (uint32_t p = 0; p < np; p++) {
+      const float mp = a.part_ml[(((size_t)p * nrows + row) * a.heads + head) * 2];
+      mm = mp > mm ? mp : mm;
+    }
+    float ll = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t p = 0; p < np; p++) {
+      const size_t pr = (size_t)p * nrows + row;
+      const float2 ml = *(const float2 *)(a.part_ml + (pr * a.heads + head) * 2);
+      const float sc = nlg_exp2(ml.x - mm);
+      ll = fmaf(ml.y, sc, ll);
+      const float4 x = *(const float4 *)(a.part_o + pr * a.nq + (size_t)head * hd + 4 * d4);
+      acc.x = fmaf(x.x, sc, acc.x);
+      acc.y = fmaf(x.y, sc, acc.y);
+      acc.z = fmaf(x.z, sc, acc.z);
+      acc.w = fmaf(x.w, sc, acc.w);
+    }
+    v[j] = ll > 0.0f && f0 < nf4 ? make_float4(acc.x / ll, acc.y / ll, acc.z / ll, acc.w / ll)
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    float t;
+    t = dsl_abs(v[j].x); amax = t > amax ? t : amax;
+    t = dsl_abs(v[j].y); amax = t > amax ? t : amax;
+    t = dsl_abs(v[j].z); amax = t > amax ? t : amax;
+    t = dsl_abs(v[j].w); amax = t > amax ? t : amax;
+  }
+  amax = nlg_block_max_f32<4, true>(amax, red);
+  const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
+  const float ginv = 1.0f / g;
+  const bool fast = g > 0.0f && ginv < INFINITY;
+  if (threadIdx.x == 0) gamma[row] = g;
+  const uint32_t qi = threadIdx.x & 3u;
+  const uint32_t sel_lo = 0x0c0c0000u | ((4u + qi) << 8) | qi, sel_hi = 0x00000c0cu | ((4u + qi) << 24) | (qi << 16);
+  uint32_t *dst = (uint32_t *)(xq + (size_t)row * a.nq);
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const uint32_t f = threadIdx.x + 256u * j;
+    const int n = (int)quant_word(v[j], g, ginv, fast);
+    const uint32_t n0 = (uint32_t)nlg_dpp<0x00>(n), n1 = (uint32_t)nlg_dpp<0x55>(n);
+    const uint32_t n2 = (uint32_t)nlg_dpp<0xAA>(n), n3 = (uint32_t)nlg_dpp<0xFF>(n);
+    const uint32_t y = __builtin_amdgcn_perm(n1, n0, sel_lo) | __builtin_amdgcn_perm(n3, n2, sel_hi);
+    if (f < nf4) dst[f] = y;
+  }
+}
+
 }  // namespace
 
 int nlg_prefill_attn(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *pos, uint32_t rows,
                      uint32_t qper, uint32_t heads, uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
-                     float *ctx, hipStream_t st) {
+                     float *ctx, hipStream_t st, uint8_t *xq, float *gamma, bool *quantized) {
+  if (quantized) *quantized = false;
   if (!rows) return NLG_OK;
   if (!q || !kc || !vc || !pos || !ctx) return nlg_fail("prefill attn: null pointer");
   if (head_dim != 64 && head_dim != 128) return nlg_fail("prefill attn: head_dim %u not 64 or 128", head_dim);
@@ -358,6 +432,17 @@ int nlg_prefill_attn(const float *q, const uint16_t *kc, const uint16_t *vc, con
       if (head_dim == 128) PAS(128); else PAS(64);
 #undef PAS
       NLG_LAUNCHED("prefill attention (fp16 KV, MFMA, split keys)");
+      const uint32_t jq = (a.nq / 4 + 255) / 256;  // float4s per thread of a whole row
+      if (xq && gamma && quantized && a.nq % 64 == 0 && jq <= 4) {
+        // merged and quantised per row for the output projection
+        if (jq <= 1) hipLaunchKernelGGL(k_prefill_merge_q<1>, dim3(rows), dim3(256), 0, st, a, head_dim, rows, xq, gamma);
+        else if (jq <= 2) hipLaunchKernelGGL(k_prefill_merge_q<2>, dim3(rows), dim3(256), 0, st, a, head_dim, rows, xq, gamma);
+        else if (jq <= 3) hipLaunchKernelGGL(k_prefill_merge_q<3>, dim3(rows), dim3(256), 0, st, a, head_dim, rows, xq, gamma);
+        else hipLaunchKernelGGL(k_prefill_merge_q<4>, dim3(rows), dim3(256), 0, st, a, head_dim, rows, xq, gamma);
+        NLG_LAUNCHED("prefill attention merge + quantisation");
+        *quantized = true;
+        return NLG_OK;
+      }
       const uint64_t nthr = (uint64_t)rows * heads * (head_dim / 4);
       hipLaunchKernelGGL(k_prefill_merge, dim3((uint32_t)((nthr + 255) / 256)), dim3(256), 0, st, a, head_dim,
                          rows);

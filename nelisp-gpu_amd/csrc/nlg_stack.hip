@@ -372,6 +372,8 @@ static int stack_generate(nlg_stack *s) {
   return NLG_OK;
 }
 
+static int stack_tile(nlg_stack *s);
+
 extern "C" int nlg_stack_create(const nlg_stack_config *cfg, nlg_stack **out) {
   if (!cfg || !out) return nlg_fail("stack: null argument");
   *out = nullptr;
@@ -567,13 +569,21 @@ extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t 
     q.ystride = s->nq; q.hd = c.head_dim; q.kvheads = c.kv_heads; q.max_seq = c.max_seq; q.co = s->co;
     q.si = s->si; q.pos = s->pos; q.kc = y.kc; q.vc = y.vc; q.qper = P;
     if (nlg_fused_launch(q, NLG_PRO_RMS, NLG_EPI_QKV, 0, st)) return NLG_ERR;
+    // a split prompt attention leaves the merged context quantised for the
+    // output projection (xq, gamma in the batched linears' scratch)
+    uint8_t *oq = T >= NLG_BATCHED_MIN && s->nq % 256 == 0
+                      ? (uint8_t *)nlg_scratch(nlg_batched_scratch_bytes(T, s->nq), st)
+                      : nullptr;
+    float *og = oq ? (float *)(oq + ((size_t)T * s->nq + 255) / 256 * 256) : nullptr;
+    bool quantized = false;
     if (nlg_prefill_attn(s->pq, y.kc, y.vc, s->pos, T, P, c.heads, c.kv_heads, c.head_dim, c.max_seq, pctx,
-                         st))
+                         st, oq, og, &quantized))
       return NLG_ERR;
     FusedArgs o{};
     o.x = pctx; o.w2 = y.wo; o.beta = y.bo; o.seq = T; o.out = d; o.cols = s->nq;
     o.y = s->px; o.ystride = d; o.res = s->px; o.rstride = d;
-    if (nlg_fused_launch(o, NLG_PRO_NONE, NLG_EPI_RESID, 0, st)) return NLG_ERR;
+    if (quantized ? nlg_batched_gemm(o, oq, og, NLG_EPI_RESID, st) : nlg_fused_launch(o, NLG_PRO_NONE, NLG_EPI_RESID, 0, st))
+      return NLG_ERR;
     FusedArgs g{};
     g.x = s->px; g.gain = y.gffn; g.eps = c.rms_eps; g.w2 = y.wgu; g.beta = y.bgu; g.beta_per_row = 1;
     g.seq = T; g.out = 2 * f; g.cols = d; g.y = s->ph; g.ystride = f;

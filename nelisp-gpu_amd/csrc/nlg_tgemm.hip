@@ -1080,6 +1080,10 @@ int nlg_batched_launch(const FusedArgs &f, int pro, int epi, hipStream_t st) {
   if (nlg_act_q_launch(f.x, f.gain, f.eps, f.attn_mz, f.attn_nc, f.hd, pro, xq, gamma, f.seq, f.cols, st))
     return NLG_ERR;
   if (f.gamma_out) NLG_HIP(hipMemcpyAsync(f.gamma_out, gamma, (size_t)f.seq * 4, hipMemcpyDeviceToDevice, st));
+  return nlg_batched_gemm(f, xq, gamma, epi, st);
+}
+
+int nlg_batched_gemm(const FusedArgs &f, const uint8_t *xq, const float *gamma, int epi, hipStream_t st) {
   GemmArgs g{};
   g.xq = xq; g.gamma = gamma; g.w2 = f.w2; g.bias = f.bias; g.beta = f.beta; g.beta_per_row = f.beta_per_row;
   g.seq = f.seq; g.out = f.out; g.cols = f.cols; g.y = f.y; g.ystride = f.ystride; g.res = f.res;
