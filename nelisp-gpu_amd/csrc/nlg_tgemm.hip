@@ -628,10 +628,16 @@ __device__ __forceinline__ bool tl_split_meet(const GemmArgs &a, v16i (&acc)[2][
 // The epilogue of k_tgemm_l: acc[mt][nt] of lane (li, lg) of the
 // wave at token half wm, rows rw[nt] (clamped rc[nt]), with bias bo and
 // beta be per row block and the workgroup's 128 gammas in s_gm.
+//
+// QKV: s_tp holds each of the workgroup's 128 tokens' cache position (-1
+// where it is past max_seq) and s_tb its cache row's element offset
+// ((sequence x kvheads x max_seq + position) x head_dim), computed once per
+// workgroup; a row block's section, head and dimension once per block.
 template <int NB, int EPI>
 __device__ __forceinline__ void tl_epilogue(const GemmArgs &a, const v16i (&acc)[2][NB], const uint32_t (&rw)[NB],
                                             const uint32_t (&rc)[NB], const float (&bo)[NB], const float (&be)[NB],
-                                            const float *s_gm, int lane, int wm, int lg, uint32_t tok0) {
+                                            const float *s_gm, int lane, int wm, int lg, uint32_t tok0,
+                                            const int32_t *s_tp, const uint64_t *s_tb) {
   // acc[mt][nt] register r is token tok0 + 64 wm + 32 mt + (r%4) + 8 (r/4) + 4 lg,
   // row rw[nt].  gamma comes from LDS; the residual and RoPE
   // operands of a (token block, row block) are all fetched before its first
@@ -665,6 +671,50 @@ __device__ __forceinline__ void tl_epilogue(const GemmArgs &a, const v16i (&acc)
           if (lr && tk < a.seq) {
             const float sg = nlg_silu_gate(g);
             a.y[(size_t)tk * a.ystride + (rw[nt] >> 1)] = (g * sg) * u;
+          }
+        }
+      }
+    }
+    return;
+  }
+  if (EPI == NLG_EPI_QKV) {
+    const uint32_t half = a.hd >> 1;
+    const bool odd = lane & 1;
+#pragma unroll
+    for (int nt = 0; nt < NB; nt++) {
+      const uint32_t row = rw[nt], rcn = rc[nt];
+      const uint32_t sec = rcn < a.nq ? rcn : (rcn < a.nq + a.nkv ? rcn - a.nq : rcn - a.nq - a.nkv);
+      const uint32_t dd = sec % a.hd, kh = sec / a.hd, cd = dd >> 1;
+      const bool isq = row < a.nq, isk = row < a.nq + a.nkv;
+      uint16_t *const cache = (isk ? a.kc : a.vc) + ((size_t)kh * a.max_seq * a.hd + dd);
+#pragma unroll
+      for (int mt = 0; mt < 2; mt++) {
+        float cs[16], sn[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int32_t p = s_tp[64 * wm + 32 * mt + (r % 4) + 8 * (r / 4) + 4 * lg];
+          const uint32_t ci = (p >= 0 ? (uint32_t)p : 0u) * half + cd;
+          cs[r] = a.co[ci];
+          sn[r] = a.si[ci];
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const uint32_t t = 64 * wm + 32 * mt + (r % 4) + 8 * (r / 4) + 4 * lg, tk = tok0 + t;
+          // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
+          const float val =
+              __fadd_rn(bo[nt], __fmul_rn(__fmul_rn(be[nt], s_gm[t]), (float)(acc[mt][nt][r] >> 6)));
+          // decode-rope on the (row, row ^ 1) pair: C[i0] = a0*cc - a1*ss; C[i1] = a0*ss + a1*cc
+          const float pv = __int_as_float(nlg_dpp<0xB1>(__float_as_int(val)));
+          const float a0 = odd ? pv : val, a1 = odd ? val : pv;
+          const float rot = odd ? __fadd_rn(__fmul_rn(a0, sn[r]), __fmul_rn(a1, cs[r]))
+                                : __fsub_rn(__fmul_rn(a0, cs[r]), __fmul_rn(a1, sn[r]));
+          if (row < a.out && tk < a.seq) {
+            const int32_t p = s_tp[t];
+            if (isq) {
+              a.y[(size_t)tk * a.ystride + row] = rot;
+            } else if (p >= 0) {
+              cache[s_tb[t]] = __builtin_bit_cast(uint16_t, (_Float16)(isk ? rot : val));
+            }
           }
         }
       }
@@ -784,6 +834,8 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   // gamma of the workgroup's 128 tokens, for the epilogue (to LDS below,
   // ordered before the epilogue by the main loop's barriers)
   __shared__ float s_gm[128];
+  __shared__ int32_t s_tp[EPI == NLG_EPI_QKV ? 128 : 1];
+  __shared__ uint64_t s_tb[EPI == NLG_EPI_QKV ? 128 : 1];
   const float gm_t = a.gamma[tok0 + (threadIdx.x & 127u) < a.seq ? tok0 + (threadIdx.x & 127u) : a.seq - 1];
   TL_LOADW(c1, wB);
   float bo[NB], be[NB];
@@ -794,6 +846,16 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   }
   TL_STOREA(cfirst & 1, aX);
   if (threadIdx.x < 128) s_gm[threadIdx.x] = gm_t;
+  if (EPI == NLG_EPI_QKV && threadIdx.x < 128) {
+    // token t's cache position (decode rows: pos[0]; prompt rows: pos[0] +
+    // t % qper) and sequence, for the epilogue
+    const uint32_t tkc = tok0 + threadIdx.x < a.seq ? tok0 + threadIdx.x : a.seq - 1;
+    const int32_t pr = nlg_ld_uniform_i32(a.pos) + (a.qper ? (int32_t)(tkc % a.qper) : 0);
+    const bool ok = pr >= 0 && (uint32_t)pr < a.max_seq;
+    const uint32_t sq = a.qper ? tkc / a.qper : tkc;
+    s_tp[threadIdx.x] = ok ? pr : -1;
+    s_tb[threadIdx.x] = ((uint64_t)sq * a.kvheads * a.max_seq + (ok ? (uint32_t)pr : 0u)) * a.hd;
+  }
   v16i acc[2][NB];  // [token block][row block]
 #pragma unroll
   for (int mt = 0; mt < 2; mt++)
@@ -847,7 +909,7 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
     __shared__ uint32_t s_last;
     if (!tl_split_meet<NB>(a, acc, &s_last)) return;
   }
-  tl_epilogue<NB, EPI>(a, acc, rw, rc, bo, be, s_gm, lane, wm, lg, tok0);
+  tl_epilogue<NB, EPI>(a, acc, rw, rc, bo, be, s_gm, lane, wm, lg, tok0, s_tp, s_tb);
 }
 
 // ------------------------------------------------------------ launchers
