@@ -390,6 +390,213 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   }
 }
 
+// The chunk pass on the matrix cores, for head_dim 128, 4 query heads per
+// kv head and 256-position chunks over contiguous caches: the same
+// workgroups, chunks and outputs as k_attn_part<128, 4, 8, MODE>.  Wave w
+// takes positions p0 + 32 w .. + 31 of its chunk for the 4 query heads, on
+// v_mfma_f32_16x16x32_f16 (layout, checked on gfx950: lane 16g + i holds
+// A[i][8g..8g+7] and B[8g..8g+7][i]; result r of lane l is C[4(l/16) + r][l % 16]):
+//  * S^T = K Q^T per 16-position block b: A = K (lane (g, i): position
+//    16b + i, dims 32s + 8g.. at step s), B = q as fp16 hi + lo halves
+//    (columns 0..3 the heads, the rest zero), so lane (g, j < 4) receives
+//    head j's scores of positions 16b + 4g + r.
+//  * Those 8 values of a lane are exactly what the B operand P^T of
+//    O^T = V^T P^T needs (k slot 8g + 4b + r <-> position 16b + 4g + r), as
+//    fp16 hi + lo halves: no exchange between lanes.
+//  * V^T in that slot order comes from a per-wave LDS tile: each lane loads
+//    4 consecutive positions x 8 dims (every load instruction reads 4 whole
+//    rows) and writes each dim's 4 values as one 8-byte run of its V^T row;
+//    lane (g, i) then reads its A operand (dim 16n + i, slots 8g..8g+7).
+// Scores and probabilities carry ~22 bits through the hi + lo halves; the
+// matrix cores sum in their own order.  The wave's (max, sum, context)
+// merge across the 8 waves as in k_attn_part (each wave's context goes to
+// its own V^T tile once the tile is read).  A VALU-only copy of the pass
+// spent most of its time on the ~1,100 instructions per wave of the dots,
+// reductions and conversions; here they are 32 matrix-core steps per wave.
+#define AMF_PITCH 36  // V^T tile row pitch in 16-bit elements (32 slots + 4: 8-byte aligned rows)
+
+template <bool NT>
+__global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs a) {
+  constexpr int HD = 128, G = 4, NW = ATTN_WAVES, PW = 32, CS = NW * PW;
+  typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+  typedef float v4f __attribute__((ext_vector_type(4)));
+  __shared__ float s_m[NW][G], s_z[NW][G];
+  // per wave: its V^T tile, then its context [G][HD] (f32)
+  __shared__ __align__(16) uint16_t s_vt[NW][HD * AMF_PITCH];
+  asm volatile("" ::"s"(a.q), "s"(a.kc), "s"(a.vc), "s"(a.pos), "s"(a.pctx), "s"(a.pmz), "s"(a.heads),
+               "s"(a.kvheads), "s"(a.max_seq), "s"(a.nchunk), "s"(a.coef));
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const uint32_t c = blockIdx.x, h0 = blockIdx.y * G, qr = blockIdx.z;
+  const uint32_t kvh = h0 / a.grp;
+  const uint32_t b = a.qper ? qr / a.qper : qr;  // its sequence
+  const size_t cb = (size_t)qr * a.nchunk + c;
+  float *pctx = a.pctx + cb * a.heads * HD + (size_t)h0 * HD;
+  float *pmz = a.pmz + (cb * a.heads + h0) * 2;
+  const uint32_t p0 = c * CS, pw = p0 + w * PW;
+  const size_t slot = (size_t)b * a.kvheads + kvh;
+  const uint16_t *kb = a.kc + slot * a.max_seq * HD;
+  const uint16_t *vb = a.vc + slot * a.max_seq * HD;
+  // q first (loads retire in issue order): lane (lg, li) takes head
+  // h0 + li (li < 4; the others zero), dims 32 s + 8 lg .. + 7
+  const float *qb = a.q + (size_t)qr * a.heads * HD + (size_t)(h0 + (li < G ? li : 0)) * HD + 8 * lg;
+  float4 qv[8];
+#pragma unroll
+  for (int s = 0; s < 4; s++) {
+    qv[2 * s] = *(const float4 *)(qb + 32 * s);
+    qv[2 * s + 1] = *(const float4 *)(qb + 32 * s + 4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // Rows past lim - 1 clamp to it.  Large caches (NT) read the position
+  // first so that rows past it are never fetched; small ones fetch the whole
+  // chunk while the position is in flight.
+  uint32_t lim = a.max_seq;
+  if (NT) {
+    const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(qr % a.qper) : 0);
+    lim = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
+  }
+  // K, A operand layout: lane (lg, li) position pw + 16 bb + li, dims 32 s + 8 lg
+  // (each row's four 64-byte runs come from four consecutive instructions).
+  // Large caches stream K and V non-temporally, as k_attn_part does: with
+  // plain loads the K rows evict what the step's linears re-read (measured
+  // at B = 32: the pass alone 14.05 -> 14.25 us, the decode step 1.773 ->
+  // 1.713 ms).
+  uint4 kr[2][4];
+#pragma unroll
+  for (int bb = 0; bb < 2; bb++) {
+    const uint32_t pp = pw + 16 * bb + li, pc = pp < lim ? pp : lim - 1;
+#pragma unroll
+    for (int s = 0; s < 4; s++) kr[bb][s] = kv_ld<NT>(kb + (size_t)pc * HD + 32 * s + 8 * lg);
+  }
+  // V, whole rows: lane (lg, li) positions pw + 16 u + 4 lg + r, dims 8 li .. + 7
+  uint4 vr[2][4];
+#pragma unroll
+  for (int u = 0; u < 2; u++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t pp = pw + 16 * u + 4 * lg + r, pc = pp < lim ? pp : lim - 1;
+      vr[u][r] = kv_ld<NT>(vb + (size_t)pc * HD + 8 * li);
+    }
+  const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(qr % a.qper) : 0);
+  const uint32_t len = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
+  if (p0 >= len) {  // block-uniform: a chunk past the position adds nothing
+    for (int i = threadIdx.x; i < G * HD; i += NW * 64) pctx[i] = 0.0f;
+    if (threadIdx.x < G) {
+      pmz[2 * threadIdx.x] = -1.0e30f;
+      pmz[2 * threadIdx.x + 1] = 0.0f;
+    }
+    return;
+  }
+  v8h qh[4], ql[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float x = li < G ? f4_at(qv[2 * s + e / 4], e % 4) : 0.0f;
+      const _Float16 h = (_Float16)x;
+      qh[s][e] = h;
+      ql[s][e] = (_Float16)(x - (float)h);
+    }
+  // scores: lane (lg, li < 4) gets head li at positions pw + 16 bb + 4 lg + r
+  v4f sc[2];
+#pragma unroll
+  for (int bb = 0; bb < 2; bb++) {
+    sc[bb] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const v8h kf = __builtin_bit_cast(v8h, kr[bb][s]);
+      sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[s], sc[bb], 0, 0, 0);
+      sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[s], sc[bb], 0, 0, 0);
+    }
+  }
+  float m = -1.0e30f;
+#pragma unroll
+  for (int bb = 0; bb < 2; bb++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t pp = pw + 16 * bb + 4 * lg + r;
+      sc[bb][r] = pp < len ? sc[bb][r] * a.coef : -INFINITY;  // (q.k / sqrt(hd)) * log2(e)
+      m = sc[bb][r] > m ? sc[bb][r] : m;
+    }
+  // the head's maximum over the wave: lanes li, li + 16, li + 32, li + 48
+  {
+    float o = __shfl_xor(m, 16);
+    m = o > m ? o : m;
+    o = __shfl_xor(m, 32);
+    m = o > m ? o : m;
+  }
+  float z = 0.0f;
+  v8h ph, pl;
+#pragma unroll
+  for (int bb = 0; bb < 2; bb++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float e = nlg_exp2(sc[bb][r] - m);
+      z = z + e;
+      const _Float16 h = (_Float16)e;
+      ph[4 * bb + r] = h;
+      pl[4 * bb + r] = (_Float16)(e - (float)h);
+    }
+  z = z + __shfl_xor(z, 16);
+  z = z + __shfl_xor(z, 32);
+  // V^T tile: dims 8 li + e, slots 8 lg + 4 u + r (one wave's LDS operations
+  // run in order, so the tile needs no barrier)
+  uint16_t *vt = s_vt[w];
+#pragma unroll
+  for (int u = 0; u < 2; u++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const int wd = e / 2, sh = 16 * (e & 1);
+      uint32_t hv[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t word = wd == 0 ? vr[u][r].x : wd == 1 ? vr[u][r].y : wd == 2 ? vr[u][r].z : vr[u][r].w;
+        hv[r] = (word >> sh) & 0xffffu;
+      }
+      *(uint2 *)&vt[(8 * li + e) * AMF_PITCH + 8 * lg + 4 * u] = make_uint2(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16));
+    }
+  // O^T = V^T P^T per 16-dim block n: lane (lg, li < 4) gets head li, dims 16 n + 4 lg + r
+  v4f o[8];
+#pragma unroll
+  for (int n = 0; n < 8; n++) {
+    const uint16_t *row = &vt[(16 * n + li) * AMF_PITCH + 8 * lg];
+    const uint2 x0 = *(const uint2 *)row, x1 = *(const uint2 *)(row + 4);
+    const v8h vf = __builtin_bit_cast(v8h, make_uint4(x0.x, x0.y, x1.x, x1.y));
+    o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[n], 0, 0, 0);
+  }
+  // the wave's context [G][HD] over its tile (every read of the tile above
+  // feeds these values, so the stores follow them)
+  float *ctxw = (float *)vt;
+  if (li < G) {
+#pragma unroll
+    for (int n = 0; n < 8; n++) *(float4 *)&ctxw[li * HD + 16 * n + 4 * lg] = make_float4(o[n][0], o[n][1], o[n][2], o[n][3]);
+    if (lg == 0) {
+      s_m[w][li] = m;
+      s_z[w][li] = z;
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * HD; idx += NW * 64) {
+    const int h = idx / HD, d = idx % HD;
+    float mm = s_m[0][h];
+#pragma unroll
+    for (int k = 1; k < NW; k++) mm = s_m[k][h] > mm ? s_m[k][h] : mm;
+    float zz = 0.0f, cx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NW; k++) {
+      const float scl = nlg_exp2(s_m[k][h] - mm);
+      zz = fmaf(s_z[k][h], scl, zz);
+      cx = fmaf(((const float *)s_vt[k])[h * HD + d], scl, cx);
+    }
+    pctx[idx] = cx;
+    if (d == 0) {
+      pmz[2 * h] = mm;
+      pmz[2 * h + 1] = zz;
+    }
+  }
+}
+
 // Pass 2: out = sum_c pctx_c * exp(m_c - M) / sum_c z_c * exp(m_c - M),
 // M = max_c m_c, one thread per output element.
 __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ pctx,
@@ -480,6 +687,12 @@ static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, int
   a.nunits = rows * a.kvheads * a.nchunk;
   const dim3 grid = G == 1 ? dim3((a.nunits + 7) / 8 * 8 * a.grp) : dim3(a.nchunk, a.heads / G, rows);
   const dim3 blk(ATTN_WAVES * 64);
+  if (head_dim == 128 && G == 4 && ni == 8 && (mode & ~AM_NT) == AM_CONTIG) {
+    if (mode & AM_NT) hipLaunchKernelGGL(k_attn_mfma<true>, grid, blk, 0, st, a);
+    else hipLaunchKernelGGL(k_attn_mfma<false>, grid, blk, 0, st, a);
+    NLG_LAUNCHED("decode attention (fp16 KV, matrix cores)");
+    return NLG_OK;
+  }
 #define AT1(HD, GG, PGV)                                                                   \
   do {                                                                                     \
     if (ni == 8) hipLaunchKernelGGL((k_attn_part<HD, GG, 8, PGV>), grid, blk, 0, st, a);   \

@@ -188,8 +188,13 @@ def test_lm_head_argmax(seq, vocab, cols, dup):
         assert np.array_equal(da.download(np.int32, seq), np.argmax(want.reshape(seq, vocab), axis=1))
 
 
+# The last two take the matrix-core chunk pass (head_dim 128, four query
+# heads per kv head, 256-position chunks, 128+ workgroups), with and without
+# non-temporal K/V loads; their positions sit on wave (32) and chunk (256)
+# boundaries and leave whole waves and chunks past the position.
 ATTN = [(1, 20, 5, 128, 768, [0, 1, 63, 64, 65, 200, 767]), (3, 8, 8, 64, 130, [0, 129, 77]),
-        (2, 16, 2, 128, 200, [150, 3]), (1, 4, 2, 64, 64, [63, 10]), (32, 20, 5, 128, 768, [640])]
+        (2, 16, 2, 128, 200, [150, 3]), (1, 4, 2, 64, 64, [63, 10]),
+        (32, 20, 5, 128, 768, [0, 31, 32, 255, 256, 511, 640, 767]), (11, 16, 4, 128, 520, [0, 15, 16, 255, 256, 300, 519])]
 
 
 @pytest.mark.parametrize("B,heads,kvh,hd,max_seq,positions", ATTN)
