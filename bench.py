@@ -313,7 +313,7 @@ def decode_bench(batch: int, stream):
             "step_bytes": int(step_bytes), "step_gbs": round(step_bytes / (ms_tok * 1e-3) / 1e9, 1),
             "step_frac": round(step_bytes / (ms_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             # per layer: 5 launches, or 9 when the linears take the batched (quantise + GEMM) form
-            "launches_per_step": L * (9 if batch >= 8 else 5) + (2 if batch >= 8 else 1) + (2 if batch > 1 else 1),
+            "launches_per_step": L * (9 if batch >= 4 else 5) + (2 if batch >= 4 else 1) + (2 if batch > 1 else 1),
             "lm_head_bytes": int(lm_bytes), "per_kernel": per}
 
 
@@ -426,8 +426,8 @@ def ffn_bench(stream):
         r = {"us": round(us, 3), "bytes": int(nbytes), "gbs": round(nbytes / us / 1e3, 1),
              "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "tops": round(ops / us / 1e6, 2),
              "frac_int8_mfma": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
-             "path": "fused GEMV (2 launches)" if B < 8 else "per-token quantise + int8 MFMA GEMM (4 launches)"
-             + (", tiled weight copies" if B >= 8 else "")}
+             "path": "fused GEMV (2 launches)" if B < 4 else "per-token quantise + int8 MFMA GEMM (4 launches)"
+             + (", tiled weight copies" if B >= 4 else "")}
         out[f"B{B}"] = r
     for c in range(FFN_COPIES):
         nlgpu.ternary_tiled_unregister(gu_c[c])

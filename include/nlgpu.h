@@ -161,10 +161,12 @@ int nlg_ternary_linear_i8_cfg(const uint32_t *xq, const float *gamma, const uint
 
 /* The whole ternary linear from f32 activations: pack-act-rows quantisation
  * of x then nlg_ternary_linear_i8, bit-identical to running the two.  When
- * cols % 64 == 0, cols <= 16384 and seq <= 4 it is one launch (each
- * workgroup quantises the row into LDS while its weight loads are in
- * flight) and needs no workspace; otherwise it runs pack-act-rows into
- * `workspace` (nlg_ternary_linear_workspace bytes) and then the GEMV.
+ * cols % 64 == 0, cols <= 16384 and seq <= 3 (seq <= 4 when cols % 256 != 0)
+ * it is one launch (each workgroup quantises the row into LDS while its
+ * weight loads are in flight) and needs no workspace; with 4 or more tokens
+ * and cols % 256 == 0 it takes the batched form below (library scratch, no
+ * workspace); otherwise it runs pack-act-rows into `workspace`
+ * (nlg_ternary_linear_workspace bytes) and then the GEMV.
  * gamma_out (may be NULL) receives the per-token scales. */
 int nlg_ternary_linear(const float *x, const uint32_t *w2, const float *bias, const float *beta,
                        int beta_per_row, float *y, float *gamma_out, uint32_t seq, uint32_t out,
@@ -205,7 +207,7 @@ int nlg_softmax_rows(const float *a, float *c, uint32_t rows, uint32_t cols, voi
  * The RMSNorm is rmsnorm-istd + rmsnorm-fwd (kernels.el:1249-1265) with eps
  * a parameter: S = 1/sqrt(sum(x*x)/cols + eps), xn = (x*S)*gain; its sum is
  * a tree, so S may differ from the serial loop's in the last bit.
- * With 8 or more tokens and cols % 256 == 0 each of them (and
+ * With 4 or more tokens and cols % 256 == 0 each of them (and
  * nlg_ternary_linear) runs as per-token quantisation into library scratch
  * followed by the int8 matrix-core GEMM.  That scratch is one per stream:
  * calls on different streams may overlap.  It grows by allocating, so on a
@@ -409,12 +411,12 @@ int nlg_repack_packed_to_2bit(const float *wpk, uint32_t out, uint32_t cols, uin
 
 /* Tiled weight copies.  No counterpart in the reference, which reads the
  * row layout of ternary-rows (kernels.el:700-746) at every batch size; for
- * callers that run the batched linears above (8 or more tokens).
+ * callers that run the batched linears above (4 or more tokens).
  * Registering 2-bit weights w2 [rows x cols/16] (cols a multiple of 256,
  * 16-byte aligned) makes a library-owned copy of them in the matrix-core
  * GEMM's load order (the same words; each wave then loads 1 KiB runs
  * instead of 32-byte pieces of 32 rows), which every linear given this w2
- * pointer with the same rows and cols at 8+ tokens reads instead.  The
+ * pointer with the same rows and cols at 4+ tokens reads instead.  The
  * copy is taken when this is called (it waits for `stream`): register
  * again after changing the weights, and unregister before freeing w2.
  * Results are bit-identical to the row layout's.  Costs rows (rounded up

@@ -268,7 +268,14 @@ struct FusedArgs {
 // form instead (per-token quantisation into library scratch, then the int8
 // matrix-core GEMM with the same epilogue).
 int nlg_fused_launch(const FusedArgs &a, int pro, int epi, int rows_per_wave, hipStream_t st);
-#define NLG_BATCHED_MIN 8
+// From 4 tokens the matrix-core form is faster than the decode GEMV, whose
+// cost grows with every token (each workgroup quantises and dots one
+// token; the quantise + GEMM pair is latency-bound and nearly flat).
+// Measured on the config-4 FFN (2560 -> 6912 -> 2560): GEMV 14.3 / 16.4 /
+// 19.3 / 27.1 / 31.7 us at 2 / 3 / 4 / 5 / 7 tokens, matrix cores 16.9 /
+// 17.1 / 17.4 / 17.5 / 17.6 us; config-5 decode at batch 4 and 6: 3,079
+// -> 3,202 and 3,617 -> 4,502 tok/s.
+#define NLG_BATCHED_MIN 4
 bool nlg_batched(uint32_t seq, uint32_t cols);
 int nlg_batched_launch(const FusedArgs &a, int pro, int epi, hipStream_t st);
 // Its GEMM alone, over activations already quantised into xq / gamma (as

@@ -422,9 +422,9 @@ static int stack_attention(nlg_stack *s, Layer &y) {
 
 static int stack_head(nlg_stack *s);
 
-// The matrix-core GEMMs (8+ rows: prompts, and every step at batch >= 8)
+// The matrix-core GEMMs (4+ rows: prompts, and every step at batch >= 4)
 // read tiled copies of the layer weights, and of the LM head when it runs
-// on 8+ rows (batch >= 8): one more copy of them, made once.
+// on 4+ rows (batch >= 4): one more copy of them, made once.
 static int stack_tile(nlg_stack *s) {
   if (s->tiled) return NLG_OK;
   const nlg_stack_config &c = s->c;

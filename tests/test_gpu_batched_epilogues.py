@@ -256,7 +256,7 @@ def test_tiled_copy_registration():
         nlgpu.ternary_tiled_register(dw, out, 1000)
 
 
-# 8..127 tokens: the 16x16x64 GEMM with 64-row workgroups (many rows) or the
+# 4..127 tokens: the 16x16x64 GEMM with 64-row workgroups (many rows) or the
 # 16-row column-split form (few rows), each on the row layout and on a tiled copy
 SMALL = [(8, 13824, 2560), (32, 13824, 2560), (100, 6912, 1024), (32, 2560, 6912), (16, 3840, 2560),
          (32, 2560, 2560), (77, 1000, 512)]

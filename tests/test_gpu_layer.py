@@ -157,7 +157,7 @@ def test_qkv_rope_and_fp16_append(B, heads, kvh, hd, cols, max_seq, pos):
 # vocabularies of 32,768 rows and more at under 8 rows take the LM-head form
 # (one quantisation launch, then the streaming GEMV at 1, 2 or 4 chunks per lane)
 @pytest.mark.parametrize("seq,vocab,cols,dup", [(1, 128256, 2560, False), (2, 1000, 256, True), (1, 37, 64, True),
-                                                (32, 128256, 2560, False), (8, 1000, 256, True),
+                                                (32, 128256, 2560, False), (8, 1000, 256, True), (5, 9000, 2560, False),
                                                 (16, 9000, 2560, False), (32, 9000, 2560, True),
                                                 (2, 40000, 1024, True), (1, 33000, 6144, True),
                                                 (3, 32800, 9216, False)])
@@ -177,7 +177,7 @@ def test_lm_head_argmax(seq, vocab, cols, dup):
     got = dl.download(f32, seq * vocab)
     same_bits(got, want)
     assert np.array_equal(da.download(np.int32, seq), np.argmax(want.reshape(seq, vocab), axis=1))
-    if seq >= 8 and cols % 256 == 0:  # the batched form again, on a registered tiled copy
+    if seq >= 4 and cols % 256 == 0:  # the batched form again, on a registered tiled copy
         nlgpu.ternary_tiled_register(dw, vocab, cols)
         try:
             dl.zero()

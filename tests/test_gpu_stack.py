@@ -146,7 +146,7 @@ def test_prefill_matches_teacher_forced_steps(n):
     b.close()
 
 
-# Batch >= 8 takes the batched decode path (per-token quantisation + the
+# Batch >= 4 takes the batched decode path (per-token quantisation + the
 # small-batch GEMM epilogues, batched argmax partials); head_dim 128 with
 # max_seq in (512, 768] gives three attention chunks, merged by the
 # three-chunk prologue of the output projection.
@@ -154,11 +154,13 @@ MID = dict(layers=2, d_model=512, heads=4, kv_heads=2, head_dim=128, d_ff=1024, 
            batch=8)
 
 
-def test_batched_decode_graph_eager_and_reference():
-    print("[gpu] stack B=8 hd=128 max_seq=700: graph vs eager, greedy, reference", flush=True)
-    B, vocab = MID["batch"], MID["vocab"]
+@pytest.mark.parametrize("B", [8, 5])
+def test_batched_decode_graph_eager_and_reference(B):
+    print(f"[gpu] stack B={B} hd=128 max_seq=700: graph vs eager, greedy, reference", flush=True)
+    vocab = MID["vocab"]
+    kw = dict(MID, batch=B)
     P = prompts(B, 3, vocab, seed=31)
-    a, b = nlgpu.Stack(**MID), nlgpu.Stack(**MID)
+    a, b = nlgpu.Stack(**kw), nlgpu.Stack(**kw)
     r = ref.RefStack(a)
     a.start(P)
     b.start(P)

@@ -42,7 +42,7 @@ def run_both(seed, seq, out, cols):
 FORMS = {
     "batched matrix-core": ((512, 2560, 2560), (100, 640, 1024)),
     "two launches": ((40, 300, 1000), (6, 300, 1000)),
-    "one launch": ((4, 4096, 4096), (1, 2560, 2560)),
+    "one launch": ((3, 4096, 4096), (1, 2560, 2560)),
 }
 
 
