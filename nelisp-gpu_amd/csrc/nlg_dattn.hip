@@ -392,7 +392,10 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
 
 // The chunk pass on the matrix cores, for head_dim 128, 4 query heads per
 // kv head and 256-position chunks over contiguous caches: the same
-// workgroups, chunks and outputs as k_attn_part<128, 4, 8, MODE>.  Wave w
+// workgroups, chunks and outputs as k_attn_part<128, 4, 8, MODE>, over
+// contiguous caches or (RG) StreamingLLM ring caches (chunk positions are
+// cache-relative ranks; each K row is rotated by its rank in f32 and, like
+// q, split into fp16 hi + lo, three products per step: hi.hi, lo.hi, hi.lo).  Wave w
 // takes positions p0 + 32 w .. + 31 of its chunk for the 4 query heads, on
 // v_mfma_f32_16x16x32_f16 (layout, checked on gfx950: lane 16g + i holds
 // A[i][8g..8g+7] and B[8g..8g+7][i]; result r of lane l is C[4(l/16) + r][l % 16]):
@@ -415,8 +418,8 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
 // reductions and conversions; here they are 32 matrix-core steps per wave.
 #define AMF_PITCH 36  // V^T tile row pitch in 16-bit elements (32 slots + 4: 8-byte aligned rows)
 
-template <bool NT>
-__global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs a) {
+template <bool NT, bool RG>
+__global__ __launch_bounds__(512, 4) void k_attn_mfma(AttnArgs a) {
   constexpr int HD = 128, G = 4, NW = ATTN_WAVES, PW = 32, CS = NW * PW;
   typedef _Float16 v8h __attribute__((ext_vector_type(8)));
   typedef float v4f __attribute__((ext_vector_type(4)));
@@ -437,6 +440,22 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs a) {
   const size_t slot = (size_t)b * a.kvheads + kvh;
   const uint16_t *kb = a.kc + slot * a.max_seq * HD;
   const uint16_t *vb = a.vc + slot * a.max_seq * HD;
+  // ring: the stream position first (it fixes the ring's oldest slot)
+  uint32_t rlen = 0, qrank = 0, woff = 0;
+  if (RG) {
+    const int32_t ps = a.pos[b];
+    const uint32_t pos = ps < 0 ? 0u : (uint32_t)ps, cap = a.max_seq;
+    rlen = pos + 1 < cap ? pos + 1 : cap;  // pos + 1 > 0: pos < 2^31
+    const uint32_t start = pos >= cap ? pos - a.win + 1 : a.nsink;
+    woff = (start - a.nsink) % a.win;
+    qrank = pos < cap ? pos : cap - 1;
+  }
+  // a rank's slot: sink slot r below nsink, later ranks walk the ring from its oldest entry
+  auto slot_of = [&](uint32_t pc) -> uint32_t {
+    if (!RG || pc < a.nsink) return pc;
+    const uint32_t t = woff + (pc - a.nsink);  // < 2 win
+    return a.nsink + (t >= a.win ? t - a.win : t);
+  };
   // q first (loads retire in issue order): lane (lg, li) takes head
   // h0 + li (li < 4; the others zero), dims 32 s + 8 lg .. + 7
   const float *qb = a.q + (size_t)qr * a.heads * HD + (size_t)(h0 + (li < G ? li : 0)) * HD + 8 * lg;
@@ -451,7 +470,7 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs a) {
   // first so that rows past it are never fetched; small ones fetch the whole
   // chunk while the position is in flight.
   uint32_t lim = a.max_seq;
-  if (NT) {
+  if (NT && !RG) {
     const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(qr % a.qper) : 0);
     lim = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
   }
@@ -462,11 +481,19 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs a) {
   // at B = 32: the pass alone 14.05 -> 14.25 us, the decode step 1.773 ->
   // 1.713 ms).
   uint4 kr[2][4];
+  float4 rc[2][4], rs[2][4];  // ring: the rank's rotation pairs of the lane's 8 dims
 #pragma unroll
   for (int bb = 0; bb < 2; bb++) {
     const uint32_t pp = pw + 16 * bb + li, pc = pp < lim ? pp : lim - 1;
+    const size_t ro = (size_t)slot_of(pc) * HD;
 #pragma unroll
-    for (int s = 0; s < 4; s++) kr[bb][s] = kv_ld<NT>(kb + (size_t)pc * HD + 32 * s + 8 * lg);
+    for (int s = 0; s < 4; s++) {
+      kr[bb][s] = kv_ld<NT>(kb + ro + 32 * s + 8 * lg);
+      if (RG) {
+        rc[bb][s] = *(const float4 *)(a.co + (size_t)pc * (HD / 2) + 16 * s + 4 * lg);
+        rs[bb][s] = *(const float4 *)(a.si + (size_t)pc * (HD / 2) + 16 * s + 4 * lg);
+      }
+    }
   }
   // V, whole rows: lane (lg, li) positions pw + 16 u + 4 lg + r, dims 8 li .. + 7
   uint4 vr[2][4];
@@ -475,10 +502,22 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const uint32_t pp = pw + 16 * u + 4 * lg + r, pc = pp < lim ? pp : lim - 1;
-      vr[u][r] = kv_ld<NT>(vb + (size_t)pc * HD + 8 * li);
+      vr[u][r] = kv_ld<NT>(vb + (size_t)slot_of(pc) * HD + 8 * li);
     }
-  const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(qr % a.qper) : 0);
-  const uint32_t len = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
+  // ring: q rotated by the query's rank (pairs 16 s + 4 lg + j of its dims)
+  float4 qc[4], qs[4];
+  if (RG) {
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      qc[s] = *(const float4 *)(a.co + (size_t)qrank * (HD / 2) + 16 * s + 4 * lg);
+      qs[s] = *(const float4 *)(a.si + (size_t)qrank * (HD / 2) + 16 * s + 4 * lg);
+    }
+  }
+  uint32_t len = rlen;
+  if (!RG) {
+    const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(qr % a.qper) : 0);
+    len = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
+  }
   if (p0 >= len) {  // block-uniform: a chunk past the position adds nothing
     for (int i = threadIdx.x; i < G * HD; i += NW * 64) pctx[i] = 0.0f;
     if (threadIdx.x < G) {
@@ -489,14 +528,25 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs a) {
   }
   v8h qh[4], ql[4];
 #pragma unroll
-  for (int s = 0; s < 4; s++)
+  for (int s = 0; s < 4; s++) {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = li < G ? f4_at(qv[2 * s + e / 4], e % 4) : 0.0f;
+    if (RG) {  // decode-attn-stream's rotation: C[i0] = a0*c - a1*s; C[i1] = a0*s + a1*c
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float x0 = x[2 * j], x1 = x[2 * j + 1], cj = f4_at(qc[s], j), sj = f4_at(qs[s], j);
+        x[2 * j] = x0 * cj - x1 * sj;
+        x[2 * j + 1] = x0 * sj + x1 * cj;
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-      const float x = li < G ? f4_at(qv[2 * s + e / 4], e % 4) : 0.0f;
-      const _Float16 h = (_Float16)x;
+      const _Float16 h = (_Float16)x[e];
       qh[s][e] = h;
-      ql[s][e] = (_Float16)(x - (float)h);
+      ql[s][e] = (_Float16)(x[e] - (float)h);
     }
+  }
   // scores: lane (lg, li < 4) gets head li at positions pw + 16 bb + 4 lg + r
   v4f sc[2];
 #pragma unroll
@@ -504,9 +554,31 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs a) {
     sc[bb] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-      const v8h kf = __builtin_bit_cast(v8h, kr[bb][s]);
-      sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[s], sc[bb], 0, 0, 0);
-      sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[s], sc[bb], 0, 0, 0);
+      if (RG) {  // K rotated by its rank in f32, then hi + lo halves
+        const v8h k16 = __builtin_bit_cast(v8h, kr[bb][s]);
+        float kf32[8];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float k0 = (float)k16[2 * j], k1 = (float)k16[2 * j + 1];
+          const float cj = f4_at(rc[bb][s], j), sj = f4_at(rs[bb][s], j);
+          kf32[2 * j] = k0 * cj - k1 * sj;
+          kf32[2 * j + 1] = k0 * sj + k1 * cj;
+        }
+        v8h kh, kl;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const _Float16 h = (_Float16)kf32[e];
+          kh[e] = h;
+          kl[e] = (_Float16)(kf32[e] - (float)h);
+        }
+        sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[s], sc[bb], 0, 0, 0);
+        sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[s], sc[bb], 0, 0, 0);
+        sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[s], sc[bb], 0, 0, 0);
+      } else {
+        const v8h kf = __builtin_bit_cast(v8h, kr[bb][s]);
+        sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[s], sc[bb], 0, 0, 0);
+        sc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[s], sc[bb], 0, 0, 0);
+      }
     }
   }
   float m = -1.0e30f;
@@ -687,10 +759,18 @@ static int attn_chunks_launch(AttnArgs &a, uint32_t rows, uint32_t head_dim, int
   a.nunits = rows * a.kvheads * a.nchunk;
   const dim3 grid = G == 1 ? dim3((a.nunits + 7) / 8 * 8 * a.grp) : dim3(a.nchunk, a.heads / G, rows);
   const dim3 blk(ATTN_WAVES * 64);
-  if (head_dim == 128 && G == 4 && ni == 8 && (mode & ~AM_NT) == AM_CONTIG) {
-    if (mode & AM_NT) hipLaunchKernelGGL(k_attn_mfma<true>, grid, blk, 0, st, a);
-    else hipLaunchKernelGGL(k_attn_mfma<false>, grid, blk, 0, st, a);
-    NLG_LAUNCHED("decode attention (fp16 KV, matrix cores)");
+  // (ring caches small enough for plain loads keep the VALU pass: that
+  // variant's registers spill under the two-workgroups-per-CU bound)
+  if (head_dim == 128 && G == 4 && ni == 8 &&
+      ((mode & ~AM_NT) == AM_CONTIG || mode == (AM_RING | AM_NT))) {
+    const bool nt = mode & AM_NT, rg = (mode & ~AM_NT) == AM_RING;
+    if (rg) {
+      hipLaunchKernelGGL((k_attn_mfma<true, true>), grid, blk, 0, st, a);
+    } else {
+      if (nt) hipLaunchKernelGGL((k_attn_mfma<true, false>), grid, blk, 0, st, a);
+      else hipLaunchKernelGGL((k_attn_mfma<false, false>), grid, blk, 0, st, a);
+    }
+    NLG_LAUNCHED(rg ? "decode attention (ring fp16 KV, matrix cores)" : "decode attention (fp16 KV, matrix cores)");
     return NLG_OK;
   }
 #define AT1(HD, GG, PGV)                                                                   \

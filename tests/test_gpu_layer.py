@@ -331,11 +331,12 @@ def _rope_tables(rows, hd, theta=500000.0):
 
 @pytest.mark.parametrize("B,heads,kvh,hd,nsink,win", [(1, 4, 2, 64, 2, 6), (3, 8, 1, 64, 0, 37),
                                                       (4, 4, 4, 128, 4, 250), (2, 16, 2, 128, 4, 1020),
-                                                      (32, 20, 5, 128, 4, 508)])
+                                                      (32, 20, 5, 128, 4, 508), (32, 20, 5, 128, 4, 764)])
 def test_ring_f16_attention(B, heads, kvh, hd, nsink, win):
     """StreamingLLM decode attention over fp16 ring caches: sequences before
     the ring fills, exactly at capacity and wrapped many times, against the
-    CPU restatement."""
+    CPU restatement.  The last case (768 slots, 32 sequences, non-temporal
+    loads) takes the matrix-core chunk pass."""
     print(f"[gpu] ring attention B={B} heads={heads}/{kvh} hd={hd} nsink={nsink} win={win}", flush=True)
     cap = nsink + win
     rng = np.random.default_rng(B * 7 + win)
