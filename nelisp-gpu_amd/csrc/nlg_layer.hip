@@ -108,14 +108,18 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   // each activation chunk from LDS once per lane instead of R times; the
   // packed form there measured 3.48 -> 3.68 us for the 4096^2 step).
   constexpr bool PACK = CPL == 1 && F4 <= 3 && R >= 4;
+  // packed rows: a row has at most 16 F4 chunks, so a lane holds at most
+  // KPL = ceil(16 F4 / G) of them (3 of R = 4, 6 of 8, 12 of 16 at 2560
+  // columns) -- no load issued for a chunk slot no row length can reach
   constexpr int G = PACK ? 64 / R : 64;
   const uint32_t prow = (uint32_t)lane / G, pj = (uint32_t)lane % G;
+  constexpr int KPL = PACK ? ((16 * F4 + (64 / R) - 1) / (64 / R) < R ? (16 * F4 + (64 / R) - 1) / (64 / R) : R) : R;
   uint4 wv[R][CPL];
   if (PACK) {
     const uint32_t row = row0 + prow < a.out ? row0 + prow : a.out - 1;
     const uint4 *wr = (const uint4 *)(a.w2 + (size_t)row * a.wng);
 #pragma unroll
-    for (int k = 0; k < R; k++) {
+    for (int k = 0; k < KPL; k++) {
       const uint32_t c = pj + G * k;
       wv[k][0] = nlg_ld_stream(&wr[c < nchunk ? c : nchunk - 1]);
     }
@@ -242,7 +246,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   if (PACK) {
     int acc = 0;
 #pragma unroll
-    for (int k = 0; k < R; k++) {
+    for (int k = 0; k < KPL; k++) {
       if ((uint32_t)(G * k) < nchunk) {  // wave-uniform: some lane's chunk is real
         const uint32_t c = pj + G * k, cc = c < nchunk ? c : nchunk - 1;
         const bool valid = c < nchunk;
