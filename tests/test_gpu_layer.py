@@ -160,7 +160,10 @@ def test_qkv_rope_and_fp16_append(B, heads, kvh, hd, cols, max_seq, pos):
                                                 (32, 128256, 2560, False), (8, 1000, 256, True), (5, 9000, 2560, False),
                                                 (16, 9000, 2560, False), (32, 9000, 2560, True),
                                                 (2, 40000, 1024, True), (1, 33000, 6144, True),
-                                                (3, 32800, 9216, False)])
+                                                (3, 32800, 9216, False),
+                                                # 1,024+ 64-row tiles: the resident-activation GEMM
+                                                (20, 66000, 2560, True), (5, 70000, 512, True),
+                                                (40, 33000, 768, False)])
 def test_lm_head_argmax(seq, vocab, cols, dup):
     print(f"[gpu] argmax seq={seq} vocab={vocab} cols={cols}", flush=True)
     x, g = int_rows(vocab, seq * cols), gains(cols + 9, cols)

@@ -143,7 +143,11 @@ BATCHED = [(4, 100, 1024), (6, 2560, 6912), (7, 3840, 2560), (8, 64, 256), (16, 
            (64, 512, 4096), (100, 256, 1024), (512, 2560, 2560), (512, 6912, 2560),
            (200, 1000, 512), (600, 16448, 256),  # 64-row tiles, ragged; 128-row tiles, ragged
            (40, 16400, 512), (32, 8200, 768),  # enough 64-row workgroups: the unsplit small-batch kernel
-           (24, 1000, 12288), (9, 130, 8192)]  # split columns, 12 and 8 chunks per wave (the 16-chunk form)
+           (24, 1000, 12288), (9, 130, 8192),  # split columns, 12 and 8 chunks per wave (the 16-chunk form)
+           # 1,024+ 64-row tiles of <= 2,560 columns: resident activations, a
+           # loop over row tiles (16 and 32 tokens, ragged rows, two token
+           # blocks, rows shorter than the 10-chunk stage)
+           (20, 65600, 512), (9, 66001, 2560), (40, 33000, 256)]
 
 
 @pytest.mark.parametrize("seq,out,cols", BATCHED)
