@@ -344,7 +344,10 @@ __global__ __launch_bounds__(512) void k_attn_part(AttnArgs a) {
   }
 #pragma unroll
   for (int i = 0; i < NI; i++) {
-    const uint4 vi = PG || EN ? keep_u4((rowm >> i) & 1u, vr[i]) : vr[i];
+    // rows past the position are zeros here, as rows outside a pool are: the
+    // score's -inf makes e 0, but a cache row nobody wrote may hold NaN or
+    // Inf bits, and 0 x NaN is NaN
+    const uint4 vi = keep_u4(EN ? (rowm >> i) & 1u : (pp[i] < len && (!PG || ((rowm >> i) & 1u))), vr[i]);
 #pragma unroll
     for (int h = 0; h < G; h++) {
       const float e = nlg_exp2(s[i][h] - m[h]);
@@ -612,7 +615,9 @@ __global__ __launch_bounds__(512, 4) void k_attn_mfma(AttnArgs a) {
   z = z + __shfl_xor(z, 16);
   z = z + __shfl_xor(z, 32);
   // V^T tile: dims 8 li + e, slots 8 lg + 4 u + r (one wave's LDS operations
-  // run in order, so the tile needs no barrier)
+  // run in order, so the tile needs no barrier).  Rows past the position go
+  // in as zeros: their probability is 0, but a cache row nobody wrote may
+  // hold NaN or Inf bits, and 0 x NaN is NaN.
   uint16_t *vt = s_vt[w];
 #pragma unroll
   for (int u = 0; u < 2; u++)
@@ -623,7 +628,7 @@ __global__ __launch_bounds__(512, 4) void k_attn_mfma(AttnArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const uint32_t word = wd == 0 ? vr[u][r].x : wd == 1 ? vr[u][r].y : wd == 2 ? vr[u][r].z : vr[u][r].w;
-        hv[r] = (word >> sh) & 0xffffu;
+        hv[r] = (word >> sh) & (pw + 16 * u + 4 * lg + r < len ? 0xffffu : 0u);
       }
       *(uint2 *)&vt[(8 * li + e) * AMF_PITCH + 8 * lg + 4 * u] = make_uint2(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16));
     }

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
       }                                                                                   \
     }                                                                                     \
   } while (0)
-#define PA_STORE(buf)                                                                     \
+#define PA_STORE(buf, kb)                                                                 \
   do {                                                                                    \
     _Pragma("unroll") for (int u = 0; u < KI; u++) {                                      \
       const uint32_t t = threadIdx.x + NT * u;                                            \
@@ -126,13 +126,18 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
       const uint32_t t = threadIdx.x + NT * u;                                            \
       if ((PA_KB / 4 * HD / 4) % NT == 0 || t < PA_KB / 4 * HD / 4) {                                                       \
         const uint32_t k4 = 4 * (t / (HD / 4)), d4 = 4 * (t % (HD / 4));                  \
+        /* keys past plast (never attended here; the cache may hold anything  */         \
+        /* there, NaN included, and 0 x NaN is NaN) go in as zeros            */         \
+        const int32_t kk = (int32_t)((kb) * PA_KB + k4);                                   \
+        const uint32_t m0 = kk <= plast ? 0xffffu : 0u, m1 = kk + 1 <= plast ? 0xffffu : 0u; \
+        const uint32_t m2 = kk + 2 <= plast ? 0xffffu : 0u, m3 = kk + 3 <= plast ? 0xffffu : 0u; \
         /* dims d4 + c: the 4 keys' halves c, low key first */                            \
         _Pragma("unroll") for (int c = 0; c < 4; c++) {                                   \
           const int sh = 16 * (c & 1);                                                    \
-          const uint32_t h0 = (vr[8 * u + 0 + c / 2] >> sh) & 0xffffu;                    \
-          const uint32_t h1 = (vr[8 * u + 2 + c / 2] >> sh) & 0xffffu;                    \
-          const uint32_t h2 = (vr[8 * u + 4 + c / 2] >> sh) & 0xffffu;                    \
-          const uint32_t h3 = (vr[8 * u + 6 + c / 2] >> sh) & 0xffffu;                    \
+          const uint32_t h0 = (vr[8 * u + 0 + c / 2] >> sh) & m0;                         \
+          const uint32_t h1 = (vr[8 * u + 2 + c / 2] >> sh) & m1;                         \
+          const uint32_t h2 = (vr[8 * u + 4 + c / 2] >> sh) & m2;                         \
+          const uint32_t h3 = (vr[8 * u + 6 + c / 2] >> sh) & m3;                         \
           *(uint2 *)(&s_v[buf][(d4 + c) * VP + k4]) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16)); \
         }                                                                                 \
       }                                                                                   \
@@ -161,7 +166,7 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
   float m = -1.0e30f, l = 0.0f;
   if (nkb > kbf) {
     PA_LOAD(kbf);
-    PA_STORE(kbf & 1);
+    PA_STORE(kbf & 1, kbf);
   }
   for (uint32_t kb = kbf; kb < nkb; kb++) {
     const int buf = kb & 1;
@@ -231,7 +236,7 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
         o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pl, o[t], 0, 0, 0);
       }
     }
-    if (kb + 1 < nkb) PA_STORE(buf ^ 1);
+    if (kb + 1 < nkb) PA_STORE(buf ^ 1, kb + 1);
   }
 #undef PA_LOAD
 #undef PA_STORE
