@@ -166,6 +166,17 @@ def test_batched_matrix_core_linear_bit_exact(seq, out, cols):
     y = dy.download(np.float32, seq * out)
     bad = np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))
     assert bad.size == 0, f"{bad.size} differ, first {bad[:5]}: {y[bad[:3]]} vs {y_ref[bad[:3]]}"
+    if out >= 32768:  # the resident-activation GEMM again, on a registered tiled copy
+        dw = nlgpu.to_device(w2)
+        nlgpu.ternary_tiled_register(dw, out, cols)
+        try:
+            dy.zero()
+            nlgpu.ternary_linear(nlgpu.to_device(x), dw, nlgpu.to_device(bias), nlgpu.to_device(beta),
+                                 dy, seq, out, cols, beta_per_row=per_row)
+        finally:
+            nlgpu.ternary_tiled_unregister(dw)
+        y = dy.download(np.float32, seq * out)
+        assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), "tiled copy"
 
 
 @pytest.mark.parametrize("seq,out,cols", [(16, 300, 2496), (2, 50, 1000), (5, 64, 4032)])
