@@ -73,6 +73,13 @@ __device__ __forceinline__ int nlg_dpp(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
 }
 
+// A quad permutation (every source lane exists, so no fill value is needed:
+// no zeroing move ahead of the DPP move).
+template <int CTRL>
+__device__ __forceinline__ uint32_t nlg_qperm(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, true);
+}
+
 __device__ __forceinline__ int nlg_wave_sum_i32(int v) {
   v += nlg_dpp<0xB1>(v);        // quad_perm [1,0,3,2]
   v += nlg_dpp<0x4E>(v);        // quad_perm [2,3,0,1]

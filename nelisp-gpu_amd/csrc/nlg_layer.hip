@@ -226,7 +226,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   //    stored already in the dots' operand order: a 16-column group's four
   //    words sit in the four lanes of a quad, and lane i keeps byte i of
   //    each (xpose4 across the quad, by DPP broadcasts)
-  const bool fast = g > 0.0f && ginv < INFINITY;
+  const bool fast = quant_fast(g);
   uint32_t *s_xq = (uint32_t *)s_xq4;
   const uint32_t qi = threadIdx.x & 3u;
   const uint32_t sel_lo = 0x0c0c0000u | ((4u + qi) << 8) | qi, sel_hi = 0x00000c0cu | ((4u + qi) << 24) | (qi << 16);
@@ -234,8 +234,8 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   for (int k = 0; k < F4; k++) {
     const uint32_t f = threadIdx.x + 256u * k;
     const int wd = (int)quant_word(xv4[k], g, ginv, fast);
-    const uint32_t n0 = (uint32_t)nlg_dpp<0x00>(wd), n1 = (uint32_t)nlg_dpp<0x55>(wd);
-    const uint32_t n2 = (uint32_t)nlg_dpp<0xAA>(wd), n3 = (uint32_t)nlg_dpp<0xFF>(wd);
+    const uint32_t n0 = nlg_qperm<0x00>((uint32_t)wd), n1 = nlg_qperm<0x55>((uint32_t)wd);
+    const uint32_t n2 = nlg_qperm<0xAA>((uint32_t)wd), n3 = nlg_qperm<0xFF>((uint32_t)wd);
     if (f < nf4) s_xq[f] = __builtin_amdgcn_perm(n1, n0, sel_lo) | __builtin_amdgcn_perm(n3, n2, sel_hi);
   }
   __syncthreads();

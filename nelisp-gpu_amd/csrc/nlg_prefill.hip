@@ -368,7 +368,7 @@ __global__ __launch_bounds__(256) void k_prefill_merge_q(PrefillArgs a, uint32_t
   amax = nlg_block_max_f32<4, true>(amax, red);
   const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
   const float ginv = 1.0f / g;
-  const bool fast = g > 0.0f && ginv < INFINITY;
+  const bool fast = quant_fast(g);
   if (threadIdx.x == 0) gamma[row] = g;
   const uint32_t qi = threadIdx.x & 3u;
   const uint32_t sel_lo = 0x0c0c0000u | ((4u + qi) << 8) | qi, sel_hi = 0x00000c0cu | ((4u + qi) << 24) | (qi << 16);
@@ -377,8 +377,8 @@ __global__ __launch_bounds__(256) void k_prefill_merge_q(PrefillArgs a, uint32_t
   for (int j = 0; j < J; j++) {
     const uint32_t f = threadIdx.x + 256u * j;
     const int n = (int)quant_word(v[j], g, ginv, fast);
-    const uint32_t n0 = (uint32_t)nlg_dpp<0x00>(n), n1 = (uint32_t)nlg_dpp<0x55>(n);
-    const uint32_t n2 = (uint32_t)nlg_dpp<0xAA>(n), n3 = (uint32_t)nlg_dpp<0xFF>(n);
+    const uint32_t n0 = nlg_qperm<0x00>((uint32_t)n), n1 = nlg_qperm<0x55>((uint32_t)n);
+    const uint32_t n2 = nlg_qperm<0xAA>((uint32_t)n), n3 = nlg_qperm<0xFF>((uint32_t)n);
     const uint32_t y = __builtin_amdgcn_perm(n1, n0, sel_lo) | __builtin_amdgcn_perm(n3, n2, sel_hi);
     if (f < nf4) dst[f] = y;
   }

@@ -26,25 +26,32 @@ __device__ __forceinline__ uint32_t pack_lane(float v, float gamma) {
 
 // ---- exact quantisation without a division per element ----
 //
-// pack-act-rows' lane magnitude is ri = min(trunc(t'), 127) with
-// t' = RN(RN(|v|/gamma) + 0.5).  With ginv = RN(1/gamma) finite, the estimate
-// t = RN(|v|*ginv + 0.5) (one fused rounding) differs from t' by less than
-// 3e-5 whenever t < 128 (the reciprocal errs by at most 2^-24 relative on a
-// quotient below 128.5, and each of the three roundings by half an ulp of a
-// value below 128.5), so trunc(t) == trunc(t') unless t lies within 2^-13 of
-// an integer, i.e. unless |frac(t) - 1/2| > 1/2 - 2^-13 (both sides exact).
-// t >= 128 means t' > 127.99, which the clamp maps to 127 either way.  The
-// few elements inside that band (and NaNs) are recomputed with the
-// reference's IEEE division.  |v|/gamma = |v/gamma| under round-to-nearest,
-// and a nonzero lane implies |v/gamma| >= 0.5, so the sign is v's: the
-// stored byte is the low byte of the signed magnitude, (256 - ri) % 256 for
-// a negative v.  About 9 instructions per lane: fma, trunc, two subtracts, a
-// compare, min, copysign, convert and a third of a byte permute.
-__device__ __forceinline__ int32_t lane_est(float v, float ginv, bool &near) {
-  const float t = fmaf(fabsf(v), ginv, 0.5f);
-  const float kf = truncf(t);
-  near = !(fabsf((t - kf) - 0.5f) <= 0.5f - 0x1p-13f);  // NaN lands here
-  return (int32_t)__builtin_copysignf(fminf(kf, 127.0f), v);
+// pack-act-rows' lane is ri = min(trunc(RN(|q| + 0.5)), 127) with
+// q = RN(v/gamma), stored as the low byte of ri, or of -ri when q < 0.
+// The quotient comes from the row's reciprocal y = RN(1/gamma) (one IEEE
+// division per row) and one correction step (Markstein): q0 = RN(v*y),
+// r = v - q0*gamma (exact in one fma), q = RN(q0 + r*y) (one fma).  With y
+// correctly rounded, q0 within an ulp of v/gamma and no underflow, q is
+// exactly the correctly rounded quotient RN(v/gamma) -- the reference's
+// OpFDiv result under IEEE rounding -- for every v (pinned on the CPU across
+// every rounding boundary of many scales in tests/test_quant_rule.py).
+// gamma >= 2^-90 keeps the remainder clear of underflow; rows with a smaller
+// (or zero, or infinite) gamma divide per element (`fast` false).
+// RN is symmetric, so RN(|q| + 0.5) with q's sign is RN(q + copysign(0.5, v))
+// (q has v's sign, -0 included), and its truncation is +-ri.  NaN converts
+// to 0, the reference's (uint f) of NaN.  Seven instructions per lane, no
+// branch: mul, two fma, copysign, add, convert, clamp (the clamp never binds
+// when gamma comes from the row's own absmax: |q| <= 127.0000077), plus a
+// quarter of a byte pack.  (The previous estimate-and-fix-up form spent
+// ~0.5 us of a 4096-column decode GEMV in its fix-up branches.)
+__device__ __forceinline__ bool quant_fast(float gamma) { return gamma >= 0x1p-90f && gamma < INFINITY; }
+__device__ __forceinline__ int32_t lane_q8(float v, float gamma, float ginv) {
+  const float q0 = v * ginv;
+  const float q = fmaf(fmaf(-q0, gamma, v), ginv, q0);  // RN(v / gamma)
+  const float s = q + __builtin_copysignf(0.5f, v);
+  int32_t t;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(t) : "v"(s));  // truncates; NaN -> 0 (no poison)
+  return min(max(t, -127), 127);
 }
 // the low bytes of a, b, c, d as one word (a in bits 0..7)
 __device__ __forceinline__ uint32_t pack_low_bytes(int32_t a, int32_t b, int32_t c, int32_t d) {
@@ -52,24 +59,14 @@ __device__ __forceinline__ uint32_t pack_low_bytes(int32_t a, int32_t b, int32_t
   const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000c0cu);
   return lo | hi;
 }
-// The packed word pack-act-rows stores for v.  `fast` (1/gamma finite and
-// gamma > 0) is uniform across the block.  The exact fix-up of flagged lanes
-// sits behind a wave-uniform vote, so a wave with no flagged lane skips it.
+// The packed word pack-act-rows stores for v.  `fast` (quant_fast(gamma))
+// is uniform across the block.
 __device__ __forceinline__ uint32_t quant_word(float4 v, float gamma, float ginv, bool fast) {
-  if (!fast)
+  if (__builtin_expect(!fast, 0))
     return pack_lane(v.x, gamma) | (pack_lane(v.y, gamma) << 8) | (pack_lane(v.z, gamma) << 16) |
            (pack_lane(v.w, gamma) << 24);
-  bool n0, n1, n2, n3;
-  const int32_t k0 = lane_est(v.x, ginv, n0), k1 = lane_est(v.y, ginv, n1);
-  const int32_t k2 = lane_est(v.z, ginv, n2), k3 = lane_est(v.w, ginv, n3);
-  uint32_t w = pack_low_bytes(k0, k1, k2, k3);
-  if (__builtin_amdgcn_ballot_w64(n0 || n1 || n2 || n3) != 0ull) {
-    if (n0) w = (w & 0xFFFFFF00u) | pack_lane(v.x, gamma);
-    if (n1) w = (w & 0xFFFF00FFu) | (pack_lane(v.y, gamma) << 8);
-    if (n2) w = (w & 0xFF00FFFFu) | (pack_lane(v.z, gamma) << 16);
-    if (n3) w = (w & 0x00FFFFFFu) | (pack_lane(v.w, gamma) << 24);
-  }
-  return w;
+  return pack_low_bytes(lane_q8(v.x, gamma, ginv), lane_q8(v.y, gamma, ginv), lane_q8(v.z, gamma, ginv),
+                        lane_q8(v.w, gamma, ginv));
 }
 
 // 4x4 byte transpose: X[k] holds columns 4k..4k+3 of a 16-column group;

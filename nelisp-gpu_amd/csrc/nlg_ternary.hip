@@ -55,7 +55,7 @@ __global__ __launch_bounds__(256) void k_pack_act_rows(const float *__restrict__
   const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
   const float ginv = 1.0f / g;
   if (threadIdx.x == 0) gamma[row] = g;
-  const bool fast = g > 0.0f && ginv < INFINITY;
+  const bool fast = quant_fast(g);
   uint32_t *q = xq + (size_t)row * ng;
   for (uint32_t w = threadIdx.x; w < ng; w += blockDim.x) {
     uint32_t word = 0;

@@ -144,7 +144,7 @@ __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
   amax = nlg_block_max_f32<4, true>(amax, red2);
   const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
   const float ginv = 1.0f / g;
-  const bool fast = g > 0.0f && ginv < INFINITY;
+  const bool fast = quant_fast(g);
   if (threadIdx.x == 0) a.gamma[tok] = g;
   // Lane i of a quad holds the group's word n_i (its columns 4i..4i+3) and
   // writes y_i = (n0.b_i, n1.b_i, n2.b_i, n3.b_i): byte i of each word.
@@ -155,8 +155,8 @@ __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
   for (int j = 0; j < J; j++) {
     const uint32_t f = threadIdx.x + 256u * j;
     const int n = (int)quant_word(v[j], g, ginv, fast);
-    const uint32_t n0 = (uint32_t)nlg_dpp<0x00>(n), n1 = (uint32_t)nlg_dpp<0x55>(n);
-    const uint32_t n2 = (uint32_t)nlg_dpp<0xAA>(n), n3 = (uint32_t)nlg_dpp<0xFF>(n);
+    const uint32_t n0 = nlg_qperm<0x00>((uint32_t)n), n1 = nlg_qperm<0x55>((uint32_t)n);
+    const uint32_t n2 = nlg_qperm<0xAA>((uint32_t)n), n3 = nlg_qperm<0xFF>((uint32_t)n);
     const uint32_t y = __builtin_amdgcn_perm(n1, n0, sel_lo) | __builtin_amdgcn_perm(n3, n2, sel_hi);
     if (f < nf4) dst[f] = y;
   }
