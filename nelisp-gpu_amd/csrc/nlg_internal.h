@@ -133,6 +133,13 @@ __device__ __forceinline__ uint4 nlg_ld_stream(const uint4 *p) {
   return make_uint4(t.x, t.y, t.z, t.w);
 }
 
+// A buffer resource over `bytes` bytes at p (raw, unswizzled; the gfx9
+// descriptor word 3): loads through it at offsets past the end read 0
+// instead of faulting, so edge lanes need no clamped address.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t nlg_buffer_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // A device-resident int32 that the kernel does not write (the decode
 // position), read with a scalar load from the constant address space.  Its
 // wait counts scalar loads only, so code that needs it early (RoPE table
@@ -233,6 +240,9 @@ enum {
   NLG_EPI_SWIGLU = 2,  // rows 2j, 2j+1 = gate j, up j; y[j] = silu(gate)*up
   NLG_EPI_QKV = 3,     // rows = q | k | v; RoPE on q, k; k, v appended to fp16 caches
   NLG_EPI_ARGMAX = 4,  // y = logits, plus one (max, index) per wave
+  // kernel-internal: NLG_EPI_STORE with no bias, a per-tensor beta and no
+  // gamma output (the bare linear: no per-row operand loads)
+  NLG_EPI_STORE_PLAIN = 5,
 };
 struct FusedArgs {
   const float *x;        // [seq x cols] f32 activation rows

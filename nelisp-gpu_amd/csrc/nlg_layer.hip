@@ -35,7 +35,7 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
 // F4: float4s of the activation row per thread (cols <= 1024*F4).
 template <int R, int CPL, int F4, int PRO, int EPI>
 __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
-  extern __shared__ uint4 s_xq4[];  // cols/16 uint4 = cols int8 lanes
+  extern __shared__ uint4 s_xq4[];  // 64 F4 uint4: cols int8 lanes, then the words past the row
   __shared__ float red[4], red2[4];  // the two reductions' own scratch: no reuse barrier
   // Every argument the kernel uses is pinned into SGPRs here, so they all
   // arrive with the first kernarg fetch instead of in later round trips.
@@ -43,7 +43,10 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   float *const gamma_out = a.gamma_out;
   const uint32_t ystride = a.ystride;
   asm volatile("" ::"s"(y_out), "s"(gamma_out), "s"(ystride));
-  const int lane = threadIdx.x & 63, wvi = threadIdx.x >> 6;
+  // the wave index as a scalar: row addresses then live in SGPRs and each
+  // load is one SGPR base plus the lane's offset (no 64-bit vector math
+  // ahead of the weight stream)
+  const int lane = threadIdx.x & 63, wvi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t tok = blockIdx.y;
   const uint32_t wave = blockIdx.x * 4 + wvi;
   const uint32_t row0 = wave * R;
@@ -66,6 +69,10 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   // is loaded; the fourth chunk's weight is 0 in the general form, so the
   // merged values differ at most in the sign of a zero, which quantises alike)
   constexpr bool ATT = PRO == NLG_PRO_ATTN || PRO == NLG_PRO_ATTN3;
+  // PRO_NONE: the activation is loaded already transposed (below).  The
+  // RMS and merge prologues keep float4 loads: their sums run in the batched
+  // quantiser's element order, so both forms quantise a row alike.
+  constexpr bool XPOSE_LOAD = PRO == NLG_PRO_NONE;
   constexpr int NCA = PRO == NLG_PRO_ATTN3 ? 3 : (ATT ? NLG_ATTN_MAX_CHUNKS : 1);
   float4 cx4[F4][NCA];
   float2 mz2[F4][NCA];
@@ -84,6 +91,21 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
         mz2[k][c] = *(const float2 *)(a.attn_mz + (tc * heads + h) * 2);
       }
     }
+  } else if (XPOSE_LOAD) {
+    // word f of the LDS row is byte i of the four words of its 16-column
+    // group (the dots' operand order), i.e. columns 16 (f / 4) + f % 4 + 4 m,
+    // m = 0..3: loaded in that order, the quantised bytes pack straight into
+    // it (no cross-lane transpose); the quad's four loads of a 16-column
+    // group read one 64-byte piece.  Buffer loads bounded by the row: words
+    // past it read 0 (no clamped addresses, one offset register for all)
+    const __amdgpu_buffer_rsrc_t xr = nlg_buffer_rsrc(a.x + (size_t)tok * a.cols, a.cols * 4u);
+    const int32_t xo = (int32_t)(4u * (16u * (threadIdx.x >> 2) + (threadIdx.x & 3u)));
+#pragma unroll
+    for (int k = 0; k < F4; k++)
+      xv4[k] = make_float4(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, xo, 4096 * k, 0)),
+                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, xo + 16, 4096 * k, 0)),
+                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, xo + 32, 4096 * k, 0)),
+                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xr, xo + 48, 4096 * k, 0)));
   } else {
     const float4 *x4 = (const float4 *)(a.x + (size_t)tok * a.cols);
 #pragma unroll
@@ -99,6 +121,34 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
       const uint32_t f = threadIdx.x + 256u * k;
       gv4[k] = g4[f < nf4 ? f : nf4 - 1];
     }
+  }
+  // The epilogue's operands (a few bytes per row, cache-resident) before the
+  // weight stream, which is issued last: nothing then waits behind it, and
+  // its four loads go out back to back (with these after it, the 4096^2
+  // step took 0.14 us longer).
+  const uint32_t orow_u = row0 + (lane < R ? lane : 0);
+  const uint32_t orow = orow_u < a.out ? orow_u : a.out - 1;  // every lane loads a valid row
+  const bool olive = lane < R && orow_u < a.out;
+  const float *bsrc = a.bias ? a.bias : a.beta;  // a real address either way
+  constexpr bool PLAIN = EPI == NLG_EPI_STORE_PLAIN;
+  const float bo_raw = PLAIN ? 0.0f : bsrc[a.bias ? orow : 0];
+  const float be = a.beta[PLAIN || !a.beta_per_row ? 0 : orow];
+  const float bo = a.bias && !PLAIN ? bo_raw : 0.0f;
+  float rv = 0.0f;
+  if (EPI == NLG_EPI_RESID) rv = a.res[(size_t)tok * a.rstride + orow];
+  // QKV: this lane's row is q, k or v; RoPE pair m of head dimension dd
+  float cc = 0.0f, ss = 0.0f;
+  uint32_t dd = 0, p = 0;
+  bool pos_ok = false;
+  if (EPI == NLG_EPI_QKV) {
+    const int32_t pr = pos0 + (a.qper ? (int32_t)(tok % a.qper) : 0);
+    pos_ok = pr >= 0 && (uint32_t)pr < a.max_seq;
+    p = pos_ok ? (uint32_t)pr : 0u;
+    const uint32_t sec = orow < a.nq ? orow : (orow < a.nq + a.nkv ? orow - a.nq : orow - a.nq - a.nkv);
+    dd = sec % a.hd;
+    const uint32_t half = a.hd >> 1, ci = p * half + (dd >> 1);
+    cc = a.co[ci];
+    ss = a.si[ci];  // SG[0] = +1: SI*SG is SI exactly
   }
   // Rows of at most 48 chunks (3072 columns: lanes 48..63 would idle on
   // every row) with R >= 4: G = 64/R lanes per row, lane (prow, pj)
@@ -135,35 +185,22 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
       }
     }
   }
-  const uint32_t orow_u = row0 + (lane < R ? lane : 0);
-  const uint32_t orow = orow_u < a.out ? orow_u : a.out - 1;  // every lane loads a valid row
-  const bool olive = lane < R && orow_u < a.out;
-  const float *bsrc = a.bias ? a.bias : a.beta;  // a real address either way
-  const float bo_raw = bsrc[a.bias ? orow : 0];
-  const float be = a.beta[a.beta_per_row ? orow : 0];
-  const float bo = a.bias ? bo_raw : 0.0f;
-  float rv = 0.0f;
-  if (EPI == NLG_EPI_RESID) rv = a.res[(size_t)tok * a.rstride + orow];
-  // QKV: this lane's row is q, k or v; RoPE pair m of head dimension dd
-  float cc = 0.0f, ss = 0.0f;
-  uint32_t dd = 0, p = 0;
-  bool pos_ok = false;
-  if (EPI == NLG_EPI_QKV) {
-    const int32_t pr = pos0 + (a.qper ? (int32_t)(tok % a.qper) : 0);
-    pos_ok = pr >= 0 && (uint32_t)pr < a.max_seq;
-    p = pos_ok ? (uint32_t)pr : 0u;
-    const uint32_t sec = orow < a.nq ? orow : (orow < a.nq + a.nkv ? orow - a.nq : orow - a.nq - a.nkv);
-    dd = sec % a.hd;
-    const uint32_t half = a.hd >> 1, ci = p * half + (dd >> 1);
-    cc = a.co[ci];
-    ss = a.si[ci];  // SG[0] = +1: SI*SG is SI exactly
-  }
+  // every load above issued before any of them is waited for
+  __builtin_amdgcn_sched_barrier(0);
   // Chunks past the row stay as loaded (the dots skip them): writing a
   // register whose load is in flight waits for that load, which would put
-  // the weights' HBM fetch in front of the quantisation.
+  // the weights' HBM fetch in front of the quantisation.  Activation
+  // float4s past the row (clamped repeats of the last one) change neither
+  // the absmax nor any stored word, so only the RMS sum of squares needs
+  // them zeroed -- by selects: a conditional block here made the wait-count
+  // pass drain loads at its join (0.11 us of the 4096^2 step).
+  if (PRO == NLG_PRO_RMS) {
 #pragma unroll
-  for (int k = 0; k < F4; k++)
-    if (threadIdx.x + 256u * k >= nf4) xv4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int k = 0; k < F4; k++) {
+      const bool in = threadIdx.x + 256u * k < nf4;
+      xv4[k] = make_float4(in ? xv4[k].x : 0.0f, in ? xv4[k].y : 0.0f, in ? xv4[k].z : 0.0f, in ? xv4[k].w : 0.0f);
+    }
+  }
   // 2a. attention merge: x = sum_c ctx_c*exp(m_c - M) / sum_c z_c*exp(m_c - M)
   //     in k_attn_merge's exact operation order, so the two agree bit for bit
   if (ATT) {
@@ -184,7 +221,6 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
         acc.w = fmaf(cx4[k][c].w, sc, acc.w);
       }
       xv4[k] = make_float4(acc.x / zz, acc.y / zz, acc.z / zz, acc.w / zz);
-      if (threadIdx.x + 256u * k >= nf4) xv4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
   }
   // 2. RMSNorm: S = 1/sqrt(sum(x*x)/N + eps); C = (X*S)*G
@@ -219,9 +255,9 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
     t = dsl_abs(xv4[k].w); amax = t > amax ? t : amax;
   }
   amax = nlg_block_max_f32<4, true>(amax, red2);
-  const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
+  const float g = nlg_gamma_of(__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))));
   const float ginv = 1.0f / g;
-  if (gamma_out && blockIdx.x == 0 && threadIdx.x == 0) gamma_out[tok] = g;
+  if (EPI != NLG_EPI_STORE_PLAIN && gamma_out && blockIdx.x == 0 && threadIdx.x == 0) gamma_out[tok] = g;
   // 4. quantise into LDS, one packed word per float4 (exact; see lane_est),
   //    stored already in the dots' operand order: a 16-column group's four
   //    words sit in the four lanes of a quad, and lane i keeps byte i of
@@ -230,13 +266,19 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   uint32_t *s_xq = (uint32_t *)s_xq4;
   const uint32_t qi = threadIdx.x & 3u;
   const uint32_t sel_lo = 0x0c0c0000u | ((4u + qi) << 8) | qi, sel_hi = 0x00000c0cu | ((4u + qi) << 24) | (qi << 16);
+  uint32_t qw[F4];
+  quant_words<F4>(xv4, g, ginv, fast, qw);
 #pragma unroll
   for (int k = 0; k < F4; k++) {
     const uint32_t f = threadIdx.x + 256u * k;
-    const int wd = (int)quant_word(xv4[k], g, ginv, fast);
-    const uint32_t n0 = nlg_qperm<0x00>((uint32_t)wd), n1 = nlg_qperm<0x55>((uint32_t)wd);
-    const uint32_t n2 = nlg_qperm<0xAA>((uint32_t)wd), n3 = nlg_qperm<0xFF>((uint32_t)wd);
-    if (f < nf4) s_xq[f] = __builtin_amdgcn_perm(n1, n0, sel_lo) | __builtin_amdgcn_perm(n3, n2, sel_hi);
+    const uint32_t wd = qw[k];
+    if (XPOSE_LOAD) {
+      s_xq[f] = wd;
+    } else {
+      const uint32_t n0 = nlg_qperm<0x00>(wd), n1 = nlg_qperm<0x55>(wd);
+      const uint32_t n2 = nlg_qperm<0xAA>(wd), n3 = nlg_qperm<0xFF>(wd);
+      s_xq[f] = __builtin_amdgcn_perm(n1, n0, sel_lo) | __builtin_amdgcn_perm(n3, n2, sel_hi);
+    }
   }
   __syncthreads();
   if (row0 >= a.out) return;  // wave-uniform, after the last barrier
@@ -296,7 +338,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   }
   // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
   const float val = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, g), (float)(tl >> 6)));
-  if (EPI == NLG_EPI_STORE || EPI == NLG_EPI_ARGMAX) {
+  if (EPI == NLG_EPI_STORE || EPI == NLG_EPI_STORE_PLAIN || EPI == NLG_EPI_ARGMAX) {
     if (olive) y_out[(size_t)tok * ystride + orow] = val;
   }
   if (EPI == NLG_EPI_RESID) {
@@ -365,13 +407,16 @@ int nlg_fused_rows_per_wave(uint32_t out, int epi) {
 // thread together (cols = 64 x chunks x CPL; cols <= 1024 x F4), so only the
 // five pairs a row length can give are instantiated.
 template <int PRO, int EPI, int R>
-static void fused_go(const FusedArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+// The LDS row holds every word a thread quantises (256 F4 words, 1024 F4
+// bytes): the words past the row are stored too (never read), so the
+// stores need no per-thread condition.
+static void fused_go(const FusedArgs &a, dim3 grid, hipStream_t st) {
   const dim3 blk(256);
-  if (a.cols <= 2048) hipLaunchKernelGGL((k_tern_fused<R, 1, 2, PRO, EPI>), grid, blk, lds, st, a);
-  else if (a.cols <= 3072) hipLaunchKernelGGL((k_tern_fused<R, 1, 3, PRO, EPI>), grid, blk, lds, st, a);
-  else if (a.cols <= 4096) hipLaunchKernelGGL((k_tern_fused<R, 1, 4, PRO, EPI>), grid, blk, lds, st, a);
-  else if (a.cols <= 8192) hipLaunchKernelGGL((k_tern_fused<R, 2, 8, PRO, EPI>), grid, blk, lds, st, a);
-  else hipLaunchKernelGGL((k_tern_fused<R, 4, 16, PRO, EPI>), grid, blk, lds, st, a);
+  if (a.cols <= 2048) hipLaunchKernelGGL((k_tern_fused<R, 1, 2, PRO, EPI>), grid, blk, 2048, st, a);
+  else if (a.cols <= 3072) hipLaunchKernelGGL((k_tern_fused<R, 1, 3, PRO, EPI>), grid, blk, 3072, st, a);
+  else if (a.cols <= 4096) hipLaunchKernelGGL((k_tern_fused<R, 1, 4, PRO, EPI>), grid, blk, 4096, st, a);
+  else if (a.cols <= 8192) hipLaunchKernelGGL((k_tern_fused<R, 2, 8, PRO, EPI>), grid, blk, 8192, st, a);
+  else hipLaunchKernelGGL((k_tern_fused<R, 4, 16, PRO, EPI>), grid, blk, 16384, st, a);
 }
 
 uint32_t nlg_argmax_parts(uint32_t seq, uint32_t cols, uint32_t out) {
@@ -393,29 +438,30 @@ int nlg_fused_launch(const FusedArgs &a0, int pro, int epi, int rpw, hipStream_t
   if (rpw <= 0) rpw = nlg_fused_rows_per_wave(a.out, epi);
   if ((epi == NLG_EPI_SWIGLU || epi == NLG_EPI_QKV) && (rpw < 2 || a.out % 2))
     return nlg_fail("fused ternary linear: paired epilogues need an even row count");
-  const size_t lds = (size_t)a.cols;  // one byte per column
   const dim3 grid(nlg_blocks(a.out, 4u * rpw), a.seq);
   // one (max, index) per wave that has rows
   if (epi == NLG_EPI_ARGMAX) a.nparts = (a.out + rpw - 1) / rpw;
 #define PE(P, E)                                          \
   do {                                                    \
     switch (rpw) {                                        \
-      case 1: fused_go<P, E, 1>(a, grid, lds, st); break; \
-      case 2: fused_go<P, E, 2>(a, grid, lds, st); break; \
-      case 8: fused_go<P, E, 8>(a, grid, lds, st); break; \
-      default: fused_go<P, E, 4>(a, grid, lds, st); break; \
+      case 1: fused_go<P, E, 1>(a, grid, st); break; \
+      case 2: fused_go<P, E, 2>(a, grid, st); break; \
+      case 8: fused_go<P, E, 8>(a, grid, st); break; \
+      default: fused_go<P, E, 4>(a, grid, st); break; \
     }                                                     \
   } while (0)
   if (rpw != 1 && rpw != 2 && rpw != 4 && rpw != 8 && !(rpw == 16 && epi == NLG_EPI_ARGMAX))
     return nlg_fail("rows_per_wave must be 1, 2, 4 or 8 (or 16 for an argmax)");
-  if (pro == NLG_PRO_NONE && epi == NLG_EPI_STORE) PE(NLG_PRO_NONE, NLG_EPI_STORE);
+  if (pro == NLG_PRO_NONE && epi == NLG_EPI_STORE && !a.bias && !a.beta_per_row && !a.gamma_out)
+    PE(NLG_PRO_NONE, NLG_EPI_STORE_PLAIN);
+  else if (pro == NLG_PRO_NONE && epi == NLG_EPI_STORE) PE(NLG_PRO_NONE, NLG_EPI_STORE);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_STORE) PE(NLG_PRO_RMS, NLG_EPI_STORE);
   else if (pro == NLG_PRO_NONE && epi == NLG_EPI_RESID) PE(NLG_PRO_NONE, NLG_EPI_RESID);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_SWIGLU) PE(NLG_PRO_RMS, NLG_EPI_SWIGLU);
   else if (pro == NLG_PRO_NONE && epi == NLG_EPI_SWIGLU) PE(NLG_PRO_NONE, NLG_EPI_SWIGLU);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_QKV) PE(NLG_PRO_RMS, NLG_EPI_QKV);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_ARGMAX) {
-    if (rpw == 16) fused_go<NLG_PRO_RMS, NLG_EPI_ARGMAX, 16>(a, grid, lds, st);
+    if (rpw == 16) fused_go<NLG_PRO_RMS, NLG_EPI_ARGMAX, 16>(a, grid, st);
     else PE(NLG_PRO_RMS, NLG_EPI_ARGMAX);
   }
   else if (pro == NLG_PRO_ATTN && epi == NLG_EPI_RESID) {

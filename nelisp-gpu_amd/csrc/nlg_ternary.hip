@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void k_pack_act_rows(const float *__restrict__
     }
   }
   amax = nlg_block_max_f32(amax, red);
-  const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
+  const float g = nlg_gamma_of(__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))));
   const float ginv = 1.0f / g;
   if (threadIdx.x == 0) gamma[row] = g;
   const bool fast = quant_fast(g);

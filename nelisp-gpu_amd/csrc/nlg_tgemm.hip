@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
     t = dsl_abs(v[j].w); amax = t > amax ? t : amax;
   }
   amax = nlg_block_max_f32<4, true>(amax, red2);
-  const float g = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))) / 127.0f;
+  const float g = nlg_gamma_of(__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))));
   const float ginv = 1.0f / g;
   const bool fast = quant_fast(g);
   if (threadIdx.x == 0) a.gamma[tok] = g;
@@ -151,12 +151,13 @@ __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
   const uint32_t i = threadIdx.x & 3u;
   const uint32_t sel_lo = 0x0c0c0000u | ((4u + i) << 8) | i, sel_hi = 0x00000c0cu | ((4u + i) << 24) | (i << 16);
   uint32_t *dst = (uint32_t *)(a.xq + (size_t)tok * a.cols);
+  uint32_t qw[J];
+  quant_words<J>(v, g, ginv, fast, qw);
 #pragma unroll
   for (int j = 0; j < J; j++) {
     const uint32_t f = threadIdx.x + 256u * j;
-    const int n = (int)quant_word(v[j], g, ginv, fast);
-    const uint32_t n0 = nlg_qperm<0x00>((uint32_t)n), n1 = nlg_qperm<0x55>((uint32_t)n);
-    const uint32_t n2 = nlg_qperm<0xAA>((uint32_t)n), n3 = nlg_qperm<0xFF>((uint32_t)n);
+    const uint32_t n0 = nlg_qperm<0x00>(qw[j]), n1 = nlg_qperm<0x55>(qw[j]);
+    const uint32_t n2 = nlg_qperm<0xAA>(qw[j]), n3 = nlg_qperm<0xFF>(qw[j]);
     const uint32_t y = __builtin_amdgcn_perm(n1, n0, sel_lo) | __builtin_amdgcn_perm(n3, n2, sel_hi);
     if (f < nf4) dst[f] = y;
   }

@@ -4,7 +4,8 @@ rounding (pack-act-rows, lisp/nelisp-gpu-kernels.el:912-926:
 q = RN(v/g), ri = min(trunc(RN(|q| + 0.5)), 127), byte = ri or
 (256 - ri) % 256 when q < 0), both restated in numpy.
 
-The kernels divide once per row (y = RN(1/g)) and per element take
+The kernels form g = RN(amax/127) (itself by one correction step of the
+constant RN(1/127)) and y = RN(1/g) once per row, and per element take
 q0 = RN(v*y), r = fma(-q0, g, v), q = fma(r, y, q0) -- one correction step
 of the reciprocal product -- then trunc(RN(q + copysign(0.5, v))) clamped to
 +-127.  The claim under test is that q is exactly the correctly rounded
@@ -126,6 +127,33 @@ def test_special_values():
     check(np.array([190 * step, step, 0, -3 * step], f32), step)
     check(np.array([1.0, -1.0, 0.0], f32), f32(np.inf))  # amax = inf
     check(np.array([1.0, -1.0, 0.0], f32), f32(0.0))  # all-zero row: gamma 0
+
+
+def kernel_gamma(amax):
+    """nlg_gamma_of: RN(amax / 127) by the same correction step with the
+    constant y = RN(1/127); amax below 2^-90 (or not finite) divides."""
+    amax = np.asarray(amax, f32)
+    y = (f32(1.0) / f32(127.0)).astype(f32)
+    with np.errstate(all="ignore"):
+        q0 = (amax * y).astype(f32)
+        fast = fmaf(fmaf(-q0, f32(127.0), amax), y, q0)
+        slow = (amax / f32(127.0)).astype(f32)
+    return np.where((amax >= FAST_MIN) & np.isfinite(amax), fast, slow)
+
+
+def test_gamma_is_the_ieee_division():
+    """Every significand at two exponents, and random values at every
+    exponent from 2^-149 to 2^127, against float32 amax / 127."""
+    sig = np.arange(1 << 23, dtype=np.uint32)
+    for e in (127, 127 + 60):  # amax in [1, 2) and [2^60, 2^61)
+        amax = ((np.uint32(e) << 23) | sig).view(f32)
+        with np.errstate(all="ignore"):
+            assert np.array_equal(kernel_gamma(amax), (amax / f32(127.0)).astype(f32))
+    rng = np.random.default_rng(5)
+    bits = rng.integers(0, 0x7F800000, 4_000_000, dtype=np.uint32)  # every finite positive float
+    amax = bits.view(f32)
+    with np.errstate(all="ignore"):
+        assert np.array_equal(kernel_gamma(amax), (amax / f32(127.0)).astype(f32))
 
 
 def test_without_the_correction_step_bytes_flip():
