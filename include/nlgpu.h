@@ -74,6 +74,8 @@ int nlg_upload_file(void *dev_dst, const char *path, uint64_t offset, size_t byt
                     size_t *missing);
 
 void *nlg_stream_create(void);
+/* Waits for the stream, releases the scratch the batched linears keep per
+ * stream, and destroys it (a graph captured on it must not run afterwards). */
 int nlg_stream_destroy(void *stream);
 int nlg_stream_sync(void *stream);
 /* The library's default stream (what NULL means). */
@@ -394,6 +396,22 @@ int nlg_prefill_attn_f16(const float *q, const uint16_t *kcache, const uint16_t 
                          const int32_t *pos, uint32_t rows, uint32_t qper, uint32_t heads,
                          uint32_t kvheads, uint32_t head_dim, uint32_t max_seq, float *ctx,
                          void *stream);
+/* That attention and the attention output projection with its residual:
+ * y = res + linear(ctx) over rows x heads*head_dim (out rows of w2), the
+ * prompt's counterpart of nlg_attn_ternary_linear_residual.  When the keys
+ * are split (few prompts), the pieces are merged and quantised for the
+ * projection in one launch; otherwise ctx_ws ([rows][heads*head_dim] f32)
+ * receives the context on the way.  Bit-identical to nlg_prefill_attn_f16
+ * followed by nlg_ternary_linear_residual.  The reference runs a prompt as
+ * attn-causal-gqa, pack-act-rows, bitlinear-dp4a-1f and add2
+ * (kernels.el:934-990, :884-932, :619-634, :812-821). */
+int nlg_prefill_attn_ternary_linear_residual(const float *q, const uint16_t *kcache,
+                                             const uint16_t *vcache, const int32_t *pos, uint32_t rows,
+                                             uint32_t qper, uint32_t heads, uint32_t kvheads,
+                                             uint32_t head_dim, uint32_t max_seq, float *ctx_ws,
+                                             const uint32_t *w2, const float *bias, const float *beta,
+                                             int beta_per_row, const float *res, float *y, uint32_t out,
+                                             void *stream);
 
 /* Weight ingest: the reference's other ternary formats repacked into the
  * 2-bit layout of ternary-rows (kernels.el:700-746) that every ternary entry
@@ -417,8 +435,13 @@ int nlg_repack_packed_to_2bit(const float *wpk, uint32_t out, uint32_t cols, uin
  * GEMM's load order (the same words; each wave then loads 1 KiB runs
  * instead of 32-byte pieces of 32 rows), which every linear given this w2
  * pointer with the same rows and cols at 4+ tokens reads instead.  The
- * copy is taken when this is called (it waits for `stream`): register
- * again after changing the weights, and unregister before freeing w2.
+ * copy is taken when this is called (it waits for `stream`).  Writes into
+ * registered weights through this library -- nlg_upload, nlg_upload_file,
+ * nlg_copy_d2d, nlg_zero, the repacks above -- refresh the copy in stream
+ * order after the write (in place, so captured graphs see it); nlg_free of
+ * the allocation holding w2 drops the registration.  Weights changed any
+ * other way (a kernel of the caller's, a dispatch by name) need
+ * nlg_ternary_tiled_register again, which refreshes the copy in place.
  * Results are bit-identical to the row layout's.  Costs rows (rounded up
  * to 32) x cols/4 bytes of device memory. */
 int nlg_ternary_tiled_register(const uint32_t *w2, uint32_t rows, uint32_t cols, void *stream);
@@ -468,6 +491,12 @@ int nlg_stack_step(nlg_stack *s, uint32_t steps, int use_graph);
  * composition; the reference has no counterpart (its model code runs the
  * named kernels from Lisp and can read any buffer back). */
 int nlg_stack_step_trace(nlg_stack *s, float *xs);
+/* nlg_stack_prefill that also writes the prompt rows' residual stream to xs
+ * (host, [layers + 1][batch x n_prompt][d_model]: the embedded prompt rows,
+ * then the rows after each layer; row z = sequence z / n_prompt, position
+ * z % n_prompt), so that each layer of a prefill can be checked on its own
+ * against the reference kernels (kernels.el:934-990, :340-365, :1249-1265). */
+int nlg_stack_prefill_trace(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt, float *xs);
 /* Current position (tokens consumed per sequence). */
 int nlg_stack_position(nlg_stack *s, uint32_t *pos);
 /* Token history [batch x max_seq] (prompt, then generated; -1 unwritten) and
@@ -477,7 +506,13 @@ int nlg_stack_tokens(nlg_stack *s, int32_t *tokens, int32_t *greedy);
 int nlg_stack_logits(nlg_stack *s, float *logits);
 /* Device pointer and size of a named tensor ("wqkv", "bqkv", "wo", "bo",
  * "wgu", "bgu", "wd", "bd", "gattn", "gffn", "kc", "vc" with a layer;
- * "wlm", "blm", "gfinal", "emb", "rope_cos", "rope_sin", "x" with layer -1). */
+ * "wlm", "blm", "gfinal", "emb", "rope_cos", "rope_sin", "x" with layer -1).
+ * The tensors may be written.  The matrix-core linears (4+ rows) of a stack
+ * read tiled copies of the 2-bit weights (wqkv, wo, wgu, wd, wlm); handing
+ * out one of those pointers makes the next prefill / step / step trace
+ * refresh the copies from the weights first, so weights written between
+ * this call and that one are what every path computes with.  To write them
+ * again after a step, ask for the pointer again. */
 int nlg_stack_tensor(nlg_stack *s, const char *name, int layer, void **ptr, size_t *bytes);
 
 #ifdef __cplusplus

@@ -230,10 +230,19 @@ int nlg_attn_chunks(const float *q, const uint16_t *kc, const uint16_t *vc, cons
 // the merged context quantised for the output projection in xq ([rows x
 // heads*head_dim] int8 in matrix-core order) and gamma ([rows]) instead of
 // ctx, and sets *quantized; otherwise ctx is written as without them.
+// pos_bound (0: none) bounds the positions any row attends (pos[0] + qper
+// when the caller knows pos[0]), which sizes the split form's workspace.
 int nlg_prefill_attn(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *pos, uint32_t rows,
                      uint32_t qper, uint32_t heads, uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
                      float *ctx, hipStream_t st, uint8_t *xq = nullptr, float *gamma = nullptr,
-                     bool *quantized = nullptr);
+                     bool *quantized = nullptr, uint32_t pos_bound = 0);
+// Prompt attention + output projection + residual (the stack's prefill
+// form; nlg_prefill_attn_ternary_linear_residual in the C ABI).
+int nlg_prefill_attn_o_resid(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *pos,
+                             uint32_t rows, uint32_t qper, uint32_t heads, uint32_t kvheads, uint32_t head_dim,
+                             uint32_t max_seq, uint32_t pos_bound, float *ctx_ws, const uint32_t *w2,
+                             const float *bias, const float *beta, int beta_per_row, const float *res, float *y,
+                             uint32_t out, hipStream_t st);
 enum {
   NLG_EPI_STORE = 0,   // y = bias + (beta*gamma)*acc
   NLG_EPI_RESID = 1,   // y = res + that
@@ -316,6 +325,10 @@ void *nlg_noalloc_scratch(void);
 const uint32_t *nlg_tiled_find(const uint32_t *w2, uint32_t rows, uint32_t cols);
 size_t nlg_tiled_bytes(uint32_t rows, uint32_t cols);
 void nlg_tiled_release_all(void);
+// Refresh (in stream order) the copies of registrations overlapping a write
+// of `bytes` at dst; drop those registered inside memory being freed.
+void nlg_tiled_refresh_range(const void *dst, size_t bytes, hipStream_t st);
+void nlg_tiled_drop_range(const void *base, size_t bytes);
 // Bytes the batched form needs for seq tokens of cols columns.
 size_t nlg_batched_scratch_bytes(uint32_t seq, uint32_t cols);
 // The rows-per-wave the launcher uses for `out` rows in mode `epi`.

@@ -389,7 +389,7 @@ __global__ __launch_bounds__(256) void k_prefill_merge_q(PrefillArgs a, uint32_t
 
 int nlg_prefill_attn(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *pos, uint32_t rows,
                      uint32_t qper, uint32_t heads, uint32_t kvheads, uint32_t head_dim, uint32_t max_seq,
-                     float *ctx, hipStream_t st, uint8_t *xq, float *gamma, bool *quantized) {
+                     float *ctx, hipStream_t st, uint8_t *xq, float *gamma, bool *quantized, uint32_t pos_bound) {
   if (quantized) *quantized = false;
   if (!rows) return NLG_OK;
   if (!q || !kc || !vc || !pos || !ctx) return nlg_fail("prefill attn: null pointer");
@@ -417,7 +417,11 @@ int nlg_prefill_attn(const float *q, const uint16_t *kc, const uint16_t *vc, con
   // unsplit 27.2).  The pieces' partials go to a per-stream workspace;
   // without one (a capture that would have to grow it) the launch stays
   // unsplit.
-  const uint32_t kblocks = (max_seq + PA_KB - 1) / PA_KB, kps = nqb / 2 + nqb % 2 > 4 ? nqb / 2 + nqb % 2 : 4;
+  // Keys reach at most the last prompt position: max_seq, or pos_bound when
+  // the caller knows a smaller bound (the stack: the prompt length), which
+  // sizes the pieces' workspace by the prompt instead of the cache.
+  const uint32_t kreach = pos_bound && pos_bound < max_seq ? pos_bound : max_seq;
+  const uint32_t kblocks = (kreach + PA_KB - 1) / PA_KB, kps = nqb / 2 + nqb % 2 > 4 ? nqb / 2 + nqb % 2 : 4;
   if ((uint64_t)nqb * kvheads * nseq < 256 && kblocks > kps) {
     const uint32_t maxp = (kblocks + kps - 1) / kps;
     const size_t o_bytes = (size_t)maxp * rows * a.nq * 4, ml_bytes = (size_t)maxp * rows * heads * 2 * 4;
@@ -477,4 +481,43 @@ extern "C" int nlg_prefill_attn_f16(const float *q, const uint16_t *kcache, cons
   if (nlg_ensure_init()) return NLG_ERR;
   return nlg_prefill_attn(q, kcache, vcache, pos, rows, qper, heads, kvheads, head_dim, max_seq, ctx,
                           nlg_stream(stream));
+}
+
+// Prompt attention and the attention output projection with its residual,
+// as the stack's prefill runs them: when the keys are split (few prompts),
+// the pieces are merged and quantised for the projection in one launch
+// (k_prefill_merge_q) and the projection's GEMM reads those int8 rows;
+// otherwise ctx_ws receives the context and the projection quantises it.
+// Both give the bits of nlg_prefill_attn_f16 followed by
+// nlg_ternary_linear_residual.
+int nlg_prefill_attn_o_resid(const float *q, const uint16_t *kc, const uint16_t *vc, const int32_t *pos,
+                             uint32_t rows, uint32_t qper, uint32_t heads, uint32_t kvheads, uint32_t head_dim,
+                             uint32_t max_seq, uint32_t pos_bound, float *ctx_ws, const uint32_t *w2,
+                             const float *bias, const float *beta, int beta_per_row, const float *res, float *y,
+                             uint32_t out, hipStream_t st) {
+  const uint32_t nq = heads * head_dim;
+  uint8_t *oq = rows >= NLG_BATCHED_MIN && nq % 256 == 0 ? (uint8_t *)nlg_scratch(nlg_batched_scratch_bytes(rows, nq), st)
+                                                        : nullptr;
+  float *og = oq ? (float *)(oq + ((size_t)rows * nq + 255) / 256 * 256) : nullptr;
+  bool quantized = false;
+  if (nlg_prefill_attn(q, kc, vc, pos, rows, qper, heads, kvheads, head_dim, max_seq, ctx_ws, st, oq, og, &quantized,
+                       pos_bound))
+    return NLG_ERR;
+  FusedArgs o{};
+  o.x = ctx_ws; o.w2 = w2; o.bias = bias; o.beta = beta; o.beta_per_row = beta_per_row; o.seq = rows; o.out = out;
+  o.cols = nq; o.y = y; o.ystride = out; o.res = res; o.rstride = out;
+  return quantized ? nlg_batched_gemm(o, oq, og, NLG_EPI_RESID, st) : nlg_fused_launch(o, NLG_PRO_NONE, NLG_EPI_RESID, 0, st);
+}
+
+extern "C" int nlg_prefill_attn_ternary_linear_residual(const float *q, const uint16_t *kcache,
+                                                        const uint16_t *vcache, const int32_t *pos, uint32_t rows,
+                                                        uint32_t qper, uint32_t heads, uint32_t kvheads,
+                                                        uint32_t head_dim, uint32_t max_seq, float *ctx_ws,
+                                                        const uint32_t *w2, const float *bias, const float *beta,
+                                                        int beta_per_row, const float *res, float *y, uint32_t out,
+                                                        void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!w2 || !beta || !res || !y) return nlg_fail("prefill attn + projection: null pointer");
+  return nlg_prefill_attn_o_resid(q, kcache, vcache, pos, rows, qper, heads, kvheads, head_dim, max_seq, 0, ctx_ws,
+                                  w2, bias, beta, beta_per_row, res, y, out, nlg_stream(stream));
 }

@@ -167,6 +167,8 @@ extern "C" int nlg_repack_i8_to_2bit(const uint32_t *wp, uint32_t out, uint32_t 
   else
     hipLaunchKernelGGL(k_repack_i8<false>, grid, blk, 0, nlg_stream(stream), wp, out, cols, ng, wng, w2, nbad);
   NLG_LAUNCHED("repack int8 lanes to 2-bit");
+  nlg_tiled_refresh_range(w2, (size_t)out * ((cols + 15) / 16) * 4, nlg_stream(stream));
+  NLG_LAUNCHED("tiled-copy refresh");
   return NLG_OK;
 }
 
@@ -193,6 +195,8 @@ extern "C" int nlg_repack_packed_to_2bit(const float *wpk, uint32_t out, uint32_
   else
     hipLaunchKernelGGL(k_repack_packed<16>, grid, blk, 0, nlg_stream(stream), wpk, out, cols, pk, fcount, wng, w2, nbad);
   NLG_LAUNCHED("repack base-4 codes to 2-bit");
+  nlg_tiled_refresh_range(w2, (size_t)out * wng * 4, nlg_stream(stream));
+  NLG_LAUNCHED("tiled-copy refresh");
   return NLG_OK;
 }
 
@@ -227,6 +231,7 @@ __global__ __launch_bounds__(256) void k_tile_2bit(const uint32_t *w2, uint32_t 
 struct TiledCopy {
   uint32_t rows, cols;
   uint32_t *wt;
+  size_t bytes() const { return (size_t)rows * (cols / 16) * 4; }  // the row layout it copies
 };
 std::mutex g_tiled_mu;
 std::unordered_map<const uint32_t *, TiledCopy> g_tiled;
@@ -241,6 +246,41 @@ const uint32_t *nlg_tiled_find(const uint32_t *w2, uint32_t rows, uint32_t cols)
   std::lock_guard<std::mutex> lk(g_tiled_mu);
   const auto it = g_tiled.find(w2);
   return it != g_tiled.end() && it->second.rows == rows && it->second.cols == cols ? it->second.wt : nullptr;
+}
+
+// Writes into registered weights through the library (uploads, device
+// copies, fills, repacks) refresh the copies they touch, in stream order
+// after the write, in place (a captured graph keeps reading the same copy).
+void nlg_tiled_refresh_range(const void *dst, size_t bytes, hipStream_t st) {
+  if (!bytes || !__atomic_load_n(&g_tiled_n, __ATOMIC_RELAXED)) return;
+  const uintptr_t lo = (uintptr_t)dst, hi = lo + bytes;
+  std::lock_guard<std::mutex> lk(g_tiled_mu);
+  for (auto &kv : g_tiled) {
+    const uintptr_t a = (uintptr_t)kv.first, b = a + kv.second.bytes();
+    if (a >= hi || b <= lo) continue;
+    const uint32_t nch = kv.second.cols / 256;
+    const uint64_t nunits = nlg_tiled_bytes(kv.second.rows, kv.second.cols) / 16;
+    hipLaunchKernelGGL(k_tile_2bit, dim3((unsigned)((nunits + 255) / 256)), dim3(256), 0, st, kv.first,
+                       kv.second.rows, kv.second.cols / 16, nch, nunits, (uint4 *)kv.second.wt);
+  }
+}
+
+// Freeing device memory drops the copies of every registration inside it
+// (a later allocation at the same address must not meet a stale copy).
+void nlg_tiled_drop_range(const void *base, size_t bytes) {
+  if (!__atomic_load_n(&g_tiled_n, __ATOMIC_RELAXED)) return;
+  const uintptr_t lo = (uintptr_t)base, hi = lo + (bytes ? bytes : 1);
+  std::lock_guard<std::mutex> lk(g_tiled_mu);
+  for (auto it = g_tiled.begin(); it != g_tiled.end();) {
+    const uintptr_t a = (uintptr_t)it->first;
+    if (a >= lo && a < hi) {
+      (void)hipFree(it->second.wt);
+      it = g_tiled.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  __atomic_store_n(&g_tiled_n, g_tiled.size(), __ATOMIC_RELAXED);
 }
 
 void nlg_tiled_release_all(void) {

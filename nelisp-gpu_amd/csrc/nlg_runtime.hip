@@ -185,6 +185,8 @@ __global__ void k_zero(uint4 *p, uint64_t n16, uint8_t *tail, uint32_t ntail) {
 extern "C" int nlg_zero(void *dev, size_t bytes, void *stream) {
   if (nlg_ensure_init()) return NLG_ERR;
   if (!bytes) return NLG_OK;
+  void *const dst0 = dev;
+  const size_t bytes0 = bytes;
   // fast path needs 16-byte alignment; hipMalloc gives 256
   uintptr_t a = (uintptr_t)dev;
   if (a & 15) {
@@ -203,6 +205,8 @@ extern "C" int nlg_zero(void *dev, size_t bytes, void *stream) {
   hipLaunchKernelGGL(k_zero, dim3(grid), dim3(256), 0, nlg_stream(stream), (uint4 *)dev, n16,
                      (uint8_t *)dev + n16 * 16, tail);
   NLG_LAUNCHED("zero");
+  nlg_tiled_refresh_range(dst0, bytes0, nlg_stream(stream));
+  NLG_LAUNCHED("tiled-copy refresh");
   return NLG_OK;
 }
 
@@ -224,6 +228,13 @@ extern "C" void *nlg_malloc(size_t bytes) {
 
 extern "C" int nlg_free(void *dev) {
   if (!dev) return NLG_OK;
+  // registrations of tiled weight copies inside this allocation go with it
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)dev) == hipSuccess && base)
+    nlg_tiled_drop_range((const void *)base, size);
+  else
+    nlg_tiled_drop_range(dev, 1);
   NLG_HIP(hipFree(dev));
   return NLG_OK;
 }
@@ -233,6 +244,8 @@ extern "C" int nlg_upload(void *dst, const void *src, size_t bytes) {
   if (!bytes) return NLG_OK;
   NLG_HIP(hipStreamSynchronize(g_stream));
   NLG_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  nlg_tiled_refresh_range(dst, bytes, g_stream);
+  NLG_LAUNCHED("tiled-copy refresh");
   return NLG_OK;
 }
 
@@ -248,6 +261,8 @@ extern "C" int nlg_copy_d2d(void *dst, const void *src, size_t bytes, void *stre
   if (nlg_ensure_init()) return NLG_ERR;
   if (!bytes) return NLG_OK;
   NLG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, nlg_stream(stream)));
+  nlg_tiled_refresh_range(dst, bytes, nlg_stream(stream));
+  NLG_LAUNCHED("tiled-copy refresh");
   return NLG_OK;
 }
 
@@ -296,6 +311,8 @@ extern "C" int nlg_upload_file(void *dst, const char *path, uint64_t offset, siz
   if (short_by && done < bytes) {
     // the rest of the destination stays as nlg_malloc left it (zero)
   }
+  nlg_tiled_refresh_range(dst, done, g_stream);
+  NLG_LAUNCHED("tiled-copy refresh");
   NLG_HIP(hipStreamSynchronize(g_stream));
   if (missing) *missing = short_by;
   return NLG_OK;
@@ -311,8 +328,24 @@ extern "C" void *nlg_stream_create(void) {
   }
   return (void *)s;
 }
+// Destroying a stream releases the batched-linear scratch the library keeps
+// for it (after the stream's work is done); a graph captured on the stream
+// must not be launched afterwards.
 extern "C" int nlg_stream_destroy(void *s) {
-  if (s) NLG_HIP(hipStreamDestroy((hipStream_t)s));
+  if (!s) return NLG_OK;
+  NLG_HIP(hipStreamSynchronize((hipStream_t)s));
+  {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    for (auto it = g_scratch.begin(); it != g_scratch.end();) {
+      if (it->first.first == (hipStream_t)s) {
+        for (void *p : it->second.bufs) (void)hipFree(p);
+        it = g_scratch.erase(it);
+      } else {
+        ++it;
+      }
+    }
+  }
+  NLG_HIP(hipStreamDestroy((hipStream_t)s));
   return NLG_OK;
 }
 extern "C" int nlg_stream_sync(void *s) {

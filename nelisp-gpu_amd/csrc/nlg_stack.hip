@@ -220,6 +220,9 @@ struct nlg_stack {
   size_t pattn_ws_bytes;
   uint32_t pcap;
   bool tiled;  // prompt-order copies of the layer weights registered
+  // a weight pointer was handed out (nlg_stack_tensor): the next prefill or
+  // step refreshes the tiled copies from the row layout first
+  bool retile;
   void *graph;
   uint32_t host_pos;
   bool started;
@@ -425,11 +428,14 @@ static int stack_head(nlg_stack *s);
 // The matrix-core GEMMs (4+ rows: prompts, and every step at batch >= 4)
 // read tiled copies of the layer weights, and of the LM head when it runs
 // on 4+ rows (batch >= 4): one more copy of them, made once.
+// Registering again refreshes a copy in place (same buffers: the captured
+// step graph keeps reading them).
 static int stack_tile(nlg_stack *s) {
-  if (s->tiled) return NLG_OK;
+  if (s->tiled && !s->retile) return NLG_OK;
   const nlg_stack_config &c = s->c;
   const uint32_t d = c.d_model, f = c.d_ff, qkv = s->nq + 2 * s->nkv;
   s->tiled = true;
+  s->retile = false;
   for (Layer &y : s->L) {
     if ((d % 256 == 0 && (nlg_ternary_tiled_register(y.wqkv, qkv, d, nullptr) ||
                           nlg_ternary_tiled_register(y.wgu, 2 * f, d, nullptr))) ||
@@ -535,7 +541,9 @@ static int upload_prompt(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt
   return NLG_OK;
 }
 
-extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt) {
+// trace (device, may be null): the prompt rows' residual stream before
+// layer 0 and after every layer, [layers + 1][batch x n_prompt][d_model].
+static int stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt, float *trace) {
   if (!s || !prompts) return nlg_fail("stack prefill: null argument");
   const nlg_stack_config &c = s->c;
   const uint32_t d = c.d_model, f = c.d_ff, B = c.batch, P = n_prompt;
@@ -556,10 +564,12 @@ extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t 
     if (!s->px || !s->pq || !s->ph || !s->pattn_ws) return NLG_ERR;
     s->pcap = T;
   }
-  if (T >= NLG_BATCHED_MIN && stack_tile(s)) return NLG_ERR;
+  if ((T >= NLG_BATCHED_MIN || s->tiled) && stack_tile(s)) return NLG_ERR;
   hipLaunchKernelGGL(k_embed_prompt, dim3(nlg_blocks(d, 256), T), dim3(256), 0, st, s->emb, s->prompt,
                      c.max_seq, P, s->px, d);
   NLG_LAUNCHED("embed prompt");
+  const size_t rows_bytes = (size_t)T * d * 4;
+  if (trace) NLG_HIP(hipMemcpyAsync(trace, s->px, rows_bytes, hipMemcpyDeviceToDevice, st));
   float *pctx = (float *)s->pattn_ws;  // [T][nq] attention output
   for (uint32_t l = 0; l < c.layers; l++) {
     Layer &y = s->L[l];
@@ -569,20 +579,11 @@ extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t 
     q.ystride = s->nq; q.hd = c.head_dim; q.kvheads = c.kv_heads; q.max_seq = c.max_seq; q.co = s->co;
     q.si = s->si; q.pos = s->pos; q.kc = y.kc; q.vc = y.vc; q.qper = P;
     if (nlg_fused_launch(q, NLG_PRO_RMS, NLG_EPI_QKV, 0, st)) return NLG_ERR;
-    // a split prompt attention leaves the merged context quantised for the
-    // output projection (xq, gamma in the batched linears' scratch)
-    uint8_t *oq = T >= NLG_BATCHED_MIN && s->nq % 256 == 0
-                      ? (uint8_t *)nlg_scratch(nlg_batched_scratch_bytes(T, s->nq), st)
-                      : nullptr;
-    float *og = oq ? (float *)(oq + ((size_t)T * s->nq + 255) / 256 * 256) : nullptr;
-    bool quantized = false;
-    if (nlg_prefill_attn(s->pq, y.kc, y.vc, s->pos, T, P, c.heads, c.kv_heads, c.head_dim, c.max_seq, pctx,
-                         st, oq, og, &quantized))
-      return NLG_ERR;
-    FusedArgs o{};
-    o.x = pctx; o.w2 = y.wo; o.beta = y.bo; o.seq = T; o.out = d; o.cols = s->nq;
-    o.y = s->px; o.ystride = d; o.res = s->px; o.rstride = d;
-    if (quantized ? nlg_batched_gemm(o, oq, og, NLG_EPI_RESID, st) : nlg_fused_launch(o, NLG_PRO_NONE, NLG_EPI_RESID, 0, st))
+    // prompt attention and the output projection (a split attention
+    // leaves the merged context quantised for it); prompts start at
+    // position 0, so no row attends past P
+    if (nlg_prefill_attn_o_resid(s->pq, y.kc, y.vc, s->pos, T, P, c.heads, c.kv_heads, c.head_dim, c.max_seq, P,
+                                 pctx, y.wo, nullptr, y.bo, 0, s->px, s->px, d, st))
       return NLG_ERR;
     FusedArgs g{};
     g.x = s->px; g.gain = y.gffn; g.eps = c.rms_eps; g.w2 = y.wgu; g.beta = y.bgu; g.beta_per_row = 1;
@@ -592,6 +593,8 @@ extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t 
     w.x = s->ph; w.w2 = y.wd; w.beta = y.bd; w.seq = T; w.out = d; w.cols = f; w.y = s->px; w.ystride = d;
     w.res = s->px; w.rstride = d;
     if (nlg_fused_launch(w, NLG_PRO_NONE, NLG_EPI_RESID, 0, st)) return NLG_ERR;
+    if (trace)
+      NLG_HIP(hipMemcpyAsync((char *)trace + (size_t)(l + 1) * rows_bytes, s->px, rows_bytes, hipMemcpyDeviceToDevice, st));
   }
   hipLaunchKernelGGL(k_last_rows, dim3(nlg_blocks(d, 256), B), dim3(256), 0, st, s->px, P, s->x, d);
   NLG_LAUNCHED("last prompt rows");
@@ -604,8 +607,25 @@ extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t 
   return NLG_OK;
 }
 
+extern "C" int nlg_stack_prefill(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt) {
+  return stack_prefill(s, prompts, n_prompt, nullptr);
+}
+
+extern "C" int nlg_stack_prefill_trace(nlg_stack *s, const int32_t *prompts, uint32_t n_prompt, float *xs) {
+  if (!s || !prompts || !xs) return nlg_fail("stack prefill trace: null argument");
+  if (!n_prompt || n_prompt > s->c.max_seq) return nlg_fail("stack: prompt length must be 1..max_seq");
+  const size_t bytes = (size_t)(s->c.layers + 1) * s->c.batch * n_prompt * s->c.d_model * 4;
+  float *dev = (float *)nlg_malloc(bytes);
+  if (!dev) return NLG_ERR;
+  int rc = stack_prefill(s, prompts, n_prompt, dev);
+  if (!rc) rc = nlg_download(xs, dev, bytes);  // synchronous: ordered after the prefill
+  nlg_free(dev);
+  return rc;
+}
+
 extern "C" int nlg_stack_step(nlg_stack *s, uint32_t steps, int use_graph) {
   if (!s || !s->started) return nlg_fail("stack step: not started");
+  if (s->tiled && stack_tile(s)) return NLG_ERR;
   if ((uint64_t)s->host_pos + steps > s->c.max_seq)
     return nlg_fail("stack step: %u steps from position %u pass max_seq %u", steps, s->host_pos, s->c.max_seq);
   if (use_graph && !s->graph) {
@@ -632,6 +652,7 @@ extern "C" int nlg_stack_step_trace(nlg_stack *s, float *xs) {
   if (!xs) return nlg_fail("stack step trace: null argument");
   if ((uint64_t)s->host_pos + 1 > s->c.max_seq)
     return nlg_fail("stack step trace: position %u is at max_seq %u", s->host_pos, s->c.max_seq);
+  if (s->tiled && stack_tile(s)) return NLG_ERR;
   const size_t bytes = (size_t)(s->c.layers + 1) * s->c.batch * s->c.d_model * 4;
   float *dev = (float *)nlg_malloc(bytes);
   if (!dev) return NLG_ERR;
@@ -677,7 +698,12 @@ extern "C" int nlg_stack_tensor(nlg_stack *s, const char *name, int layer, void 
                      {"gattn", y.gattn, (size_t)d * 4},            {"gffn", y.gffn, (size_t)d * 4},
                      {"kc", y.kc, cache},                          {"vc", y.vc, cache}};
     for (const Ent &e : t)
-      if (!strcmp(e.n, name)) { *ptr = e.p; *bytes = e.b; return NLG_OK; }
+      if (!strcmp(e.n, name)) {
+        *ptr = e.p;
+        *bytes = e.b;
+        if (name[0] == 'w') s->retile = true;  // wqkv, wo, wgu, wd: may be written
+        return NLG_OK;
+      }
   } else {
     const size_t half = c.head_dim / 2;
     const Ent t[] = {{"wlm", s->wlm, (size_t)c.vocab * (d / 16) * 4}, {"blm", s->blm, 4},
@@ -685,7 +711,12 @@ extern "C" int nlg_stack_tensor(nlg_stack *s, const char *name, int layer, void 
                      {"rope_cos", s->co, c.max_seq * half * 4},      {"rope_sin", s->si, c.max_seq * half * 4},
                      {"x", s->x, (size_t)c.batch * d * 4}};
     for (const Ent &e : t)
-      if (!strcmp(e.n, name)) { *ptr = e.p; *bytes = e.b; return NLG_OK; }
+      if (!strcmp(e.n, name)) {
+        *ptr = e.p;
+        *bytes = e.b;
+        if (!strcmp(name, "wlm")) s->retile = true;
+        return NLG_OK;
+      }
   }
   return nlg_fail("stack tensor: no tensor '%s' (layer %d)", name, layer);
 }

@@ -107,6 +107,8 @@ def lib() -> C.CDLL:
         "nlg_attn_ternary_linear_residual": (i32, [vp, sz, u32, u32, u32, u32, u32, vp, vp, vp, i32, vp,
                                                    vp, u32, vp]),
         "nlg_prefill_attn_f16": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp, vp]),
+        "nlg_prefill_attn_ternary_linear_residual": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp, vp, vp,
+                                                           vp, i32, vp, vp, u32, vp]),
         "nlg_repack_i8_to_2bit": (i32, [vp, u32, u32, vp, vp, vp]),
         "nlg_decode_attn_paged_f16": (i32, [vp, vp, vp, vp, vp, u32, vp, u32, u32, u32, u32, u32, u32, vp, sz,
                                             vp]),
@@ -128,6 +130,7 @@ def lib() -> C.CDLL:
         "nlg_stack_destroy": (None, [vp]),
         "nlg_stack_start": (i32, [vp, vp, u32]),
         "nlg_stack_prefill": (i32, [vp, vp, u32]),
+        "nlg_stack_prefill_trace": (i32, [vp, vp, u32, vp]),
         "nlg_stack_step": (i32, [vp, u32, i32]),
         "nlg_stack_step_trace": (i32, [vp, vp]),
         "nlg_stack_position": (i32, [vp, C.POINTER(u32)]),
@@ -379,6 +382,15 @@ def prefill_attn_f16(q, kc, vc, pos, rows, qper, heads, kvheads, head_dim, max_s
                                       max_seq, ctx.ptr, stream), "prefill_attn_f16")
 
 
+def prefill_attn_ternary_linear_residual(q, kc, vc, pos, rows, qper, heads, kvheads, head_dim, max_seq, ctx_ws,
+                                         w2, bias, beta, res, y, out, beta_per_row=False, stream=None) -> None:
+    """That attention, then y = res + linear(ctx) (the stack's prefill form)."""
+    _check(lib().nlg_prefill_attn_ternary_linear_residual(
+        q.ptr, kc.ptr, vc.ptr, pos.ptr, rows, qper, heads, kvheads, head_dim, max_seq, ctx_ws.ptr, w2.ptr,
+        _ptr(bias), beta.ptr, int(beta_per_row), res.ptr, y.ptr, out, stream),
+        "prefill_attn_ternary_linear_residual")
+
+
 def decode_attn_paged_f16_workspace(batch, heads, kvheads, head_dim, bs, mbps) -> int:
     return int(lib().nlg_decode_attn_paged_f16_workspace(batch, heads, kvheads, head_dim, bs, mbps))
 
@@ -485,6 +497,18 @@ class Stack:
         p = np.ascontiguousarray(prompts, np.int32)
         assert p.ndim == 2 and p.shape[0] == self.cfg.batch
         _check(lib().nlg_stack_prefill(self.h, p.ctypes.data, p.shape[1]), "stack_prefill")
+
+    def prefill_trace(self, prompts: np.ndarray) -> np.ndarray:
+        """prefill(prompts), returning the prompt rows' residual stream
+        [layers + 1, batch * n_prompt, d_model]: the embedded rows, then the
+        rows after each layer."""
+        p = np.ascontiguousarray(prompts, np.int32)
+        assert p.ndim == 2 and p.shape[0] == self.cfg.batch
+        c = self.cfg
+        xs = np.empty((c.layers + 1) * p.size * c.d_model, np.float32)
+        _check(lib().nlg_stack_prefill_trace(self.h, p.ctypes.data, p.shape[1], xs.ctypes.data),
+               "stack_prefill_trace")
+        return xs.reshape(c.layers + 1, p.size, c.d_model)
 
     def step(self, steps: int = 1, graph: bool = True) -> None:
         _check(lib().nlg_stack_step(self.h, steps, int(graph)), "stack_step")

@@ -73,12 +73,12 @@ class RefStack:
         self.kc = [np.zeros(shape, np.float16) for _ in range(c.layers)]
         self.vc = [np.zeros(shape, np.float16) for _ in range(c.layers)]
 
-    def load_caches(self, stack, upto):
+    def load_caches(self, stack, upto, layers=None):
         """Take the device stack's fp16 K/V rows of positions < upto (e.g.
         after a prefill) as this composition's own, so the next step starts
-        from the same state."""
+        from the same state (every layer, or the given ones)."""
         c = self.c
-        for l in range(c.layers):
+        for l in (range(c.layers) if layers is None else layers):
             for name, dst in (("kc", self.kc[l]), ("vc", self.vc[l])):
                 dev = stack.tensor(name, l, np.float16).reshape(c.batch, c.kv_heads, c.max_seq, c.head_dim)
                 dst[:] = 0

@@ -218,42 +218,91 @@ def test_qkv_prompt_rejects_ragged_rows():
 
 
 def test_tiled_copy_registration():
-    """A tiled copy is taken at registration: changed weights need a new
-    registration (which refreshes the copy in place); after unregistering,
-    the row layout is read again.  Shapes the copy cannot serve are refused."""
-    seq, out, cols = 256, 512, 1024
-    x = nlgpu.normal(7, seq * cols)
+    """A registered tiled copy follows every write the library makes into its
+    weights (nlg_upload, nlg_copy_d2d, nlg_zero, a repack): calls at 1 token
+    (the GEMV, row layout), 8 tokens (the small-batch GEMM) and 512 tokens
+    (the 128 x 128 tiles) all give the oracle's bits for the new weights.
+    Registering again refreshes it too; after unregistering, the row layout
+    is read.  Shapes the copy cannot serve are refused or read the rows."""
+    out, cols = 512, 1024
+    seqs = (1, 8, 512)
+    xs = {n: nlgpu.normal(7 + n, n * cols) for n in seqs}
+    dxs = {n: nlgpu.to_device(xs[n]) for n in seqs}
     w_a, beta = weights(31, out, cols, per_row=False)
     w_b, _ = weights(32, out, cols, per_row=False)
-    dx, dw, db = nlgpu.to_device(x), nlgpu.to_device(w_a), nlgpu.to_device(beta)
-    dy = nlgpu.DeviceArray(seq * out * 4)
+    dw, db = nlgpu.to_device(w_a), nlgpu.to_device(beta)
+    dy = nlgpu.DeviceArray(max(seqs) * out * 4)
 
-    def run():
-        dy.zero()
-        nlgpu.ternary_linear(dx, dw, None, db, dy, seq, out, cols)
-        return dy.download(f32, seq * out)
+    def check(w, what):
+        for n in seqs:
+            dy.zero()
+            nlgpu.ternary_linear(dxs[n], dw, None, db, dy, n, out, cols)
+            same_bits(dy.download(f32, n * out), ref.linear(xs[n], w, beta, n, out, cols), f"{what}, {n} tokens")
 
-    want_a = ref.linear(x, w_a, beta, seq, out, cols)
-    want_b = ref.linear(x, w_b, beta, seq, out, cols)
     nlgpu.ternary_tiled_register(dw, out, cols)
     try:
-        same_bits(run(), want_a, "tiled copy of A")
+        check(w_a, "tiled copy of A")
         dw.upload(w_b)
-        same_bits(run(), want_a, "stale copy still A")  # the copy, not the rows, is read
-        nlgpu.ternary_tiled_register(dw, out, cols)
-        same_bits(run(), want_b, "refreshed copy of B")
+        check(w_b, "after nlg_upload of B")
+        da = nlgpu.to_device(w_a)
+        _check_rc(nlgpu.lib().nlg_copy_d2d(dw.ptr, da.ptr, w_a.nbytes, None))
+        check(w_a, "after nlg_copy_d2d of A")
+        dw.upload(w_b[:out // 2], offset=0)  # a partial write: the first half of the rows
+        w_mix = np.concatenate([w_b[:out // 2], w_a[out // 2:]])
+        check(w_mix, "after a partial upload")
+        dw.zero()
+        check(np.zeros_like(w_a), "after nlg_zero")
+        # a repack writing into the registered buffer (int8 lanes of B -> 2-bit)
+        lanes = nlgpu.unpack_ternary(w_b, cols).astype(np.int8).reshape(out, cols).view(np.uint32)
+        dl = nlgpu.to_device(np.ascontiguousarray(lanes))
+        nlgpu.repack_i8_to_2bit(dl, out, cols, dw)
+        check(w_b, "after a repack into it")
+        nlgpu.ternary_tiled_register(dw, out, cols)  # again: a refresh in place
+        check(w_b, "registered again")
         # another shape over the same pointer is not served by the copy
         dy.zero()
-        nlgpu.ternary_linear(dx, dw, None, db, dy, seq, out - 32, cols)
-        same_bits(dy.download(f32, seq * (out - 32)), ref.linear(x, w_b[:out - 32], beta, seq, out - 32, cols),
+        nlgpu.ternary_linear(dxs[512], dw, None, db, dy, 512, out - 32, cols)
+        same_bits(dy.download(f32, 512 * (out - 32)), ref.linear(xs[512], w_b[:out - 32], beta, 512, out - 32, cols),
                   "other rows: row layout")
     finally:
         nlgpu.ternary_tiled_unregister(dw)
     dw.upload(w_a)
-    same_bits(run(), want_a, "unregistered: row layout")
+    check(w_a, "unregistered: row layout")
     nlgpu.ternary_tiled_unregister(dw)  # no copy: a no-op
     with pytest.raises(nlgpu.NlgError, match="multiple of 256"):
         nlgpu.ternary_tiled_register(dw, out, 1000)
+
+
+def _check_rc(rc):
+    if rc:
+        raise nlgpu.NlgError(nlgpu.last_error())
+
+
+def test_tiled_copy_dropped_with_its_memory():
+    """nlg_free of registered weights drops the registration: new weights in
+    a buffer allocated afterwards -- at the same address, which the
+    allocator hands back for the same size -- are read as they are, not
+    through the freed buffer's copy."""
+    out, cols, n = 512, 1024, 512
+    x = nlgpu.normal(9, n * cols)
+    w_a, beta = weights(41, out, cols, per_row=False)
+    w_b, _ = weights(42, out, cols, per_row=False)
+    dx, db, dy = nlgpu.to_device(x), nlgpu.to_device(beta), nlgpu.DeviceArray(n * out * 4)
+    reused = 0
+    for attempt in range(4):
+        d1 = nlgpu.to_device(w_a)
+        nlgpu.ternary_tiled_register(d1, out, cols)
+        nlgpu.ternary_linear(dx, d1, None, db, dy, n, out, cols)
+        same_bits(dy.download(f32, n * out), ref.linear(x, w_a, beta, n, out, cols), "registered A")
+        addr = d1.ptr
+        d1.free()  # no unregister: nlg_free drops it
+        d2 = nlgpu.to_device(w_b)
+        reused += d2.ptr == addr
+        dy.zero()
+        nlgpu.ternary_linear(dx, d2, None, db, dy, n, out, cols)
+        same_bits(dy.download(f32, n * out), ref.linear(x, w_b, beta, n, out, cols), f"new buffer, attempt {attempt}")
+        d2.free()
+    print(f"  same address handed back in {reused} of 4 attempts", flush=True)
 
 
 # 4..127 tokens: the 16x16x64 GEMM with 64-row workgroups (many rows) or the

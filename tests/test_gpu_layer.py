@@ -278,6 +278,45 @@ def test_prefill_attention_fp16(B, heads, kvh, hd, max_seq, P, pos0):
     assert worst <= 1e-4
 
 
+@pytest.mark.parametrize("B,heads,kvh,hd,max_seq,P,pos0,out", [
+    (1, 20, 5, 128, 768, 512, 0, 2560),   # the stack's prompt: keys split, merged + quantised in one launch
+    (2, 8, 2, 64, 600, 200, 0, 512),      # two prompts: still split
+    (1, 16, 2, 128, 300, 100, 7, 1024),   # later start position
+    (8, 20, 5, 128, 768, 256, 0, 2560)])  # enough workgroups: unsplit, the context quantised by the GEMM
+def test_prefill_attention_projection_bits(B, heads, kvh, hd, max_seq, P, pos0, out):
+    """Prompt attention + output projection + residual in the stack's form
+    (a split attention's pieces merged and quantised in one launch, the GEMM
+    reading those int8 rows) give the bits of the attention's context
+    followed by the linear's own quantisation and GEMM."""
+    print(f"[gpu] prefill attention + projection B={B} heads={heads}/{kvh} hd={hd} P={P} pos0={pos0} out={out}",
+          flush=True)
+    nq, T = heads * hd, B * P
+    n = B * kvh * max_seq * hd
+    kc = nlgpu.normal(hd + 7 * B, n).astype(np.float16).view(np.uint16)
+    vc = nlgpu.normal(hd + 7 * B + 1, n).astype(np.float16).view(np.uint16)
+    q = (nlgpu.normal(P + pos0 + 1, T * nq) * f32(2.0)).astype(f32)
+    w2, beta = weights(out + nq, out, nq, per_row=True)
+    res = nlgpu.normal(out + 3, T * out)
+    dq, dkc, dvc = nlgpu.to_device(q), nlgpu.to_device(kc), nlgpu.to_device(vc)
+    dpos, dw, db = nlgpu.to_device(np.array([pos0], np.int32)), nlgpu.to_device(w2), nlgpu.to_device(beta)
+    ctx = nlgpu.DeviceArray(T * nq * 4)
+    nlgpu.prefill_attn_f16(dq, dkc, dvc, dpos, T, P, heads, kvh, hd, max_seq, ctx)
+    y_ref = nlgpu.to_device(res)
+    nlgpu.ternary_linear_residual(ctx, dw, None, db, y_ref, y_ref, T, out, nq, beta_per_row=True)
+    ws = nlgpu.DeviceArray(T * nq * 4)
+    y = nlgpu.to_device(res)
+    nlgpu.prefill_attn_ternary_linear_residual(dq, dkc, dvc, dpos, T, P, heads, kvh, hd, max_seq, ws, dw, None, db,
+                                               y, y, out, beta_per_row=True)
+    same_bits(y.download(f32, T * out), y_ref.download(f32, T * out))
+    # and the projection's input is the context the attention test pins
+    qr, got = q.reshape(B, P, nq), ctx.download(f32, T * nq).reshape(B, P, nq)
+    per = kvh * max_seq * hd
+    for b, i in ((0, 0), (B - 1, P - 1)):
+        want = orc.decode_attn_f16(qr[b, i], kc[b * per:(b + 1) * per], vc[b * per:(b + 1) * per], pos0 + i,
+                                   1, heads, kvh, hd, max_seq)
+        assert np.abs(got[b, i] - want).max() <= 1e-4 * np.abs(want).max()
+
+
 @pytest.mark.parametrize("B,heads,kvh,hd,bs,mbps,npool", [(3, 20, 5, 128, 16, 48, 160), (4, 8, 2, 64, 7, 10, 30),
                                                        (32, 20, 5, 128, 16, 48, 1600)])
 def test_paged_f16_attention(B, heads, kvh, hd, bs, mbps, npool):

@@ -185,6 +185,67 @@ def test_batched_decode_graph_eager_and_reference(B):
     b.close()
 
 
+def _write_weights(s, name, layer, words):
+    """Write 2-bit weight words into a stack tensor through the device
+    pointer nlg_stack_tensor hands out."""
+    import ctypes as C
+    p, n = C.c_void_p(), C.c_size_t(0)
+    L = nlgpu.lib()
+    assert L.nlg_stack_tensor(s.h, name.encode(), layer, C.byref(p), C.byref(n)) == 0
+    w = np.ascontiguousarray(words, np.uint32)
+    assert w.nbytes == n.value
+    assert L.nlg_upload(p.value, w.ctypes.data, w.nbytes) == 0
+
+
+def test_weights_written_through_tensor_pointers():
+    """Weights written through the pointers nlg_stack_tensor hands out reach
+    the matrix-core linears, which read tiled copies (batch 8: the decode
+    step's linears; prefill): the stack refreshes the copies before its next
+    prefill or step.  Checked against the CPU composition reading the new
+    weights (a stale copy would put the logits O(1) off), graph replay
+    against eager bits, and prefill against teacher-forced steps."""
+    print("[gpu] stack B=8: weights written through tensor pointers", flush=True)
+    B, n = MID["batch"], 3
+    c = MID
+    d, f, nq, nkv = c["d_model"], c["d_ff"], c["heads"] * c["head_dim"], c["kv_heads"] * c["head_dim"]
+    new = {("wqkv", 0): nlgpu.pack_ternary(nlgpu.trits(901, (nq + 2 * nkv, d))),
+           ("wd", 1): nlgpu.pack_ternary(nlgpu.trits(902, (d, f))),
+           ("wlm", -1): nlgpu.pack_ternary(nlgpu.trits(903, (c["vocab"], d)))}
+    P = prompts(B, n, c["vocab"], seed=35)
+    a, b, e = nlgpu.Stack(**MID), nlgpu.Stack(**MID), nlgpu.Stack(**MID)
+    for st in (a, b, e):
+        for (name, layer), w in new.items():
+            _write_weights(st, name, layer, w)
+    for (name, layer), w in new.items():
+        assert np.array_equal(a.tensor(name, layer, np.uint32), w.ravel())
+    r = ref.RefStack(a)
+    a.start(P)
+    b.start(P)
+    for pos in range(6):
+        toks, _ = a.tokens()
+        want = r.step(toks[:, pos], pos)
+        a.step(1, graph=False)
+        err = np.abs(a.logits() - want).max(axis=1) / np.abs(want).max(axis=1)
+        print(f"  pos={pos} max|dlogit|/max|logit| per sequence = {np.array2string(err, precision=1)}", flush=True)
+        assert np.all(err <= 5e-2)
+        if pos < 3:
+            assert np.sum(err <= 1e-5) >= B // 2, err
+    b.step(6, graph=True)
+    assert np.array_equal(a.logits().view(np.uint32), b.logits().view(np.uint32))
+    e.prefill(P)
+    t = nlgpu.Stack(**MID)
+    for (name, layer), w in new.items():
+        _write_weights(t, name, layer, w)
+    t.start(P)
+    t.step(n, graph=False)
+    lt, le = t.logits(), e.logits()
+    err = np.abs(lt - le).max() / np.abs(lt).max()
+    print(f"  prefill vs teacher-forced logits max|d|/max = {err:.2e}", flush=True)
+    assert err <= 5e-2
+    for st in (a, b, e, t):
+        st.close()
+
+
 def test_batched_decode_after_long_prefill():
     """A 600-token prompt (three chunks in use) prefilled at once against the
     same prompt teacher-forced, then decode steps: graph == eager bits,
@@ -295,3 +356,41 @@ def test_config5_full_size(B):
     assert np.all(ta[:, n + 5:] == -1)
     a.close()
     c.close()
+
+
+def test_config5_prefill_layers_against_reference():
+    """Config 5's prefill (B = 1, a 512-token prompt: batched int8 linears,
+    split prompt attention merged and quantised for the output projection)
+    checked a layer at a time against the reference kernels chained on the
+    CPU: for layers 0, 15 and 29 and prompt rows 0, 1, 255 and 511, the
+    reference's decode step at that row's position, fed the device's input
+    rows of that layer and the device's caches of the positions before the
+    row, against the device's output rows.  A lane flip moves one check by
+    ~1e-2; a systematic error would move them all (bar: median <= 1e-5,
+    max <= 5e-2, as for the decode step)."""
+    n, B = 512, 1
+    print(f"[gpu] config 5 full size B={B}: prefill {n} layer by layer vs reference", flush=True)
+    P = prompts(B, n, FULL["vocab"], seed=43)
+    a = nlgpu.Stack(**FULL, batch=B)
+    xs = a.prefill_trace(P)
+    cfg = a.cfg
+    assert xs.shape == (cfg.layers + 1, n, cfg.d_model)
+    r = ref.RefStack(a)
+    assert np.array_equal(xs[0].view(np.uint32), r.emb[P[0]].astype(np.float32).view(np.uint32))
+    errs = []
+    for l in (0, 15, cfg.layers - 1):
+        for row in (0, 1, 255, n - 1):
+            r.load_caches(a, row, layers=[l])
+            want = r.layer(l, xs[l][row:row + 1], row)
+            e = float(np.abs(xs[l + 1][row] - want[0]).max() / np.abs(want).max())
+            print(f"  layer {l:2d} row {row:3d}: max|d|/max = {e:.2e}", flush=True)
+            errs.append(e)
+    del r
+    errs = np.array(errs)
+    assert errs.max() <= 5e-2 and np.median(errs) <= 1e-5, errs
+    # the prefilled state decodes on
+    a.step(2)
+    t, g = a.tokens()
+    assert np.array_equal(t[:, :n], P) and np.array_equal(t[:, n + 1:n + 3], g[:, n:n + 2])
+    a.close()
+
