@@ -13,6 +13,13 @@ value    = algorithmic bytes of a step (4,227,076 B: packed W 4 MiB, f32 x,
            beta, f32 y) / measured step time, GB/s.
 roofline = the same kernel (the only one in the step): those bytes over its
            average launch duration from HIP events on the stream it runs on.
+roofline.traffic is the HBM bytes per launch of the PMC traffic summary in
+profiles/ (read, not measured here); roofline.ceiling_us is what one dependent
+launch can reach on this part: the measured empty-launch floor plus the
+bytes at the kernel's own streaming rate (the 128-matrix launch).
+device_timing: the same step with every wave's start and end read from the
+device's 100 MHz wall clock in a replayed graph (kernel duration and the idle
+gap to the next launch), no profiler attached.
 Extra fields: the GEMV alone on pre-quantised int8 x (4,214,792 B/launch),
 the same GEMV kernel over all 128 copies stacked into one [524288 x 4096]
 launch (launch cost amortised: the kernel's streaming rate), and the
@@ -32,6 +39,7 @@ import ctypes
 import ctypes as C
 import json
 import os
+import re
 import sys
 import time
 
@@ -45,8 +53,22 @@ OUT, COLS = 4096, 4096
 COPIES = 128
 STEP_BYTES = OUT * COLS // 4 + COLS * 4 + 4 + OUT * 4          # 4,227,076
 GEMV_BYTES = OUT * COLS // 4 + COLS + 4 + 4 + OUT * 4          # 4,214,792
-# HBM bytes per step measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-STEP_TRAFFIC = 4511247 + 16384
+# HBM bytes per step: the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary of
+# this kernel (read from the committed profile, not measured by this run)
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "ternary_gemv_4096_decode_pmc_traffic.md")
+WALL_CLOCK_MHZ = 100.0  # s_memrealtime's constant clock on this part
+
+
+def step_traffic():
+    """(bytes per step, FETCH_SIZE calibration factor) from the traffic
+    summary in profiles/, or (None, None) when it is not there."""
+    try:
+        txt = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None, None
+    m = re.search(r"\*\*traffic = ([\d,]+) B\*\*", txt)
+    f = re.search(r"factor \*\*([\d.]+)\*\*", txt)
+    return (int(m.group(1).replace(",", "")) if m else None), (f.group(1) if f else None)
 METRIC = "ternary GEMV GB/s (% HBM peak) at 4096²; decode tok/s, 2B ternary model, batch 1"
 
 
@@ -142,6 +164,29 @@ def gpu_bench(steps: int, warmup: int, sweep: bool):
     nlgpu.sync()
     res["step_stats"] = {}
     res["step_ms"] = timed(step, steps, stream, res["step_stats"])
+    nlgpu.sync()
+    # the same step with each wave's start and end on the device's wall
+    # clock (nlg_ternary_linear_timed): per launch of the last replay, the
+    # first wave's start to the last wave's end, and the idle gap to the
+    # next launch's first wave
+    nst = int(L.nlg_ternary_linear_timed_stamps(OUT))
+    dts = nlgpu.DeviceArray(nst * COPIES)
+
+    def tstep(i):
+        rc = L.nlg_ternary_linear_timed(dx.ptr, w_ptr(i), dbeta.ptr, dy.ptr, OUT, COLS,
+                                        dts.ptr + (i % COPIES) * nst, nst, stream)
+        if rc:
+            raise nlgpu.NlgError(nlgpu.last_error())
+
+    for i in range(warmup):
+        tstep(i)
+    res["timed_ms"] = timed(tstep, steps, stream)
+    st = dts.download(np.uint64, nst * COPIES // 8).reshape(COPIES, -1, 2).astype(np.int64)
+    t0, t1 = st[:, :, 0].min(axis=1), st[:, :, 1].max(axis=1)
+    res["device_us"] = (t1 - t0) / WALL_CLOCK_MHZ
+    res["gap_us"] = (t0[1:] - t1[:-1]) / WALL_CLOCK_MHZ
+    res["replay_span_us"] = (t1[-1] - t0[0]) / WALL_CLOCK_MHZ
+    dts.free()
     nlgpu.sync()
     for i in range(warmup):
         gemv(i)
@@ -857,6 +902,8 @@ def main():
     value = STEP_BYTES / (r["step_ms"] * 1e-3) / 1e9
     gemv_gbs = GEMV_BYTES / (r["gemv_ms"] * 1e-3) / 1e9
     stacked_gbs = GEMV_BYTES * COPIES / (r["stacked_ms"] * 1e-3) / 1e9
+    ceiling_us = r["floor_ms"] * 1e3 + STEP_BYTES / (stacked_gbs * 1e3)
+    traffic, tfac = step_traffic()
     cpu = cpu_baseline(r["x"], r["w_one"], args.cpu_seconds)
     out = {
         "metric": METRIC,
@@ -879,13 +926,28 @@ def main():
         "timing": dict(r["step_stats"], how="HIP events around each replay of a 128-launch graph on the "
                                              "kernel's stream; value uses the mean over every launch"),
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": STEP_TRAFFIC,
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "copy_peak_gbs": round(r["copy_gbs"], 1),
                      "frac_of_copy_peak": round(value / r["copy_gbs"], 4),
-                     "traffic_source": "profiles/ternary_gemv_4096_decode_pmc_traffic.md (FETCH_SIZE x 1.9993 "
-                                       "+ WRITE_SIZE, calibrated on a 64 MiB copy)",
+                     "traffic_source": ("profiles/ternary_gemv_4096_decode_pmc_traffic.md (FETCH_SIZE x "
+                                        f"{tfac} + WRITE_SIZE, calibrated on a 64 MiB copy)") if traffic else
+                                       "profile absent",
                      "kernel": "k_tern_fused", "bytes_per_launch": STEP_BYTES,
-                     "us_per_launch": round(r["step_ms"] * 1e3, 3)},
+                     "us_per_launch": round(r["step_ms"] * 1e3, 3),
+                     # what one dependent launch can reach on this part: the
+                     # empty-launch floor plus the bytes at the kernel's own
+                     # streaming rate (the 128-matrix launch)
+                     "ceiling_us": round(ceiling_us, 3),
+                     "frac_of_ceiling": round(ceiling_us / (r["step_ms"] * 1e3), 4)},
+        "device_timing": {"kernel_us": round(float(np.mean(r["device_us"])), 3),
+                          "kernel_us_p10_p90": [round(float(np.percentile(r["device_us"], q)), 3) for q in (10, 90)],
+                          "gap_to_next_us": round(float(np.mean(r["gap_us"])), 3),
+                          "kernel_plus_gap_us": round(float(np.mean(r["device_us"][:-1] + r["gap_us"])), 3),
+                          "event_us_per_launch": round(r["timed_ms"] * 1e3, 3),
+                          "how": "nlg_ternary_linear_timed: the same step with every wave's start and end read "
+                                 "from the 100 MHz wall clock (s_memrealtime) in a replayed 128-launch graph; "
+                                 "kernel = first wave's start to last wave's end of a launch, gap = idle time "
+                                 "to the next launch's first wave; no profiler attached"},
         "gemv_prequantised": {"gbs": round(gemv_gbs, 2), "us_per_launch": round(r["gemv_ms"] * 1e3, 3),
                               "bytes_per_launch": GEMV_BYTES, "kernel": "k_tern_i8_dec"},
         "gemv_stacked_one_launch": {"gbs": round(stacked_gbs, 2), "frac": round(stacked_gbs / HBM_PEAK_GBS, 4),

@@ -427,6 +427,17 @@ int nlg_repack_i8_to_2bit(const uint32_t *wp, uint32_t out, uint32_t cols, uint3
 int nlg_repack_packed_to_2bit(const float *wpk, uint32_t out, uint32_t cols, uint32_t pk, uint32_t fcount,
                               uint32_t *w2, uint32_t *nbad, void *stream);
 
+/* Measurement (no counterpart in the reference, which times a submitted
+ * command buffer from the host, vkmatmul.c:146-169): the bare one-token
+ * linear of nlg_ternary_linear (no bias, one beta, no gamma output) whose
+ * waves also write their start and end on the device's 100 MHz wall clock
+ * to stamps ([waves][2] u64; nlg_ternary_linear_timed_stamps(out) bytes):
+ * the kernel's device-side duration in a replayed graph, with no profiler
+ * attached.  Same outputs as nlg_ternary_linear. */
+int nlg_ternary_linear_timed(const float *x, const uint32_t *w2, const float *beta, float *y, uint32_t out,
+                             uint32_t cols, unsigned long long *stamps, size_t stamps_bytes, void *stream);
+size_t nlg_ternary_linear_timed_stamps(uint32_t out);
+
 /* Tiled weight copies.  No counterpart in the reference, which reads the
  * row layout of ternary-rows (kernels.el:700-746) at every batch size; for
  * callers that run the batched linears above (4 or more tokens).

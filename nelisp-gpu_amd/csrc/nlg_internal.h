@@ -252,6 +252,9 @@ enum {
   // kernel-internal: NLG_EPI_STORE with no bias, a per-tensor beta and no
   // gamma output (the bare linear: no per-row operand loads)
   NLG_EPI_STORE_PLAIN = 5,
+  // kernel-internal: NLG_EPI_STORE_PLAIN that also records each wave's
+  // start and end on the 100 MHz wall clock (FusedArgs::stamps)
+  NLG_EPI_STORE_TIMED = 6,
 };
 struct FusedArgs {
   const float *x;        // [seq x cols] f32 activation rows
@@ -287,6 +290,8 @@ struct FusedArgs {
   float *pval;
   int32_t *pidx;
   uint32_t nparts;
+  // EPI_STORE_TIMED: [gridDim.x * 4 waves][2] (start, end) wall-clock stamps
+  unsigned long long *stamps;
 };
 // Launch the fused kernel; rows_per_wave 0 picks a default.  Requires
 // cols % 64 == 0, cols <= 16384 and 16-byte aligned x and w2.  With
@@ -332,7 +337,7 @@ void nlg_tiled_drop_range(const void *base, size_t bytes);
 // Bytes the batched form needs for seq tokens of cols columns.
 size_t nlg_batched_scratch_bytes(uint32_t seq, uint32_t cols);
 // The rows-per-wave the launcher uses for `out` rows in mode `epi`.
-int nlg_fused_rows_per_wave(uint32_t out, int epi);
+int nlg_fused_rows_per_wave(uint32_t out, int epi, uint32_t cols = 0);
 
 // ---------------------------------------------------------------- launchers
 // One per kernel name (Appendix A of the survey, lisp/nelisp-gpu-kernels.el).

@@ -39,6 +39,10 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   __shared__ float red[4], red2[4];  // the two reductions' own scratch: no reuse barrier
   // Every argument the kernel uses is pinned into SGPRs here, so they all
   // arrive with the first kernarg fetch instead of in later round trips.
+  // TIMED: the wave's start on the constant 100 MHz wall clock (a scalar
+  // read of the clock, no memory access); its end is taken after its stores
+  constexpr bool TIMED = EPI == NLG_EPI_STORE_TIMED;
+  const unsigned long long t_start = TIMED ? __builtin_amdgcn_s_memrealtime() : 0ull;
   float *const y_out = a.y;
   float *const gamma_out = a.gamma_out;
   const uint32_t ystride = a.ystride;
@@ -130,7 +134,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   const uint32_t orow = orow_u < a.out ? orow_u : a.out - 1;  // every lane loads a valid row
   const bool olive = lane < R && orow_u < a.out;
   const float *bsrc = a.bias ? a.bias : a.beta;  // a real address either way
-  constexpr bool PLAIN = EPI == NLG_EPI_STORE_PLAIN;
+  constexpr bool PLAIN = EPI == NLG_EPI_STORE_PLAIN || EPI == NLG_EPI_STORE_TIMED;
   const float bo_raw = PLAIN ? 0.0f : bsrc[a.bias ? orow : 0];
   const float be = a.beta[PLAIN || !a.beta_per_row ? 0 : orow];
   const float bo = a.bias && !PLAIN ? bo_raw : 0.0f;
@@ -257,7 +261,7 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   amax = nlg_block_max_f32<4, true>(amax, red2);
   const float g = nlg_gamma_of(__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(amax))));
   const float ginv = 1.0f / g;
-  if (EPI != NLG_EPI_STORE_PLAIN && gamma_out && blockIdx.x == 0 && threadIdx.x == 0) gamma_out[tok] = g;
+  if (!PLAIN && gamma_out && blockIdx.x == 0 && threadIdx.x == 0) gamma_out[tok] = g;
   // 4. quantise into LDS, one packed word per float4 (exact; see lane_est),
   //    stored already in the dots' operand order: a 16-column group's four
   //    words sit in the four lanes of a quad, and lane i keeps byte i of
@@ -338,8 +342,14 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
   }
   // Y = BIAS[o] + (BETA * GAMMA[s]) * float(acc)   (kernels.el:633)
   const float val = __fadd_rn(bo, __fmul_rn(__fmul_rn(be, g), (float)(tl >> 6)));
-  if (EPI == NLG_EPI_STORE || EPI == NLG_EPI_STORE_PLAIN || EPI == NLG_EPI_ARGMAX) {
+  if (EPI == NLG_EPI_STORE || PLAIN || EPI == NLG_EPI_ARGMAX) {
     if (olive) y_out[(size_t)tok * ystride + orow] = val;
+  }
+  if (TIMED && lane == 0) {
+    const unsigned long long t_end = __builtin_amdgcn_s_memrealtime();
+    unsigned long long *ts = a.stamps + 2 * ((size_t)blockIdx.x * 4 + wvi);
+    ts[0] = t_start;
+    ts[1] = t_end;
   }
   if (EPI == NLG_EPI_RESID) {
     if (olive) y_out[(size_t)tok * ystride + orow] = __fadd_rn(rv, val);
@@ -394,11 +404,14 @@ __global__ __launch_bounds__(256) void k_tern_fused(FusedArgs a) {
 // workgroups waste less -- down to about one workgroup per CU.  Measured
 // at the decode shapes (graph-timed, weights streamed from HBM): 4 rows per
 // wave for 2560..4096 outputs, 8 for the 13824-row gate|up and the LM head.
-int nlg_fused_rows_per_wave(uint32_t out, int epi) {
-  // the LM head: 16 rows per wave (128,256 x 2,560, one row, graph-timed with
-  // the argmax: 8 rows 34.9 us, 16 30.6, 32 34.0; the quantisation as its
-  // own launch in front of a prologue-free GEMV measured 32.0)
-  if (epi == NLG_EPI_ARGMAX) return out >= 32768 ? 16 : 4;
+int nlg_fused_rows_per_wave(uint32_t out, int epi, uint32_t cols) {
+  // the LM head: 16 rows per wave on rows of up to 3072 columns, the packed
+  // form (128,256 x 2,560, one row, graph-timed with the argmax: 8 rows
+  // 34.9 us, 16 30.6, 32 34.0; the quantisation as its own launch in front
+  // of a prologue-free GEMV measured 32.0); wider rows keep 8, since 16 rows
+  // of unpacked chunks there need 238+ VGPRs (two waves per SIMD or one).
+  // cols 0 (unknown) answers 8: the most partials any call can leave.
+  if (epi == NLG_EPI_ARGMAX) return out >= 32768 ? (cols && cols <= 3072 ? 16 : 8) : 4;
   if (epi == NLG_EPI_SWIGLU || epi == NLG_EPI_QKV) return out >= 8192 ? 8 : (out >= 2048 ? 4 : 2);
   return out >= 8192 ? 8 : (out >= 2048 ? 4 : (out >= 1024 ? 2 : 1));
 }
@@ -421,7 +434,7 @@ static void fused_go(const FusedArgs &a, dim3 grid, hipStream_t st) {
 
 uint32_t nlg_argmax_parts(uint32_t seq, uint32_t cols, uint32_t out) {
   if (nlg_batched(seq, cols)) return (out + 63) / 64;  // one per GEMM workgroup
-  const uint32_t rpw = (uint32_t)nlg_fused_rows_per_wave(out, NLG_EPI_ARGMAX);
+  const uint32_t rpw = (uint32_t)nlg_fused_rows_per_wave(out, NLG_EPI_ARGMAX, cols);
   return (out + rpw - 1) / rpw;
 }
 
@@ -435,7 +448,7 @@ int nlg_fused_launch(const FusedArgs &a0, int pro, int epi, int rpw, hipStream_t
     return nlg_fail("fused ternary linear: x, w2 and gain must be 16-byte aligned");
   if (a.seq > 65535) return nlg_fail("fused ternary linear: seq %u > 65535", a.seq);
   a.wng = a.cols / 16;
-  if (rpw <= 0) rpw = nlg_fused_rows_per_wave(a.out, epi);
+  if (rpw <= 0) rpw = nlg_fused_rows_per_wave(a.out, epi, a.cols);
   if ((epi == NLG_EPI_SWIGLU || epi == NLG_EPI_QKV) && (rpw < 2 || a.out % 2))
     return nlg_fail("fused ternary linear: paired epilogues need an even row count");
   const dim3 grid(nlg_blocks(a.out, 4u * rpw), a.seq);
@@ -452,7 +465,10 @@ int nlg_fused_launch(const FusedArgs &a0, int pro, int epi, int rpw, hipStream_t
   } while (0)
   if (rpw != 1 && rpw != 2 && rpw != 4 && rpw != 8 && !(rpw == 16 && epi == NLG_EPI_ARGMAX))
     return nlg_fail("rows_per_wave must be 1, 2, 4 or 8 (or 16 for an argmax)");
-  if (pro == NLG_PRO_NONE && epi == NLG_EPI_STORE && !a.bias && !a.beta_per_row && !a.gamma_out)
+  if (pro == NLG_PRO_NONE && epi == NLG_EPI_STORE && a.stamps && !a.bias && !a.beta_per_row && !a.gamma_out &&
+      a.seq == 1)
+    PE(NLG_PRO_NONE, NLG_EPI_STORE_TIMED);
+  else if (pro == NLG_PRO_NONE && epi == NLG_EPI_STORE && !a.bias && !a.beta_per_row && !a.gamma_out)
     PE(NLG_PRO_NONE, NLG_EPI_STORE_PLAIN);
   else if (pro == NLG_PRO_NONE && epi == NLG_EPI_STORE) PE(NLG_PRO_NONE, NLG_EPI_STORE);
   else if (pro == NLG_PRO_RMS && epi == NLG_EPI_STORE) PE(NLG_PRO_RMS, NLG_EPI_STORE);
@@ -592,7 +608,7 @@ __global__ __launch_bounds__(1024) void k_argmax_parts(const float *pval, const 
 
 extern "C" size_t nlg_rms_ternary_argmax_workspace(uint32_t seq, uint32_t vocab) {
   // the larger of the two forms' partial counts, whatever cols the call uses
-  const int rpw = nlg_fused_rows_per_wave(vocab, NLG_EPI_ARGMAX);
+  const int rpw = nlg_fused_rows_per_wave(vocab, NLG_EPI_ARGMAX, 0);
   size_t nparts = (vocab + rpw - 1) / rpw;
   if ((size_t)(vocab + 63) / 64 > nparts) nparts = (vocab + 63) / 64;
   return (size_t)seq * nparts * 8;
@@ -608,7 +624,7 @@ extern "C" int nlg_rms_ternary_argmax(const float *x, const float *gain, float e
   if (!workspace || workspace_bytes < need)
     return nlg_fail("rms ternary argmax: needs a %zu-byte workspace", need);
   hipStream_t st = nlg_stream(stream);
-  const int rpw = nlg_fused_rows_per_wave(vocab, NLG_EPI_ARGMAX);
+  const int rpw = nlg_fused_rows_per_wave(vocab, NLG_EPI_ARGMAX, cols);
   const uint32_t nparts = nlg_argmax_parts(seq, cols, vocab);
   FusedArgs a{};
   a.x = x; a.gain = gain; a.eps = eps; a.w2 = w2; a.beta = beta; a.beta_per_row = beta_per_row;

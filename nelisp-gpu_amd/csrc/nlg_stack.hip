@@ -479,7 +479,7 @@ static int stack_head(nlg_stack *s) {
   a.x = s->x; a.gain = s->gfinal; a.eps = c.rms_eps; a.w2 = s->wlm; a.beta = s->blm;
   a.seq = B; a.out = c.vocab; a.cols = d; a.y = s->logits; a.ystride = c.vocab;
   a.pval = s->pval; a.pidx = s->pidx;
-  const int rpw = nlg_fused_rows_per_wave(c.vocab, NLG_EPI_ARGMAX);
+  const int rpw = nlg_fused_rows_per_wave(c.vocab, NLG_EPI_ARGMAX, d);
   if (nlg_fused_launch(a, NLG_PRO_RMS, NLG_EPI_ARGMAX, rpw, nlg_stream(nullptr))) return NLG_ERR;
   SampleArgs sa;
   sa.pval = s->pval; sa.pidx = s->pidx; sa.nparts = s->nparts; sa.prompt = s->prompt;

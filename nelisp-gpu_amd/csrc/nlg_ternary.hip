@@ -478,6 +478,29 @@ static int linear_go(const float *x, const uint32_t *w2, const float *bias, cons
   return tern_launch(ta, rpw, wpb, st);
 }
 
+// The bare one-token linear (no bias, one beta, no gamma output) with each
+// wave's start and end stamped on the device's 100 MHz wall clock: a
+// device-side duration of graph-replayed launches, no profiler attached.
+extern "C" int nlg_ternary_linear_timed(const float *x, const uint32_t *w2, const float *beta, float *y,
+                                        uint32_t out, uint32_t cols, unsigned long long *stamps,
+                                        size_t stamps_bytes, void *stream) {
+  if (nlg_ensure_init()) return NLG_ERR;
+  if (!out) return NLG_OK;
+  if (!x || !w2 || !beta || !y || !stamps) return nlg_fail("timed linear: null pointer");
+  if (!linear_fusable(x, w2, 1, cols)) return nlg_fail("timed linear: cols must be a multiple of 64 in [64, 16384]");
+  if (stamps_bytes < nlg_ternary_linear_timed_stamps(out)) return nlg_fail("timed linear: stamps buffer is short");
+  FusedArgs a{};
+  a.x = x; a.w2 = w2; a.beta = beta; a.y = y; a.ystride = out; a.seq = 1; a.out = out; a.cols = cols;
+  a.stamps = stamps;
+  return nlg_fused_launch(a, NLG_PRO_NONE, NLG_EPI_STORE, 0, nlg_stream(stream));
+}
+
+// 16 bytes per wave of the default geometry (4 waves per workgroup)
+extern "C" size_t nlg_ternary_linear_timed_stamps(uint32_t out) {
+  const uint32_t rpw = (uint32_t)nlg_fused_rows_per_wave(out, NLG_EPI_STORE);
+  return (size_t)((out + 4 * rpw - 1) / (4 * rpw)) * 4 * 16;
+}
+
 extern "C" int nlg_ternary_linear_cfg(const float *x, const uint32_t *w2, const float *bias,
                                       const float *beta, int beta_per_row, float *y, float *gamma_out,
                                       uint32_t seq, uint32_t out, uint32_t cols, int rows_per_wave,

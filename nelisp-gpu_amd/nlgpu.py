@@ -107,6 +107,8 @@ def lib() -> C.CDLL:
         "nlg_attn_ternary_linear_residual": (i32, [vp, sz, u32, u32, u32, u32, u32, vp, vp, vp, i32, vp,
                                                    vp, u32, vp]),
         "nlg_prefill_attn_f16": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp, vp]),
+        "nlg_ternary_linear_timed": (i32, [vp, vp, vp, vp, u32, u32, vp, sz, vp]),
+        "nlg_ternary_linear_timed_stamps": (sz, [u32]),
         "nlg_prefill_attn_ternary_linear_residual": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp, vp, vp,
                                                            vp, i32, vp, vp, u32, vp]),
         "nlg_repack_i8_to_2bit": (i32, [vp, u32, u32, vp, vp, vp]),

@@ -216,3 +216,31 @@ def test_batched_linears_on_two_streams_do_not_share_scratch():
         assert np.array_equal(cases[i][4].download(np.uint32, seq * out), want[i].view(np.uint32)), i
     for st in streams:
         nlgpu.lib().nlg_stream_destroy(st)
+
+
+def test_timed_linear_matches_and_stamps():
+    """The measurement variant (nlg_ternary_linear_timed) computes the same
+    bits as the plain linear and leaves one (start, end) wall-clock pair per
+    wave, end after start, all within one launch's span."""
+    out, cols = 4096, 4096
+    w2 = nlgpu.pack_ternary(nlgpu.trits(77, (out, cols)))
+    x = nlgpu.normal(78, cols)
+    beta = np.array([0.03], np.float32)
+    dx, dw, db = nlgpu.to_device(x), nlgpu.to_device(w2), nlgpu.to_device(beta)
+    y0, y1 = nlgpu.DeviceArray(out * 4), nlgpu.DeviceArray(out * 4)
+    nlgpu.ternary_linear(dx, dw, None, db, y0, 1, out, cols)
+    L = nlgpu.lib()
+    nst = int(L.nlg_ternary_linear_timed_stamps(out))
+    assert nst == 256 * 4 * 16
+    ds = nlgpu.DeviceArray(nst)
+    assert L.nlg_ternary_linear_timed(dx.ptr, dw.ptr, db.ptr, y1.ptr, out, cols, ds.ptr, nst, None) == 0
+    nlgpu.sync()
+    a, b = y0.download(np.float32, out), y1.download(np.float32, out)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    st = ds.download(np.uint64, nst // 8).reshape(-1, 2).astype(np.int64)
+    assert np.all(st[:, 0] > 0) and np.all(st[:, 1] >= st[:, 0])
+    span = (st[:, 1].max() - st[:, 0].min()) / 100.0  # us at 100 MHz
+    assert 0.0 < span < 1000.0, span
+    with pytest.raises(nlgpu.NlgError, match="short"):
+        nlgpu._check(L.nlg_ternary_linear_timed(dx.ptr, dw.ptr, db.ptr, y1.ptr, out, cols, ds.ptr, nst - 16, None),
+                     "timed")
