@@ -24,6 +24,12 @@
 // A[lane 16g + i][b] * B[lane 16g + j][b], and lane l's result r is
 // C[4(l/16) + r][l % 16].  Here i = token, j = output row, and lane group g
 // at step t of a chunk covers 2-bit word 4g + t of the chunk.
+//
+// 128 tokens and more: k_tgemm_l (32 x 32 x 32 MFMAs, 64 / 128 / 256-row
+// workgroups of token-half waves, split over the columns when there are few
+// tiles) and, once there are as many 256-row x 128-token tiles as CUs,
+// k_tgemm_w (waves of 64 rows x 128 tokens fed by direct global-to-LDS
+// activation loads).
 #include <math.h>
 
 #include "nlg_quant.h"
@@ -794,16 +800,16 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 // -- integer sums, the same in any order -- and returns true to run the
 // epilogue.  It also re-zeros the tile's counter for the next launch,
 // which the stream orders after this one.  s_last: one LDS word.
-template <int NB>
-__device__ __forceinline__ bool tl_split_meet(const GemmArgs &a, v16i (&acc)[2][NB], uint32_t *s_last) {
-  constexpr int NR = 2 * NB * 16;  // accumulators per thread
+template <int MB, int NB>
+__device__ __forceinline__ bool tl_split_meet(const GemmArgs &a, v16i (&acc)[MB][NB], uint32_t *s_last) {
+  constexpr int NR = MB * NB * 16;  // accumulators per thread
   const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x, ntile = gridDim.x * gridDim.y, ks = gridDim.z;
   const size_t nthr = blockDim.x;
   // register j of every thread side by side: each store and load of a
   // wave covers 256 contiguous bytes
   int32_t *mine = a.ksum + ((size_t)blockIdx.z * ntile + tile) * NR * nthr + threadIdx.x;
 #pragma unroll
-  for (int mt = 0; mt < 2; mt++)
+  for (int mt = 0; mt < MB; mt++)
 #pragma unroll
     for (int nt = 0; nt < NB; nt++)
 #pragma unroll
@@ -823,7 +829,7 @@ __device__ __forceinline__ bool tl_split_meet(const GemmArgs &a, v16i (&acc)[2][
     if (z == blockIdx.z) continue;
     const int32_t *other = a.ksum + ((size_t)z * ntile + tile) * NR * nthr + threadIdx.x;
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int mt = 0; mt < MB; mt++)
 #pragma unroll
       for (int nt = 0; nt < NB; nt++)
 #pragma unroll
@@ -834,16 +840,17 @@ __device__ __forceinline__ bool tl_split_meet(const GemmArgs &a, v16i (&acc)[2][
   return true;
 }
 
-// The epilogue of k_tgemm_l: acc[mt][nt] of lane (li, lg) of the
-// wave at token half wm, rows rw[nt] (clamped rc[nt]), with bias bo and
-// beta be per row block and the workgroup's 128 gammas in s_gm.
+// The epilogue of k_tgemm_l and k_tgemm_w: acc[mt][nt] of lane (li, lg) of
+// the wave at token half wm (k_tgemm_w: MB = 4 token blocks, wm = 0), rows
+// rw[nt] (clamped rc[nt]), with bias bo and beta be per row block and the
+// workgroup's 128 gammas in s_gm.
 //
 // QKV: s_tp holds each of the workgroup's 128 tokens' cache position (-1
 // where it is past max_seq) and s_tb its cache row's element offset
 // ((sequence x kvheads x max_seq + position) x head_dim), computed once per
 // workgroup; a row block's section, head and dimension once per block.
-template <int NB, int EPI>
-__device__ __forceinline__ void tl_epilogue(const GemmArgs &a, const v16i (&acc)[2][NB], const uint32_t (&rw)[NB],
+template <int MB, int NB, int EPI>
+__device__ __forceinline__ void tl_epilogue(const GemmArgs &a, const v16i (&acc)[MB][NB], const uint32_t (&rw)[NB],
                                             const uint32_t (&rc)[NB], const float (&bo)[NB], const float (&be)[NB],
                                             const float *s_gm, int lane, int wm, int lg, uint32_t tok0,
                                             const int32_t *s_tp, const uint64_t *s_tb) {
@@ -860,7 +867,7 @@ __device__ __forceinline__ void tl_epilogue(const GemmArgs &a, const v16i (&acc)
     // odd lane 8..15, after swapping the other half's value with its partner.
     const bool odd = lane & 1;
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
+    for (int mt = 0; mt < MB; mt++) {
 #pragma unroll
       for (int nt = 0; nt < NB; nt++) {
         const v16i q = acc[mt][nt];
@@ -897,7 +904,7 @@ __device__ __forceinline__ void tl_epilogue(const GemmArgs &a, const v16i (&acc)
       const bool isq = row < a.nq, isk = row < a.nq + a.nkv;
       uint16_t *const cache = (isk ? a.kc : a.vc) + ((size_t)kh * a.max_seq * a.hd + dd);
 #pragma unroll
-      for (int mt = 0; mt < 2; mt++) {
+      for (int mt = 0; mt < MB; mt++) {
         float cs[16], sn[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
@@ -931,7 +938,7 @@ __device__ __forceinline__ void tl_epilogue(const GemmArgs &a, const v16i (&acc)
     return;
   }
 #pragma unroll
-  for (int mt = 0; mt < 2; mt++) {
+  for (int mt = 0; mt < MB; mt++) {
 #pragma unroll
     for (int nt = 0; nt < NB; nt++) {
       TgPre pre[16];
@@ -1116,10 +1123,232 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
 #undef TL_STOREA
   if (SPLIT) {
     __shared__ uint32_t s_last;
-    if (!tl_split_meet<NB>(a, acc, &s_last)) return;
+    if (!tl_split_meet<2, NB>(a, acc, &s_last)) return;
   }
-  tl_epilogue<NB, EPI>(a, acc, rw, rc, bo, be, s_gm, lane, wm, lg, tok0, s_tp, s_tb);
+  tl_epilogue<2, NB, EPI>(a, acc, rw, rc, bo, be, s_gm, lane, wm, lg, tok0, s_tp, s_tb);
 }
+
+// Many tokens, wide waves: a workgroup owns 256 output rows x 128 tokens,
+// each of its 4 waves 64 rows (two 32-row blocks) x all 128 tokens (four
+// 32-token blocks).  Every weight chunk is fetched once per workgroup and
+// every decoded B operand feeds four MFMAs (k_tgemm_l's token-half waves
+// fetch each chunk twice and feed two).  Activations go from global memory
+// straight to LDS (global_load_lds_dwordx4: no staging registers, no LDS
+// stores) into two [128 tokens][256 B] stages, one chunk ahead; their
+// 16-byte units are XOR-swizzled by token (unit u of token k at slot
+// u ^ (k % 16)), so an operand read (16 consecutive tokens of one unit) hits
+// 16 distinct 16-byte bank groups, and one load instruction of a wave fills
+// 1 KiB of the stage (4 tokens).  Weights run two chunks ahead in three
+// register sets; the operand reads of step t + 1 are issued before the MFMAs
+// of step t.  The stages are separate LDS arrays indexed statically (the
+// chunk loop unrolls by six), so the compiler can tell that a load into one
+// stage does not touch the other and does not wait for it before reading
+// the other.  Two 4-wave workgroups share a CU (66 KB of LDS and at most 256
+// VGPRs each), so each SIMD runs two waves whose barriers are independent.
+// (Measured at 16,384 tokens, config-4 FFN, median of 20 interleaved
+// launches: gate|up 466.7 us, down 225.6 us, against k_tgemm_l's 556.4 and
+// 244.8.  Rejected variants: one 8-wave workgroup of 512 rows per CU, 524.1
+// and 252.3; three stages, activations two chunks ahead, 656.5 / 280.5 with
+// 4 waves (one workgroup per CU) and 534.8 / 254.7 with 8; persistent
+// workgroups that issue the next tile's first loads before the epilogue,
+// 699 with 4 waves (the tile loop spills).)
+#define TW_STAGE (128 * TG_KC)
+// s_waitcnt vmcnt(n) lgkmcnt(0) (expcnt at its maximum: no wait)
+#define TW_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (0x7 << 4) | (((n) >> 4) << 14))
+// a compiler-level fence: no memory operation moves across it
+#define TW_ORDER() asm volatile("" ::: "memory")
+
+template <int EPI, bool TILED = false>
+__global__ __launch_bounds__(256, 2) void k_tgemm_w(GemmArgs a) {
+  constexpr int WR = 4, NB = 2, MB = 4;
+  constexpr int PI = TW_STAGE / 1024 / WR;  // 1 KiB stage loads per wave and chunk
+  constexpr int NWL = 2 * NB;               // weight load instructions per wave and chunk
+  typedef uint32_t wvec __attribute__((ext_vector_type(8 * NB)));
+  __shared__ __align__(1024) uint8_t s_a0[TW_STAGE];
+  __shared__ __align__(1024) uint8_t s_a1[TW_STAGE];
+  __shared__ float s_gm[128];
+  __shared__ int32_t s_tp[EPI == NLG_EPI_QKV ? 128 : 1];
+  __shared__ uint64_t s_tb[EPI == NLG_EPI_QKV ? 128 : 1];
+  asm volatile("" ::"s"(a.xq), "s"(a.gamma), "s"(a.w2), "s"(a.bias), "s"(a.beta), "s"(a.y), "s"(a.seq),
+               "s"(a.out), "s"(a.cols), "s"(a.wng), "s"(a.ystride), "s"(a.beta_per_row));
+  const int lane = threadIdx.x & 63;
+  const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 31, lg = lane >> 5;
+  const uint32_t rbase = blockIdx.x * (64 * WR) + wn * 64;
+  const uint32_t tok0 = blockIdx.y * 128;
+  const uint32_t nchunks = a.cols / TG_KC;
+  // weight rows of this lane, as in k_tgemm_l
+  uint32_t rw[NB], rc[NB];
+  const uint4 *wp[NB];
+#pragma unroll
+  for (int nt = 0; nt < NB; nt++) {
+    rw[nt] = rbase + 32 * nt + li;
+    rc[nt] = rw[nt] < a.out ? rw[nt] : a.out - 1;
+    if (TILED) {
+      const uint32_t nrb = (a.out + 31) / 32, rb = rbase / 32 + nt < nrb ? rbase / 32 + nt : nrb - 1;
+      wp[nt] = (const uint4 *)a.w2 + (size_t)rb * nchunks * 128 + lane;
+    } else {
+      wp[nt] = (const uint4 *)(a.w2 + (size_t)rc[nt] * a.wng) + 2 * lg;
+    }
+  }
+  // Stage loads: wave wn's load i fills stage bytes [1024 b, 1024 b + 1024),
+  // b = wn PI + i: lane j writes token k = 4 b + j / 16 (clamped to the last
+  // real token), slot j % 16, i.e. unit (j % 16) ^ (k % 16) of its chunk row,
+  // at byte offset xo[i] from the chunk's column 0 (the launcher checks that
+  // seq x cols fits 32 bits, so the loads take a scalar base + 32-bit offset)
+  uint32_t xo[PI];
+#pragma unroll
+  for (int i = 0; i < PI; i++) {
+    const uint32_t k = 4 * (wn * PI + i) + lane / 16, tk = tok0 + k < a.seq ? tok0 + k : a.seq - 1;
+    xo[i] = tk * a.cols + 16 * ((lane % 16) ^ (k % 16));
+  }
+#define TW_LOADW(c, dst)                                                                   \
+  do {                                                                                     \
+    _Pragma("unroll") for (int nt = 0; nt < NB; nt++) {                                    \
+      const uint4 u0 = TILED ? wp[nt][128 * (c)] : wp[nt][4 * (c)];                         \
+      const uint4 u1 = TILED ? wp[nt][128 * (c) + 64] : wp[nt][4 * (c) + 1];                \
+      dst[8 * nt + 0] = u0.x; dst[8 * nt + 1] = u0.y; dst[8 * nt + 2] = u0.z;               \
+      dst[8 * nt + 3] = u0.w; dst[8 * nt + 4] = u1.x; dst[8 * nt + 5] = u1.y;               \
+      dst[8 * nt + 6] = u1.z; dst[8 * nt + 7] = u1.w;                                       \
+    }                                                                                      \
+  } while (0)
+#define TW_LOADA(c, stage)                                                                 \
+  do {                                                                                     \
+    const uint8_t *xc = a.xq + (size_t)(c) * TG_KC;                                        \
+    _Pragma("unroll") for (int i = 0; i < PI; i++)                                         \
+      __builtin_amdgcn_global_load_lds(                                                    \
+          (const void *)(xc + xo[i]),                                                      \
+          (__attribute__((address_space(3))) void *)((stage) + 1024 * (wn * PI + i)), 16, 0, 0); \
+  } while (0)
+  // the epilogue operands first (their loads precede every stage load, so
+  // they do not enter the waits' counts), then the first chunks in the order
+  // the steps issue theirs: stage loads, then weight loads
+  float bo[NB], be[NB];
+#pragma unroll
+  for (int nt = 0; nt < NB; nt++) {
+    bo[nt] = a.bias ? a.bias[rc[nt]] : 0.0f;
+    be[nt] = a.beta[a.beta_per_row ? rc[nt] : 0];
+  }
+  const uint32_t tkc = tok0 + (threadIdx.x & 127u) < a.seq ? tok0 + (threadIdx.x & 127u) : a.seq - 1;
+  const float gm_r = a.gamma[tkc];
+  int32_t tp_r = 0;
+  uint64_t tb_r = 0;
+  if (EPI == NLG_EPI_QKV) {
+    // token t's cache position (decode rows: pos[0]; prompt rows: pos[0] +
+    // t % qper) and its cache row's element offset
+    const int32_t pr = nlg_ld_uniform_i32(a.pos) + (a.qper ? (int32_t)(tkc % a.qper) : 0);
+    const bool ok = pr >= 0 && (uint32_t)pr < a.max_seq;
+    const uint32_t sq = a.qper ? tkc / a.qper : tkc;
+    tp_r = ok ? pr : -1;
+    tb_r = ((uint64_t)sq * a.kvheads * a.max_seq + (ok ? (uint32_t)pr : 0u)) * a.hd;
+  }
+  wvec wA, wB, wC;
+  const uint32_t c1 = nchunks > 1 ? 1 : 0;
+  TW_ORDER();
+  TW_LOADW(0, wA);
+  TW_ORDER();
+  TW_LOADA(0, s_a0);
+  TW_ORDER();
+  TW_LOADW(c1, wB);
+  // (stored before the first step, whose wait includes lgkmcnt(0))
+  if (threadIdx.x < 128) {
+    s_gm[threadIdx.x] = gm_r;
+    if (EPI == NLG_EPI_QKV) {
+      s_tp[threadIdx.x] = tp_r;
+      s_tb[threadIdx.x] = tb_r;
+    }
+  }
+  v16i acc[MB][NB];  // [token block][row block]
+#pragma unroll
+  for (int mt = 0; mt < MB; mt++)
+#pragma unroll
+    for (int nt = 0; nt < NB; nt++) acc[mt][nt] = (v16i){};
+  // the operand read of lane (li, lg), token block mt, step t: token
+  // k = 32 mt + li, unit 8 lg + t, at k * 256 + 16 ((8 lg + t) ^ (li % 16))
+  const uint32_t ra = li * TG_KC + 16 * ((8 * lg) ^ (li % 16));
+#define TW_RDA(stage, t, dst)                                                                 \
+  do {                                                                                        \
+    const uint8_t *sp = (stage) + (ra ^ (16 * (t)));                                          \
+    _Pragma("unroll") for (int mt = 0; mt < MB; mt++) {                                       \
+      const uint4 u = *(const uint4 *)(sp + 32 * TG_KC * mt);                                  \
+      dst[mt] = (v4i){(int)u.x, (int)u.y, (int)u.z, (int)u.w};                                 \
+    }                                                                                         \
+  } while (0)
+  // each A fragment feeds NB MFMAs, each decoded B operand MB
+#define TW_MMA(stage, WCUR)                                                                   \
+  {                                                                                           \
+    v4i av[2][MB];                                                                            \
+    TW_RDA(stage, 0, av[0]);                                                                  \
+    _Pragma("unroll") for (int t = 0; t < 8; t++) {                                           \
+      if (t < 7) TW_RDA(stage, t + 1, av[(t + 1) & 1]);                                       \
+      __builtin_amdgcn_sched_barrier(0);                                                      \
+      _Pragma("unroll") for (int nt = 0; nt < NB; nt++) {                                     \
+        const uint32_t x0 = WCUR[8 * nt + t];                                                 \
+        const v4i b0 = {(int)((x0 << 6) & 0xC0C0C0C0u), (int)((x0 << 4) & 0xC0C0C0C0u),       \
+                        (int)((x0 << 2) & 0xC0C0C0C0u), (int)(x0 & 0xC0C0C0C0u)};              \
+        _Pragma("unroll") for (int mt = 0; mt < MB; mt++)                                     \
+          acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[t & 1][mt], b0, acc[mt][nt], 0, 0, 0); \
+      }                                                                                       \
+    }                                                                                         \
+  }
+  // chunk c (stage SCUR, weights WCUR): wait for this wave's loads of chunk
+  // c's stage (a step issues its stage loads, then its NWL weight loads, so
+  // only the previous step's weight loads -- chunk c + 1's -- may still be
+  // out), meet the workgroup (every stage load of chunk c has landed; every
+  // wave is done reading SLOAD, chunk c - 1's stage), load chunk c + 1's
+  // activations into SLOAD and chunk c + 2's weights into WLOAD (clamped:
+  // the last fetches repeat), multiply chunk c
+#define TW_STEP(k, SCUR, SLOAD, WCUR, WLOAD)                                                  \
+  {                                                                                           \
+    const uint32_t c = c0 + (k);                                                              \
+    TW_ORDER();                                                                               \
+    __builtin_amdgcn_sched_barrier(0);                                                        \
+    TW_WAIT_VM(NWL);                                                                          \
+    __builtin_amdgcn_s_barrier();                                                             \
+    TW_ORDER();                                                                               \
+    TW_LOADA(c + 1 < nchunks ? c + 1 : nchunks - 1, SLOAD);                                   \
+    TW_ORDER();                                                                               \
+    TW_LOADW(c + 2 < nchunks ? c + 2 : nchunks - 1, WLOAD);                                   \
+    __builtin_amdgcn_sched_barrier(0);                                                        \
+    TW_MMA(SCUR, WCUR);                                                                       \
+  }
+  // whole groups of six chunks (stages alternate, weight sets rotate by
+  // three), then up to five, nested so that no register set is merged at a
+  // join
+  uint32_t c0 = 0;
+  for (; c0 + 6 <= nchunks; c0 += 6) {
+    TW_STEP(0, s_a0, s_a1, wA, wC)
+    TW_STEP(1, s_a1, s_a0, wB, wA)
+    TW_STEP(2, s_a0, s_a1, wC, wB)
+    TW_STEP(3, s_a1, s_a0, wA, wC)
+    TW_STEP(4, s_a0, s_a1, wB, wA)
+    TW_STEP(5, s_a1, s_a0, wC, wB)
+  }
+  if (c0 < nchunks) {
+    TW_STEP(0, s_a0, s_a1, wA, wC)
+    if (c0 + 1 < nchunks) {
+      TW_STEP(1, s_a1, s_a0, wB, wA)
+      if (c0 + 2 < nchunks) {
+        TW_STEP(2, s_a0, s_a1, wC, wB)
+        if (c0 + 3 < nchunks) {
+          TW_STEP(3, s_a1, s_a0, wA, wC)
+          if (c0 + 4 < nchunks) TW_STEP(4, s_a0, s_a1, wB, wA)
+        }
+      }
+    }
+  }
+#undef TW_STEP
+#undef TW_MMA
+#undef TW_RDA
+#undef TW_LOADW
+#undef TW_LOADA
+  // the last (repeated) stage loads must land before the workgroup's LDS is
+  // released
+  TW_WAIT_VM(0);
+  tl_epilogue<MB, NB, EPI>(a, acc, rw, rc, bo, be, s_gm, lane, 0, lg, tok0, s_tp, s_tb);
+}
+#undef TW_ORDER
+#undef TW_WAIT_VM
 
 // ------------------------------------------------------------ launchers
 
@@ -1211,6 +1440,32 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
     const dim3 grid(nlg_blocks(a.out, tile), ty, ks), blk(tile == 256 ? 512 : 256);
     if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
     const size_t lds = (size_t)2 * 128 * TL_PITCH;
+    // Enough 256-row x 128-token tiles to give every CU one: the wide-wave
+    // kernel (k_tgemm_w; its stage loads take 32-bit offsets).  Measured on
+    // the config-4 FFN (median of 10 interleaved launches): gate|up at 640 /
+    // 1024 / 2048 tokens (270 / 432 / 864 tiles) 37.0 / 40.6 / 76.2 us
+    // against k_tgemm_l's 40.9 / 44.5 / 85.9; at 512 tokens (216 tiles) 26.2
+    // against 23.7; the down projection at 2048 tokens (160 tiles) 54.7
+    // against 47.2, at 4096 (320) 95.2 against 100.7.
+    if (ks == 1 && tile == 256 && (uint64_t)nlg_blocks(a.out, 256) * ty >= (uint64_t)nlg_num_cu() &&
+        (uint64_t)a.seq * a.cols < (1ull << 32)) {
+      const dim3 gw(nlg_blocks(a.out, 256), ty);
+#define TWG(E)                                                                                   \
+  do {                                                                                           \
+    if (wt) hipLaunchKernelGGL((k_tgemm_w<E, true>), gw, dim3(256), 0, st, a);                  \
+    else hipLaunchKernelGGL((k_tgemm_w<E, false>), gw, dim3(256), 0, st, a);                    \
+  } while (0)
+      switch (epi) {
+        case NLG_EPI_STORE: TWG(NLG_EPI_STORE); break;
+        case NLG_EPI_RESID: TWG(NLG_EPI_RESID); break;
+        case NLG_EPI_SWIGLU: TWG(NLG_EPI_SWIGLU); break;
+        case NLG_EPI_QKV: TWG(NLG_EPI_QKV); break;
+        default: return nlg_fail("ternary GEMM: unknown epilogue %d", epi);
+      }
+#undef TWG
+      NLG_LAUNCHED("ternary GEMM (int8 MFMA, wide waves)");
+      return NLG_OK;
+    }
 #define TLT(E, T)                                                                                \
   do {                                                                                           \
     if (ks > 1) hipLaunchKernelGGL((k_tgemm_l<1, 2, E, true, T>), grid, blk, lds, st, a);        \

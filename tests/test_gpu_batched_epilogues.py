@@ -12,7 +12,11 @@ kernels on the CPU (tests/layer_ref.py):
   pos0 + r % qper).
 
 Each shape is chosen so the GEMM runs a given row tile: 256, 128 or 64 rows
-per workgroup (the largest whose grid still gives 256 workgroups).  Every
+per workgroup (the largest whose grid still gives 256 workgroups), or, once
+there are as many 256-row x 128-token tiles as CUs, the wide-wave kernel
+(k_tgemm_w: 4 waves of 64 rows x 128 tokens, activations staged by direct
+global-to-LDS loads), whose cases also cover every remainder of its
+six-chunk loop (1 to 10 chunks of 256 columns) and ragged rows.  Every
 case runs twice: with the weights' row layout, then with a registered tiled
 copy of them (nlg_ternary_tiled_register), which must give the same bits.  The
 activations of the RMSNorm cases are small integers, so the sum of squares
@@ -67,18 +71,21 @@ def with_tiled_copy(dw, rows, cols, run):
 
 
 def row_tile(seq, out):
-    """The GEMM's row tile for seq >= 128 tokens (nlg_tgemm.hip's choice)."""
+    """The GEMM's row tile for seq >= 128 tokens (nlg_tgemm.hip's choice);
+    "wide" for the wide-wave kernel."""
     ty = (seq + 127) // 128
     if (out + 255) // 256 * ty >= 128:
-        return 256
+        return "wide" if (out + 255) // 256 * ty >= nlgpu.device_info()[0] else 256
     if (out + 127) // 128 * ty >= 192:
         return 128
     return 64
 
 
-SWIGLU = [(128, 6912, 2560, True, 64), (512, 6912, 2560, True, 256), (600, 6912, 2560, True, 256),
+SWIGLU = [(128, 6912, 2560, True, 64), (512, 6912, 2560, True, 256), (600, 6912, 2560, True, "wide"),
           (512, 640, 2560, False, 64), (400, 4096, 1024, True, 256), (512, 3072, 1024, True, 128),
-          (300, 3840, 2560, False, 64)]
+          (300, 3840, 2560, False, 64),
+          (1200, 6144, 1024, True, "wide"),    # 4 chunks
+          (1100, 4096, 1536, False, "wide")]   # 6 chunks: one whole group
 
 
 @pytest.mark.parametrize("seq,dff,cols,rms,tile", SWIGLU)
@@ -106,8 +113,14 @@ def test_batched_swiglu(seq, dff, cols, rms, tile):
     same_bits(with_tiled_copy(dw, 2 * dff, cols, run), got, "tiled copy")
 
 
-RESID = [(128, 2560, 6912, 64), (512, 2560, 6912, 64), (512, 8192, 2560, 256), (600, 13824, 2560, 256),
-         (200, 1000, 512, 64), (512, 6144, 2560, 128), (512, 2560, 2560, 64)]
+RESID = [(128, 2560, 6912, 64), (512, 2560, 6912, 64), (512, 8192, 2560, 256), (600, 13824, 2560, "wide"),
+         (200, 1000, 512, 64), (512, 6144, 2560, 128), (512, 2560, 2560, 64),
+         (4096, 2048, 256, "wide"), (4096, 2048, 768, "wide"),  # 1 and 3 chunks
+         (4100, 2000, 1280, "wide"),                            # 5 chunks, ragged rows and tokens
+         (2700, 3000, 1792, "wide")]                            # 7 chunks: a group and one more
+
+
+_RESID_WANT = {}  # the last shape's reference (the in-place case follows the other)
 
 
 @pytest.mark.parametrize("inplace", [False, True])
@@ -130,8 +143,12 @@ def test_batched_residual(seq, out, cols, tile, inplace):
         return dy.download(f32, seq * out)
 
     got = run()
-    want = (res + ref.linear(x, w2, beta, seq, out, cols, bias=bias, per_row=bool(out % 3))).astype(f32)
-    same_bits(got, want, "residual")
+    key = (seq, out, cols)
+    if key not in _RESID_WANT:
+        _RESID_WANT.clear()
+        _RESID_WANT[key] = (res + ref.linear(x, w2, beta, seq, out, cols, bias=bias,
+                                             per_row=bool(out % 3))).astype(f32)
+    same_bits(got, _RESID_WANT[key], "residual")
     same_bits(with_tiled_copy(dw, out, cols, run), got, "tiled copy")
 
 
@@ -145,9 +162,11 @@ def rope_tables(max_seq, hd, theta=500000.0):
 QKV = [(512, 512, 20, 5, 128, 2560, 768, 0, 64),      # config 5's prompt at B = 1
        (600, 200, 64, 16, 128, 2560, 256, 40, 256),   # three prompts
        (512, 256, 32, 8, 128, 2560, 320, 40, 128),    # two prompts
-       (512, 128, 64, 32, 128, 2560, 160, 20, 256),   # four prompts
+       (512, 128, 64, 32, 128, 2560, 160, 20, "wide"),  # four prompts
        (128, 64, 8, 2, 64, 1024, 100, 50, 64),        # positions run past max_seq: no cache store there
-       (128, 0, 20, 5, 128, 2560, 16, 5, 64)]         # 128 decode rows at one position
+       (128, 0, 20, 5, 128, 2560, 16, 5, 64),         # 128 decode rows at one position
+       (2304, 256, 20, 5, 128, 2560, 320, 10, "wide"),  # nine prompts (10 chunks)
+       (2304, 0, 20, 5, 128, 512, 8, 3, "wide")]        # 2304 decode rows (2 chunks)
 
 
 @pytest.mark.parametrize("rows,qper,heads,kvh,hd,cols,max_seq,pos0,tile", QKV)
