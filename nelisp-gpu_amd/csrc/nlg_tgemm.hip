@@ -25,11 +25,10 @@
 // C[4(l/16) + r][l % 16].  Here i = token, j = output row, and lane group g
 // at step t of a chunk covers 2-bit word 4g + t of the chunk.
 //
-// 128 tokens and more: k_tgemm_l (32 x 32 x 32 MFMAs, 64 / 128 / 256-row
+// 128 tokens and more: k_tgemm_l (32 x 32 x 32 MFMAs, 64 / 128-row
 // workgroups of token-half waves, split over the columns when there are few
-// tiles) and, once there are as many 256-row x 128-token tiles as CUs,
-// k_tgemm_w (waves of 64 rows x 128 tokens fed by direct global-to-LDS
-// activation loads).
+// tiles) and, where 256-row tiles fill the GPU, k_tgemm_w (waves of 64 rows
+// x 128 or 64 tokens fed by direct global-to-LDS activation loads).
 #include <math.h>
 
 #include "nlg_quant.h"
@@ -1128,13 +1127,14 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
   tl_epilogue<2, NB, EPI>(a, acc, rw, rc, bo, be, s_gm, lane, wm, lg, tok0, s_tp, s_tb);
 }
 
-// Many tokens, wide waves: a workgroup owns 256 output rows x 128 tokens,
-// each of its 4 waves 64 rows (two 32-row blocks) x all 128 tokens (four
+// Many tokens, wide waves: a workgroup owns 256 output rows x MT = 32 MB
+// tokens (MB = 4, or 2 when 128-token tiles would leave CUs without one),
+// each of its 4 waves 64 rows (two 32-row blocks) x all MT tokens (MB
 // 32-token blocks).  Every weight chunk is fetched once per workgroup and
-// every decoded B operand feeds four MFMAs (k_tgemm_l's token-half waves
+// every decoded B operand feeds MB MFMAs (k_tgemm_l's token-half waves
 // fetch each chunk twice and feed two).  Activations go from global memory
 // straight to LDS (global_load_lds_dwordx4: no staging registers, no LDS
-// stores) into two [128 tokens][256 B] stages, one chunk ahead; their
+// stores) into two [MT tokens][256 B] stages, one chunk ahead; their
 // 16-byte units are XOR-swizzled by token (unit u of token k at slot
 // u ^ (k % 16)), so an operand read (16 consecutive tokens of one unit) hits
 // 16 distinct 16-byte bank groups, and one load instruction of a wave fills
@@ -1152,20 +1152,21 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
 // 4 waves (one workgroup per CU) and 534.8 / 254.7 with 8; persistent
 // workgroups that issue the next tile's first loads before the epilogue,
 // 699 with 4 waves (the tile loop spills).)
-#define TW_STAGE (128 * TG_KC)
+#define TW_STAGE (128 * TG_KC)  // bytes of a stage of 128 tokens
 // s_waitcnt vmcnt(n) lgkmcnt(0) (expcnt at its maximum: no wait)
 #define TW_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (0x7 << 4) | (((n) >> 4) << 14))
 // a compiler-level fence: no memory operation moves across it
 #define TW_ORDER() asm volatile("" ::: "memory")
 
-template <int EPI, bool TILED = false>
+template <int EPI, bool TILED = false, int MB = 4>
 __global__ __launch_bounds__(256, 2) void k_tgemm_w(GemmArgs a) {
-  constexpr int WR = 4, NB = 2, MB = 4;
-  constexpr int PI = TW_STAGE / 1024 / WR;  // 1 KiB stage loads per wave and chunk
+  constexpr int WR = 4, NB = 2, MT = 32 * MB;  // MT tokens per workgroup
+  constexpr int STAGE = MT * TG_KC;
+  constexpr int PI = STAGE / 1024 / WR;  // 1 KiB stage loads per wave and chunk
   constexpr int NWL = 2 * NB;               // weight load instructions per wave and chunk
   typedef uint32_t wvec __attribute__((ext_vector_type(8 * NB)));
-  __shared__ __align__(1024) uint8_t s_a0[TW_STAGE];
-  __shared__ __align__(1024) uint8_t s_a1[TW_STAGE];
+  __shared__ __align__(1024) uint8_t s_a0[STAGE];
+  __shared__ __align__(1024) uint8_t s_a1[STAGE];
   __shared__ float s_gm[128];
   __shared__ int32_t s_tp[EPI == NLG_EPI_QKV ? 128 : 1];
   __shared__ uint64_t s_tb[EPI == NLG_EPI_QKV ? 128 : 1];
@@ -1175,7 +1176,7 @@ __global__ __launch_bounds__(256, 2) void k_tgemm_w(GemmArgs a) {
   const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 31, lg = lane >> 5;
   const uint32_t rbase = blockIdx.x * (64 * WR) + wn * 64;
-  const uint32_t tok0 = blockIdx.y * 128;
+  const uint32_t tok0 = blockIdx.y * MT;
   const uint32_t nchunks = a.cols / TG_KC;
   // weight rows of this lane, as in k_tgemm_l
   uint32_t rw[NB], rc[NB];
@@ -1194,14 +1195,15 @@ __global__ __launch_bounds__(256, 2) void k_tgemm_w(GemmArgs a) {
   // Stage loads: wave wn's load i fills stage bytes [1024 b, 1024 b + 1024),
   // b = wn PI + i: lane j writes token k = 4 b + j / 16 (clamped to the last
   // real token), slot j % 16, i.e. unit (j % 16) ^ (k % 16) of its chunk row,
-  // at byte offset xo[i] from the chunk's column 0 (the launcher checks that
-  // seq x cols fits 32 bits, so the loads take a scalar base + 32-bit offset)
+  // at byte offset xo[i] from column 0 of the workgroup's first token row
+  // (under MT x 16384 bytes: the loads take a scalar base + 32-bit offset)
   uint32_t xo[PI];
 #pragma unroll
   for (int i = 0; i < PI; i++) {
     const uint32_t k = 4 * (wn * PI + i) + lane / 16, tk = tok0 + k < a.seq ? tok0 + k : a.seq - 1;
-    xo[i] = tk * a.cols + 16 * ((lane % 16) ^ (k % 16));
+    xo[i] = (tk - tok0) * a.cols + 16 * ((lane % 16) ^ (k % 16));
   }
+  const uint8_t *const xrow0 = a.xq + (size_t)tok0 * a.cols;
 #define TW_LOADW(c, dst)                                                                   \
   do {                                                                                     \
     _Pragma("unroll") for (int nt = 0; nt < NB; nt++) {                                    \
@@ -1214,7 +1216,7 @@ __global__ __launch_bounds__(256, 2) void k_tgemm_w(GemmArgs a) {
   } while (0)
 #define TW_LOADA(c, stage)                                                                 \
   do {                                                                                     \
-    const uint8_t *xc = a.xq + (size_t)(c) * TG_KC;                                        \
+    const uint8_t *xc = xrow0 + (size_t)(c) * TG_KC;                                       \
     _Pragma("unroll") for (int i = 0; i < PI; i++)                                         \
       __builtin_amdgcn_global_load_lds(                                                    \
           (const void *)(xc + xo[i]),                                                      \
@@ -1229,7 +1231,7 @@ __global__ __launch_bounds__(256, 2) void k_tgemm_w(GemmArgs a) {
     bo[nt] = a.bias ? a.bias[rc[nt]] : 0.0f;
     be[nt] = a.beta[a.beta_per_row ? rc[nt] : 0];
   }
-  const uint32_t tkc = tok0 + (threadIdx.x & 127u) < a.seq ? tok0 + (threadIdx.x & 127u) : a.seq - 1;
+  const uint32_t tkc = tok0 + threadIdx.x % MT < a.seq ? tok0 + threadIdx.x % MT : a.seq - 1;
   const float gm_r = a.gamma[tkc];
   int32_t tp_r = 0;
   uint64_t tb_r = 0;
@@ -1251,7 +1253,7 @@ __global__ __launch_bounds__(256, 2) void k_tgemm_w(GemmArgs a) {
   TW_ORDER();
   TW_LOADW(c1, wB);
   // (stored before the first step, whose wait includes lgkmcnt(0))
-  if (threadIdx.x < 128) {
+  if (threadIdx.x < MT) {
     s_gm[threadIdx.x] = gm_r;
     if (EPI == NLG_EPI_QKV) {
       s_tp[threadIdx.x] = tp_r;
@@ -1440,19 +1442,28 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
     const dim3 grid(nlg_blocks(a.out, tile), ty, ks), blk(tile == 256 ? 512 : 256);
     if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
     const size_t lds = (size_t)2 * 128 * TL_PITCH;
-    // Enough 256-row x 128-token tiles to give every CU one: the wide-wave
-    // kernel (k_tgemm_w; its stage loads take 32-bit offsets).  Measured on
-    // the config-4 FFN (median of 10 interleaved launches): gate|up at 640 /
-    // 1024 / 2048 tokens (270 / 432 / 864 tiles) 37.0 / 40.6 / 76.2 us
-    // against k_tgemm_l's 40.9 / 44.5 / 85.9; at 512 tokens (216 tiles) 26.2
-    // against 23.7; the down projection at 2048 tokens (160 tiles) 54.7
-    // against 47.2, at 4096 (320) 95.2 against 100.7.
-    if (ks == 1 && tile == 256 && (uint64_t)nlg_blocks(a.out, 256) * ty >= (uint64_t)nlg_num_cu() &&
-        (uint64_t)a.seq * a.cols < (1ull << 32)) {
-      const dim3 gw(nlg_blocks(a.out, 256), ty);
+    // 256-row tiles: the wide-wave kernel (k_tgemm_w), with 128-token tiles
+    // once there are as many of them as CUs, else 64-token ones (two waves
+    // per SIMD either way).  Measured on the config-4 FFN (median of 10..20
+    // interleaved launches, k_tgemm_l's 256-row tiles as the other side):
+    // gate|up at 640 / 1024 / 2048 / 16384 tokens with 128-token tiles
+    // (270 / 432 / 864 / 6912 tiles) 37.0 / 40.6 / 76.2 / 466.7 us against
+    // 40.9 / 44.5 / 85.9 / 556.4, the down projection at 4096 / 16384 tokens
+    // 95.2 / 225.6 against 100.7 / 244.8; with fewer tiles 128-token tiles
+    // leave SIMDs with one wave (gate|up at 512 tokens 26.2 against 23.7),
+    // and 64-token ones measured 23.1-23.8 against 24.2, at 300 tokens 20.9
+    // against 22.5, the down projection at 2048 tokens 45.5 against 47.8,
+    // QKV at 2048 tokens 24.9 against 25.2.
+    if (ks == 1 && tile == 256) {
+      const bool t128 = (uint64_t)nlg_blocks(a.out, 256) * ty >= (uint64_t)nlg_num_cu();
+      const dim3 gw(nlg_blocks(a.out, 256), t128 ? ty : (a.seq + 63) / 64);
+      if (gw.y > 65535) return nlg_fail("ternary GEMM: seq too large");
 #define TWG(E)                                                                                   \
   do {                                                                                           \
-    if (wt) hipLaunchKernelGGL((k_tgemm_w<E, true>), gw, dim3(256), 0, st, a);                  \
+    if (!t128) {                                                                                 \
+      if (wt) hipLaunchKernelGGL((k_tgemm_w<E, true, 2>), gw, dim3(256), 0, st, a);             \
+      else hipLaunchKernelGGL((k_tgemm_w<E, false, 2>), gw, dim3(256), 0, st, a);               \
+    } else if (wt) hipLaunchKernelGGL((k_tgemm_w<E, true>), gw, dim3(256), 0, st, a);           \
     else hipLaunchKernelGGL((k_tgemm_w<E, false>), gw, dim3(256), 0, st, a);                    \
   } while (0)
       switch (epi) {
@@ -1469,7 +1480,6 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
 #define TLT(E, T)                                                                                \
   do {                                                                                           \
     if (ks > 1) hipLaunchKernelGGL((k_tgemm_l<1, 2, E, true, T>), grid, blk, lds, st, a);        \
-    else if (tile == 256) hipLaunchKernelGGL((k_tgemm_l<2, 4, E, false, T>), grid, blk, lds, st, a); \
     else if (tile == 128) hipLaunchKernelGGL((k_tgemm_l<2, 2, E, false, T>), grid, blk, lds, st, a); \
     else hipLaunchKernelGGL((k_tgemm_l<1, 2, E, false, T>), grid, blk, lds, st, a);              \
   } while (0)

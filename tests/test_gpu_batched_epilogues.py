@@ -11,10 +11,10 @@ kernels on the CPU (tests/layer_ref.py):
   sequence s) and for prompt rows (row r = sequence r / qper at position
   pos0 + r % qper).
 
-Each shape is chosen so the GEMM runs a given row tile: 256, 128 or 64 rows
-per workgroup (the largest whose grid still gives 256 workgroups), or, once
-there are as many 256-row x 128-token tiles as CUs, the wide-wave kernel
-(k_tgemm_w: 4 waves of 64 rows x 128 tokens, activations staged by direct
+Each shape is chosen so the GEMM runs a given row tile: 128 or 64 rows per
+workgroup (k_tgemm_l), or 256 rows: the wide-wave kernel (k_tgemm_w: 4 waves
+of 64 rows x 128 tokens -- "wide" -- or x 64 tokens -- "wide64" -- when
+128-token tiles would not give every CU one; activations staged by direct
 global-to-LDS loads), whose cases also cover every remainder of its
 six-chunk loop (1 to 10 chunks of 256 columns) and ragged rows.  Every
 case runs twice: with the weights' row layout, then with a registered tiled
@@ -71,18 +71,19 @@ def with_tiled_copy(dw, rows, cols, run):
 
 
 def row_tile(seq, out):
-    """The GEMM's row tile for seq >= 128 tokens (nlg_tgemm.hip's choice);
-    "wide" for the wide-wave kernel."""
+    """The GEMM's row tile for seq >= 128 tokens (nlg_tgemm.hip's choice):
+    256-row tiles run the wide-wave kernel, "wide" with 128-token tiles once
+    there are as many as CUs, else "wide64" (64-token tiles)."""
     ty = (seq + 127) // 128
     if (out + 255) // 256 * ty >= 128:
-        return "wide" if (out + 255) // 256 * ty >= nlgpu.device_info()[0] else 256
+        return "wide" if (out + 255) // 256 * ty >= nlgpu.device_info()[0] else "wide64"
     if (out + 127) // 128 * ty >= 192:
         return 128
     return 64
 
 
-SWIGLU = [(128, 6912, 2560, True, 64), (512, 6912, 2560, True, 256), (600, 6912, 2560, True, "wide"),
-          (512, 640, 2560, False, 64), (400, 4096, 1024, True, 256), (512, 3072, 1024, True, 128),
+SWIGLU = [(128, 6912, 2560, True, 64), (512, 6912, 2560, True, "wide64"), (600, 6912, 2560, True, "wide"),
+          (512, 640, 2560, False, 64), (400, 4096, 1024, True, "wide64"), (512, 3072, 1024, True, 128),
           (300, 3840, 2560, False, 64),
           (1200, 6144, 1024, True, "wide"),    # 4 chunks
           (1100, 4096, 1536, False, "wide")]   # 6 chunks: one whole group
@@ -113,11 +114,12 @@ def test_batched_swiglu(seq, dff, cols, rms, tile):
     same_bits(with_tiled_copy(dw, 2 * dff, cols, run), got, "tiled copy")
 
 
-RESID = [(128, 2560, 6912, 64), (512, 2560, 6912, 64), (512, 8192, 2560, 256), (600, 13824, 2560, "wide"),
+RESID = [(128, 2560, 6912, 64), (512, 2560, 6912, 64), (512, 8192, 2560, "wide64"), (600, 13824, 2560, "wide"),
          (200, 1000, 512, 64), (512, 6144, 2560, 128), (512, 2560, 2560, 64),
          (4096, 2048, 256, "wide"), (4096, 2048, 768, "wide"),  # 1 and 3 chunks
          (4100, 2000, 1280, "wide"),                            # 5 chunks, ragged rows and tokens
-         (2700, 3000, 1792, "wide")]                            # 7 chunks: a group and one more
+         (2700, 3000, 1792, "wide"),                            # 7 chunks: a group and one more
+         (300, 13800, 768, "wide64"), (512, 8192, 1280, "wide64")]  # 3 and 5 chunks, ragged 64-token tiles
 
 
 _RESID_WANT = {}  # the last shape's reference (the in-place case follows the other)
@@ -160,7 +162,7 @@ def rope_tables(max_seq, hd, theta=500000.0):
 
 # rows, qper (0: decode rows), heads, kvheads, head_dim, cols, max_seq, pos0, tile
 QKV = [(512, 512, 20, 5, 128, 2560, 768, 0, 64),      # config 5's prompt at B = 1
-       (600, 200, 64, 16, 128, 2560, 256, 40, 256),   # three prompts
+       (600, 200, 64, 16, 128, 2560, 256, 40, "wide64"),  # three prompts
        (512, 256, 32, 8, 128, 2560, 320, 40, 128),    # two prompts
        (512, 128, 64, 32, 128, 2560, 160, 20, "wide"),  # four prompts
        (128, 64, 8, 2, 64, 1024, 100, 50, 64),        # positions run past max_seq: no cache store there
