@@ -25,10 +25,10 @@
 // C[4(l/16) + r][l % 16].  Here i = token, j = output row, and lane group g
 // at step t of a chunk covers 2-bit word 4g + t of the chunk.
 //
-// 128 tokens and more: k_tgemm_l (32 x 32 x 32 MFMAs, 64 / 128-row
-// workgroups of token-half waves, split over the columns when there are few
-// tiles) and, where 256-row tiles fill the GPU, k_tgemm_w (waves of 64 rows
-// x 128 or 64 tokens fed by direct global-to-LDS activation loads).
+// 128 tokens and more: k_tgemm_w (32 x 32 x 32 MFMAs; 256-row workgroups
+// whose waves own 64 rows x 64 or 32 tokens, fed by direct global-to-LDS
+// activation loads) and, for a few tiles of long rows, k_tgemm_l's column
+// split (64-row workgroups of token-half waves over gridDim.z slices).
 #include <math.h>
 
 #include "nlg_quant.h"
@@ -956,7 +956,8 @@ __device__ __forceinline__ void tl_epilogue(const GemmArgs &a, const v16i (&acc)
   }
 }
 
-// Many tokens (prefill): a workgroup owns 32 NB WR output rows x 128 tokens;
+// Many tokens, few tiles of long rows (the column-split form the launcher
+// runs: NB = 1, WR = 2): a workgroup owns 32 NB WR output rows x 128 tokens;
 // its 2 WR waves 32 NB rows x 64 tokens each (NB x 2 blocks of
 // v_mfma_i32_32x32x32_i8, whose layout, checked on gfx950, is
 // C[i][j] = sum over lane groups g = 0..1 and bytes b of
@@ -1128,11 +1129,10 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
 }
 
 // Many tokens, wide waves: a workgroup owns 256 output rows x MT = 32 MB
-// tokens (MB = 4, or 2 when 128-token tiles would leave CUs without one),
-// each of its 4 waves 64 rows (two 32-row blocks) x all MT tokens (MB
-// 32-token blocks).  Every weight chunk is fetched once per workgroup and
-// every decoded B operand feeds MB MFMAs (k_tgemm_l's token-half waves
-// fetch each chunk twice and feed two).  Activations go from global memory
+// tokens (the launcher runs MB = 2, or 1 for smaller grids), each of its 4
+// waves 64 rows (two 32-row blocks) x all MT tokens (MB 32-token blocks).
+// Every weight chunk is fetched once per workgroup (each wave owns its own
+// rows) and every decoded B operand feeds MB MFMAs.  Activations go from global memory
 // straight to LDS (global_load_lds_dwordx4: no staging registers, no LDS
 // stores) into two [MT tokens][256 B] stages, one chunk ahead; their
 // 16-byte units are XOR-swizzled by token (unit u of token k at slot
@@ -1143,16 +1143,19 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
 // of step t.  The stages are separate LDS arrays indexed statically (the
 // chunk loop unrolls by six), so the compiler can tell that a load into one
 // stage does not touch the other and does not wait for it before reading
-// the other.  Two 4-wave workgroups share a CU (66 KB of LDS and at most 256
-// VGPRs each), so each SIMD runs two waves whose barriers are independent.
+// the other.  Several 4-wave workgroups share a CU (MB = 2: 33 KB of LDS
+// and 164 VGPRs each), so each SIMD runs waves whose barriers are
+// independent.
 // (Measured at 16,384 tokens, config-4 FFN, median of 20 interleaved
-// launches: gate|up 466.7 us, down 225.6 us, against k_tgemm_l's 556.4 and
-// 244.8.  Rejected variants: one 8-wave workgroup of 512 rows per CU, 524.1
-// and 252.3; three stages, activations two chunks ahead, 656.5 / 280.5 with
-// 4 waves (one workgroup per CU) and 534.8 / 254.7 with 8; persistent
-// workgroups that issue the next tile's first loads before the epilogue,
-// 699 with 4 waves (the tile loop spills).)
-#define TW_STAGE (128 * TG_KC)  // bytes of a stage of 128 tokens
+// launches, the first form of this kernel -- MB = 4, 128-token tiles, two
+// workgroups per CU: gate|up 466.7 us, down 225.6 us, against the
+// token-half k_tgemm_l's 556.4 and 244.8; 64-token tiles then measured equal
+// or faster at every size (the launcher's sweep).  Rejected variants: one
+// 8-wave workgroup of 512 rows per CU, 524.1 and 252.3; three stages,
+// activations two chunks ahead, 656.5 / 280.5 with 4 waves (one workgroup
+// per CU) and 534.8 / 254.7 with 8; persistent workgroups that issue the
+// next tile's first loads before the epilogue, 699 with 4 waves (the tile
+// loop spills).)
 // s_waitcnt vmcnt(n) lgkmcnt(0) (expcnt at its maximum: no wait)
 #define TW_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (0x7 << 4) | (((n) >> 4) << 14))
 // a compiler-level fence: no memory operation moves across it
@@ -1387,36 +1390,46 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   const uint32_t *wt = nlg_tiled_find(a.w2, a.out, a.cols);
   if (wt) a.w2 = wt;
   if (a.seq >= 128 && epi != NLG_EPI_ARGMAX) {
-    // Row tile: 256 rows once that grid has 128 workgroups (one 8-wave
-    // workgroup per CU: fewer, larger tiles re-read the activations less),
-    // else 128 rows once that grid has 192, else 64.  Measured at 512 and
-    // 2048 tokens over the config-5 linears (STORE epilogue): gate|up at 512
-    // tokens 256-row tiles (216 workgroups) 27.2 us against 29.4 with 128;
-    // QKV, O and down at 2048 tokens (160..240 workgroups) 28.2 / 26.6 /
-    // 50.5 us against 30.6 / 28.4 / 54.7; QKV at 512 tokens 64-row tiles
-    // 13.8 us against 17.4 / 23.2.  (Gate|up at 2048 tokens, 864 256-row
-    // workgroups, is the exception: 98.3 us against 91.7 with 128.)
-    const uint32_t ty = (a.seq + 127) / 128;
-    const int tile = (uint64_t)nlg_blocks(a.out, 256) * ty >= 128   ? 256
-                     : (uint64_t)nlg_blocks(a.out, 128) * ty >= 192 ? 128
-                                                                    : 64;
-    // Too few 64-row tiles to fill the CUs (e.g. 2560 rows x 512 tokens):
-    // split the columns over gridDim.z slices (about 384 workgroups in all),
-    // when the per-stream split workspace is to be had.  Row layout: slices
-    // of at least 3 chunks, at most 8 (measured: down projection 2560 x 6912
-    // at 512 tokens 29.5 -> 24.5 us with 3 slices, at 128 tokens 25 -> 15
-    // us with 6; the O projection 2560 x 2560 at 512 tokens 15.6 us with 2
-    // slices, 14.8 with 3; 216 tiles gain nothing from 2).  Tiled copies,
-    // whose chunks cost less: only rows of 16+ chunks, in 2..4 slices
-    // (config-5 shapes: the down projection, 27 chunks, at 128 / 256 / 512
-    // tokens 23.9 / 24.5 / 26.1 us unsplit, 14.9 in 4 slices / 16.9 in 3 /
-    // 21.7 in 3, 17.4 in 8 at 128; QKV and O, 10 chunks, no faster split:
-    // QKV at 256 tokens 13.5 us unsplit, 15.4 in 3 slices, O at 512 14.6
-    // against 15.4).  Split 128- and 256-row tiles lose (the last slice to
-    // arrive reads every other slice's 64 KB of partials).
-    const uint32_t ntile = nlg_blocks(a.out, tile) * ty, nch = a.cols / TG_KC;
+    // 256-row tiles of the wide-wave kernel (k_tgemm_w), 64-token tiles
+    // once there are 400 of them, else 32-token ones; a few tiles of long
+    // rows split their columns instead (k_tgemm_l, below).  From a sweep of
+    // the config-5 linears and config 4 at 128..16384 tokens, tiled weights,
+    // kernel trace, median of 6..20 interleaved launches of each form:
+    //  * 32-token tiles against k_tgemm_l's (then) choice, residual
+    //    epilogue: QKV at 128 / 256 / 512 / 1024 tokens 11.6 / 11.4 / 13.5 /
+    //    17.5 us against 13.6 / 14.9 / 16.0 / 22.2; O 11.0 / 10.8 / 12.0 /
+    //    16.0 against 12.8 / 13.8 / 15.4 / 19.5; down at 512 / 1024 20.6 /
+    //    30.1 against 22.8 (split) / 39.3; gate|up at 128 / 256 12.1 / 17.8
+    //    against 14.5 / 22.4.
+    //  * 64-token tiles against 32-token ones: gate|up at 512 / 1024 / 2048 /
+    //    4096 / 16384 tokens (432..13824 tiles) 26.0 / 51.4 / 99.4 / 176.2 /
+    //    743 against 27.0 / 52.2 / 106.6 / 196.9 / 808; QKV at 2048 / 4096
+    //    (480 / 960) 27.4 / 50.7 against 28.1 / 52.6; but O and down at 2048
+    //    (320) 24.5 / 47.4 against 21.6 / 43.2, QKV at 1024 (240) 19.8
+    //    against 17.5.
+    //  * 128-token tiles (4 token blocks per wave, two workgroups per CU)
+    //    against 64-token ones, same epilogues as config 4: gate|up (SwiGLU)
+    //    at 1024 / 2048 / 4096 / 16384 tokens 40.3 / 75.6 / 156.5 / 550.4
+    //    against 40.2 / 68.9 / 150.2 / 550.0, down (STORE) 49.8 / 54.7 /
+    //    102.1 / 265.3 against 29.8 / 44.8 / 81.9 / 251.5: not kept.
+    //  * the column split (64-row tiles of k_tgemm_l) against 32-token tiles
+    //    for the down projection (27 chunks): 128 tokens (40 tiles) 15.4
+    //    against 18.6 us, 256 tokens (80) 19.4 against 19.2, 512 (160) 22.8
+    //    against 20.6.
+    const uint32_t rt = nlg_blocks(a.out, 256);
+    const uint64_t t1 = (uint64_t)rt * ((a.seq + 31) / 32), t2 = (uint64_t)rt * ((a.seq + 63) / 64);
+    const uint32_t nch = a.cols / TG_KC, ty = (a.seq + 127) / 128, ntile = nlg_blocks(a.out, 64) * ty;
+    // The column split: 64-row tiles of 128 tokens over gridDim.z slices
+    // (about 384 workgroups in all), when the per-stream split workspace is
+    // to be had.  Row layout: slices of at least 3 chunks, at most 8
+    // (measured: down projection 2560 x 6912 at 512 tokens 29.5 -> 24.5 us
+    // with 3 slices, at 128 tokens 25 -> 15 us with 6).  Tiled copies, whose
+    // chunks cost less: only rows of 16+ chunks, in 2..4 slices (the down
+    // projection, 27 chunks, at 128 / 256 tokens 23.9 / 24.5 us unsplit,
+    // 14.9 in 4 slices / 16.9 in 3).  Split 128- and 256-row tiles lose (the
+    // last slice to arrive reads every other slice's partials).
     uint32_t ks = 1;
-    if (a.allow_split && tile == 64 && ntile < 192 && nch >= (wt ? 16u : 8u)) {
+    if (a.allow_split && t1 < 128 && ntile < 192 && nch >= (wt ? 16u : 8u)) {
       ks = (384 + ntile - 1) / ntile;
       if (wt) {
         if (ks < 2) ks = 2;
@@ -1425,13 +1438,10 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
         if (ks > nch / 3) ks = nch / 3;
         if (ks > 8) ks = 8;
       }
-    }
-    if (ks > 1) {
-      const uint32_t nthr = tile == 256 ? 512 : 256, nr = tile == 256 ? 64 : (tile == 128 ? 64 : 32);
       // the counters' region is the same for every launch (a split grid has
       // fewer than 256 tiles), so partial sums never land on a counter
       const size_t ctr_bytes = 256 * 4;
-      uint8_t *w = (uint8_t *)nlg_scratch_try(ctr_bytes + (size_t)ks * ntile * nthr * nr * 4, st, 1);
+      uint8_t *w = (uint8_t *)nlg_scratch_try(ctr_bytes + (size_t)ks * ntile * 256 * 32 * 4, st, 1);
       if (w) {
         a.kctr = (uint32_t *)w;
         a.ksum = (int32_t *)(w + ctr_bytes);
@@ -1439,65 +1449,49 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
         ks = 1;
       }
     }
-    const dim3 grid(nlg_blocks(a.out, tile), ty, ks), blk(tile == 256 ? 512 : 256);
-    if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
-    const size_t lds = (size_t)2 * 128 * TL_PITCH;
-    // 256-row tiles: the wide-wave kernel (k_tgemm_w), with 128-token tiles
-    // once there are as many of them as CUs, else 64-token ones (two waves
-    // per SIMD either way).  Measured on the config-4 FFN (median of 10..20
-    // interleaved launches, k_tgemm_l's 256-row tiles as the other side):
-    // gate|up at 640 / 1024 / 2048 / 16384 tokens with 128-token tiles
-    // (270 / 432 / 864 / 6912 tiles) 37.0 / 40.6 / 76.2 / 466.7 us against
-    // 40.9 / 44.5 / 85.9 / 556.4, the down projection at 4096 / 16384 tokens
-    // 95.2 / 225.6 against 100.7 / 244.8; with fewer tiles 128-token tiles
-    // leave SIMDs with one wave (gate|up at 512 tokens 26.2 against 23.7),
-    // and 64-token ones measured 23.1-23.8 against 24.2, at 300 tokens 20.9
-    // against 22.5, the down projection at 2048 tokens 45.5 against 47.8,
-    // QKV at 2048 tokens 24.9 against 25.2.
-    if (ks == 1 && tile == 256) {
-      const bool t128 = (uint64_t)nlg_blocks(a.out, 256) * ty >= (uint64_t)nlg_num_cu();
-      const dim3 gw(nlg_blocks(a.out, 256), t128 ? ty : (a.seq + 63) / 64);
-      if (gw.y > 65535) return nlg_fail("ternary GEMM: seq too large");
-#define TWG(E)                                                                                   \
-  do {                                                                                           \
-    if (!t128) {                                                                                 \
-      if (wt) hipLaunchKernelGGL((k_tgemm_w<E, true, 2>), gw, dim3(256), 0, st, a);             \
-      else hipLaunchKernelGGL((k_tgemm_w<E, false, 2>), gw, dim3(256), 0, st, a);               \
-    } else if (wt) hipLaunchKernelGGL((k_tgemm_w<E, true>), gw, dim3(256), 0, st, a);           \
-    else hipLaunchKernelGGL((k_tgemm_w<E, false>), gw, dim3(256), 0, st, a);                    \
-  } while (0)
-      switch (epi) {
-        case NLG_EPI_STORE: TWG(NLG_EPI_STORE); break;
-        case NLG_EPI_RESID: TWG(NLG_EPI_RESID); break;
-        case NLG_EPI_SWIGLU: TWG(NLG_EPI_SWIGLU); break;
-        case NLG_EPI_QKV: TWG(NLG_EPI_QKV); break;
-        default: return nlg_fail("ternary GEMM: unknown epilogue %d", epi);
-      }
-#undef TWG
-      NLG_LAUNCHED("ternary GEMM (int8 MFMA, wide waves)");
-      return NLG_OK;
-    }
-#define TLT(E, T)                                                                                \
-  do {                                                                                           \
-    if (ks > 1) hipLaunchKernelGGL((k_tgemm_l<1, 2, E, true, T>), grid, blk, lds, st, a);        \
-    else if (tile == 128) hipLaunchKernelGGL((k_tgemm_l<2, 2, E, false, T>), grid, blk, lds, st, a); \
-    else hipLaunchKernelGGL((k_tgemm_l<1, 2, E, false, T>), grid, blk, lds, st, a);              \
-  } while (0)
+    if (ks > 1) {
+      const dim3 grid(nlg_blocks(a.out, 64), ty, ks);
+      if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
+      const size_t lds = (size_t)2 * 128 * TL_PITCH;
 #define TLG(E)                                                                                   \
   do {                                                                                           \
-    if (wt) TLT(E, true);                                                                        \
-    else TLT(E, false);                                                                          \
+    if (wt) hipLaunchKernelGGL((k_tgemm_l<1, 2, E, true, true>), grid, dim3(256), lds, st, a);  \
+    else hipLaunchKernelGGL((k_tgemm_l<1, 2, E, true, false>), grid, dim3(256), lds, st, a);    \
+  } while (0)
+      switch (epi) {
+        case NLG_EPI_STORE: TLG(NLG_EPI_STORE); break;
+        case NLG_EPI_RESID: TLG(NLG_EPI_RESID); break;
+        case NLG_EPI_SWIGLU: TLG(NLG_EPI_SWIGLU); break;
+        case NLG_EPI_QKV: TLG(NLG_EPI_QKV); break;
+        default: return nlg_fail("ternary GEMM: unknown epilogue %d", epi);
+      }
+#undef TLG
+      NLG_LAUNCHED("ternary GEMM (int8 MFMA, column split)");
+      return NLG_OK;
+    }
+    const bool t64 = t2 >= 400;
+    const dim3 gw(rt, t64 ? (a.seq + 63) / 64 : (a.seq + 31) / 32);
+    if (gw.y > 65535) return nlg_fail("ternary GEMM: seq too large");
+#define TWT(E, T)                                                                                \
+  do {                                                                                           \
+    if (t64) hipLaunchKernelGGL((k_tgemm_w<E, T, 2>), gw, dim3(256), 0, st, a);                 \
+    else hipLaunchKernelGGL((k_tgemm_w<E, T, 1>), gw, dim3(256), 0, st, a);                     \
+  } while (0)
+#define TWG(E)                                                                                   \
+  do {                                                                                           \
+    if (wt) TWT(E, true);                                                                        \
+    else TWT(E, false);                                                                          \
   } while (0)
     switch (epi) {
-      case NLG_EPI_STORE: TLG(NLG_EPI_STORE); break;
-      case NLG_EPI_RESID: TLG(NLG_EPI_RESID); break;
-      case NLG_EPI_SWIGLU: TLG(NLG_EPI_SWIGLU); break;
-      case NLG_EPI_QKV: TLG(NLG_EPI_QKV); break;
+      case NLG_EPI_STORE: TWG(NLG_EPI_STORE); break;
+      case NLG_EPI_RESID: TWG(NLG_EPI_RESID); break;
+      case NLG_EPI_SWIGLU: TWG(NLG_EPI_SWIGLU); break;
+      case NLG_EPI_QKV: TWG(NLG_EPI_QKV); break;
       default: return nlg_fail("ternary GEMM: unknown epilogue %d", epi);
     }
-#undef TLG
-#undef TLT
-    NLG_LAUNCHED("ternary GEMM (int8 MFMA, 128 x 128 tiles)");
+#undef TWG
+#undef TWT
+    NLG_LAUNCHED("ternary GEMM (int8 MFMA, wide waves)");
     return NLG_OK;
   }
   // up to 32 tokens per workgroup: the 32 x 2064-byte activation block

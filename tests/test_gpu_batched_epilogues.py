@@ -11,12 +11,12 @@ kernels on the CPU (tests/layer_ref.py):
   sequence s) and for prompt rows (row r = sequence r / qper at position
   pos0 + r % qper).
 
-Each shape is chosen so the GEMM runs a given row tile: 128 or 64 rows per
-workgroup (k_tgemm_l), or 256 rows: the wide-wave kernel (k_tgemm_w: 4 waves
-of 64 rows x 128 tokens -- "wide" -- or x 64 tokens -- "wide64" -- when
-128-token tiles would not give every CU one; activations staged by direct
-global-to-LDS loads), whose cases also cover every remainder of its
-six-chunk loop (1 to 10 chunks of 256 columns) and ragged rows.  Every
+Each shape is chosen so the GEMM runs a given form: the wide-wave kernel
+(k_tgemm_w: 256-row tiles, 4 waves of 64 rows x 64 tokens -- "w64" -- or x 32
+tokens -- "w32"; activations staged by direct global-to-LDS loads), whose
+cases cover every remainder of its six-chunk loop (1 to 10 chunks of 256
+columns, 27) and ragged rows and tokens for both tile heights, or the column
+split of k_tgemm_l's 64-row tiles for few tiles of long rows ("split").  Every
 case runs twice: with the weights' row layout, then with a registered tiled
 copy of them (nlg_ternary_tiled_register), which must give the same bits.  The
 activations of the RMSNorm cases are small integers, so the sum of squares
@@ -70,28 +70,30 @@ def with_tiled_copy(dw, rows, cols, run):
         nlgpu.ternary_tiled_unregister(dw)
 
 
-def row_tile(seq, out):
-    """The GEMM's row tile for seq >= 128 tokens (nlg_tgemm.hip's choice):
-    256-row tiles run the wide-wave kernel, "wide" with 128-token tiles once
-    there are as many as CUs, else "wide64" (64-token tiles)."""
-    ty = (seq + 127) // 128
-    if (out + 255) // 256 * ty >= 128:
-        return "wide" if (out + 255) // 256 * ty >= nlgpu.device_info()[0] else "wide64"
-    if (out + 127) // 128 * ty >= 192:
-        return 128
-    return 64
+def row_tile(seq, out, cols):
+    """The batched GEMM's form for seq >= 128 tokens with the row layout
+    (nlg_tgemm.hip's choice): "split" -- k_tgemm_l's column split, for few
+    tiles of long rows -- else the wide-wave kernel's 256-row tiles of 64
+    tokens ("w64", once there are 400 of them) or 32 ("w32").  The tiled
+    copy splits rows of 16+ chunks only, so it can take the other form."""
+    rt = (out + 255) // 256
+    t1, t2 = rt * ((seq + 31) // 32), rt * ((seq + 63) // 64)
+    ntile = (out + 63) // 64 * ((seq + 127) // 128)
+    if t1 < 128 and ntile < 192 and cols // 256 >= 8:
+        return "split"
+    return "w64" if t2 >= 400 else "w32"
 
 
-SWIGLU = [(128, 6912, 2560, True, 64), (512, 6912, 2560, True, "wide64"), (600, 6912, 2560, True, "wide"),
-          (512, 640, 2560, False, 64), (400, 4096, 1024, True, "wide64"), (512, 3072, 1024, True, 128),
-          (300, 3840, 2560, False, 64),
-          (1200, 6144, 1024, True, "wide"),    # 4 chunks
-          (1100, 4096, 1536, False, "wide")]   # 6 chunks: one whole group
+SWIGLU = [(128, 6912, 2560, True, "w32"), (512, 6912, 2560, True, "w64"), (600, 6912, 2560, True, "w64"),
+          (512, 640, 2560, False, "split"), (400, 4096, 1024, True, "w32"), (512, 3072, 1024, True, "w32"),
+          (300, 3840, 2560, False, "w32"),
+          (1200, 6144, 1024, True, "w64"),   # 4 chunks
+          (1100, 4096, 1536, False, "w64")]  # 6 chunks: one whole group
 
 
 @pytest.mark.parametrize("seq,dff,cols,rms,tile", SWIGLU)
 def test_batched_swiglu(seq, dff, cols, rms, tile):
-    assert row_tile(seq, 2 * dff) == tile
+    assert row_tile(seq, 2 * dff, cols) == tile
     print(f"[gpu] batched swiglu seq={seq} dff={dff} cols={cols} rms={rms} tile={tile}", flush=True)
     x = int_rows(dff + seq, seq * cols) if rms else nlgpu.normal(dff + seq, seq * cols)
     g = gains(cols + 2, cols)
@@ -114,12 +116,13 @@ def test_batched_swiglu(seq, dff, cols, rms, tile):
     same_bits(with_tiled_copy(dw, 2 * dff, cols, run), got, "tiled copy")
 
 
-RESID = [(128, 2560, 6912, 64), (512, 2560, 6912, 64), (512, 8192, 2560, "wide64"), (600, 13824, 2560, "wide"),
-         (200, 1000, 512, 64), (512, 6144, 2560, 128), (512, 2560, 2560, 64),
-         (4096, 2048, 256, "wide"), (4096, 2048, 768, "wide"),  # 1 and 3 chunks
-         (4100, 2000, 1280, "wide"),                            # 5 chunks, ragged rows and tokens
-         (2700, 3000, 1792, "wide"),                            # 7 chunks: a group and one more
-         (300, 13800, 768, "wide64"), (512, 8192, 1280, "wide64")]  # 3 and 5 chunks, ragged 64-token tiles
+RESID = [(128, 2560, 6912, "split"), (512, 2560, 6912, "w32"), (512, 8192, 2560, "w32"), (600, 13824, 2560, "w64"),
+         (200, 1000, 512, "w32"), (512, 6144, 2560, "w32"), (512, 2560, 2560, "w32"),
+         (128, 2048, 256, "w32"), (256, 2048, 1536, "w32"), (300, 13800, 768, "w32"),  # 1, 6, 3 chunks
+         (512, 8192, 1280, "w32"),                                                      # 5 chunks
+         (4096, 2048, 256, "w64"), (4096, 2048, 768, "w64"),  # 1 and 3 chunks
+         (4100, 2000, 1280, "w64"),                            # 5 chunks, ragged rows and tokens
+         (2700, 3000, 1792, "w64")]                            # 7 chunks: a group and one more
 
 
 _RESID_WANT = {}  # the last shape's reference (the in-place case follows the other)
@@ -128,7 +131,7 @@ _RESID_WANT = {}  # the last shape's reference (the in-place case follows the ot
 @pytest.mark.parametrize("inplace", [False, True])
 @pytest.mark.parametrize("seq,out,cols,tile", RESID)
 def test_batched_residual(seq, out, cols, tile, inplace):
-    assert row_tile(seq, out) == tile
+    assert row_tile(seq, out, cols) == tile
     print(f"[gpu] batched residual seq={seq} out={out} cols={cols} tile={tile} inplace={inplace}", flush=True)
     x, res = nlgpu.normal(cols + seq, seq * cols), nlgpu.normal(out + seq, seq * out)
     w2, beta = weights(cols + out, out, cols, per_row=bool(out % 3))
@@ -161,21 +164,21 @@ def rope_tables(max_seq, hd, theta=500000.0):
 
 
 # rows, qper (0: decode rows), heads, kvheads, head_dim, cols, max_seq, pos0, tile
-QKV = [(512, 512, 20, 5, 128, 2560, 768, 0, 64),      # config 5's prompt at B = 1
-       (600, 200, 64, 16, 128, 2560, 256, 40, "wide64"),  # three prompts
-       (512, 256, 32, 8, 128, 2560, 320, 40, 128),    # two prompts
-       (512, 128, 64, 32, 128, 2560, 160, 20, "wide"),  # four prompts
-       (128, 64, 8, 2, 64, 1024, 100, 50, 64),        # positions run past max_seq: no cache store there
-       (128, 0, 20, 5, 128, 2560, 16, 5, 64),         # 128 decode rows at one position
-       (2304, 256, 20, 5, 128, 2560, 320, 10, "wide"),  # nine prompts (10 chunks)
-       (2304, 0, 20, 5, 128, 512, 8, 3, "wide")]        # 2304 decode rows (2 chunks)
+QKV = [(512, 512, 20, 5, 128, 2560, 768, 0, "w32"),     # config 5's prompt at B = 1
+       (600, 200, 64, 16, 128, 2560, 256, 40, "w64"),   # three prompts
+       (512, 256, 32, 8, 128, 2560, 320, 40, "w32"),    # two prompts
+       (512, 128, 64, 32, 128, 2560, 160, 20, "w64"),   # four prompts
+       (128, 64, 8, 2, 64, 1024, 100, 50, "w32"),       # positions run past max_seq: no cache store there
+       (128, 0, 20, 5, 128, 2560, 16, 5, "split"),      # 128 decode rows at one position
+       (2304, 256, 20, 5, 128, 2560, 320, 10, "w64"),   # nine prompts (10 chunks)
+       (2304, 0, 20, 5, 128, 512, 8, 3, "w64")]         # 2304 decode rows (2 chunks)
 
 
 @pytest.mark.parametrize("rows,qper,heads,kvh,hd,cols,max_seq,pos0,tile", QKV)
 def test_batched_qkv_rope_append(rows, qper, heads, kvh, hd, cols, max_seq, pos0, tile):
     nq, nkv = heads * hd, kvh * hd
     out = nq + 2 * nkv
-    assert row_tile(rows, out) == tile
+    assert row_tile(rows, out, cols) == tile
     print(f"[gpu] batched qkv rows={rows} qper={qper} heads={heads}/{kvh} hd={hd} pos0={pos0} tile={tile}",
           flush=True)
     nseq = rows // qper if qper else rows
