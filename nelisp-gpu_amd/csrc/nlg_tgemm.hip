@@ -27,8 +27,8 @@
 //
 // 128 tokens and more: k_tgemm_w (32 x 32 x 32 MFMAs; 256-row workgroups
 // whose waves own 64 rows x 64 or 32 tokens, fed by direct global-to-LDS
-// activation loads) and, for a few tiles of long rows, k_tgemm_l's column
-// split (64-row workgroups of token-half waves over gridDim.z slices).
+// activation loads), for a few tiles of long rows with their columns split
+// over gridDim.z slices.
 #include <math.h>
 
 #include "nlg_quant.h"
@@ -192,7 +192,7 @@ struct GemmArgs {
   float *pval;
   int32_t *pidx;
   uint32_t nparts;
-  // k_tgemm_l split over the columns: gridDim.z slices of the chunks, each
+  // k_tgemm_w split over the columns: gridDim.z slices of the chunks, each
   // slice's int32 accumulators to ksum (one block of registers per
   // (slice, tile, thread)), tile arrivals counted in kctr (zero between
   // launches); the last slice of a tile to arrive adds the others' and
@@ -282,7 +282,8 @@ __device__ __forceinline__ void tg_store(const GemmArgs &a, int lane, uint32_t r
 // arrays stay in registers) of PH chunks: cols <= 256 * PH * NPH.  The
 // epilogue's operands (gamma, the residual, RoPE entries) are fetched
 // before the first phase, not after the last.
-// With TILED, a.w2 is the registered tiled copy (k_tgemm_l): lane (lg, lr)'s
+// With TILED, a.w2 is the registered tiled copy (laid out for k_tgemm_w's
+// loads): lane (lg, lr)'s
 // 16 bytes of chunk c (words 4 lg .. 4 lg + 3 of its row, the row layout's
 // wrow[4 c + lg]) are unit 128 c + 64 (lg % 2) + 32 (lg / 2) + row % 32 of its
 // 32-row block's tiles, so a load instruction reads four 256-byte runs.
@@ -788,12 +789,13 @@ __global__ __launch_bounds__(256) void k_tgemm_k(GemmArgs a) {
   }
 }
 
-// ------------------------------------------------------------ k_tgemm_l
+// ------------------------------------------------------------ k_tgemm_w
 
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-// Column slices of one tile meet here (k_tgemm_l's split form).  Every slice leaves its accumulators in its own block of
-// ksum with agent-coherent (write-through) stores, waits for them to
+// Column slices of one tile meet here (k_tgemm_w's split form).  Every
+// slice leaves its accumulators in its own block of ksum with
+// agent-coherent (write-through) stores, waits for them to
 // complete, and counts itself in; the last to arrive reads the other
 // slices' blocks (agent-coherent loads, past any stale L2 copy), adds them
 // -- integer sums, the same in any order -- and returns true to run the
@@ -839,10 +841,10 @@ __device__ __forceinline__ bool tl_split_meet(const GemmArgs &a, v16i (&acc)[MB]
   return true;
 }
 
-// The epilogue of k_tgemm_l and k_tgemm_w: acc[mt][nt] of lane (li, lg) of
-// the wave at token half wm (k_tgemm_w: MB = 4 token blocks, wm = 0), rows
+// The epilogue of k_tgemm_w: acc[mt][nt] of lane (li, lg) of the wave (MB
+// token blocks from token tok0 + 64 wm; the kernel passes wm = 0), rows
 // rw[nt] (clamped rc[nt]), with bias bo and beta be per row block and the
-// workgroup's 128 gammas in s_gm.
+// workgroup's gammas in s_gm.
 //
 // QKV: s_tp holds each of the workgroup's 128 tokens' cache position (-1
 // where it is past max_seq) and s_tb its cache row's element offset
@@ -956,178 +958,6 @@ __device__ __forceinline__ void tl_epilogue(const GemmArgs &a, const v16i (&acc)
   }
 }
 
-// Many tokens, few tiles of long rows (the column-split form the launcher
-// runs: NB = 1, WR = 2): a workgroup owns 32 NB WR output rows x 128 tokens;
-// its 2 WR waves 32 NB rows x 64 tokens each (NB x 2 blocks of
-// v_mfma_i32_32x32x32_i8, whose layout, checked on gfx950, is
-// C[i][j] = sum over lane groups g = 0..1 and bytes b of
-// A[lane 32g + i][b] * B[lane 32g + j][b], lane l's result r at row
-// (r % 4) + 8 (r / 4) + 4 (l / 32), column l % 32).  Columns go in chunks
-// of 256 (8 MFMA steps): lane group g at step t covers 2-bit word 8g + t
-// of the chunk, so a lane's weights for a chunk are 8 consecutive words
-// (32 bytes) of its row.  Weights run two chunks ahead of the matrix
-// cores, activations one: chunk c+2's weights and chunk c+1's activations
-// are fetched while chunk c computes.  (Activations two chunks ahead, in
-// three more register sets, measured slower: 16,384-token gate|up 746 ->
-// 760 us, 512 tokens 28.6 -> 33.8 us.)  Every decoded B operand feeds two
-// MFMAs.
-
-#define TL_PITCH (TG_KC + 16)   // LDS row pitch (bytes) of the activation stage
-
-template <int NB, int WR, int EPI, bool SPLIT = false, bool TILED = false>
-__global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
-  typedef uint32_t wvec __attribute__((ext_vector_type(8 * NB)));
-  constexpr int AI = 16 / WR;  // 16-byte activation pieces per thread and chunk
-  typedef uint32_t avec __attribute__((ext_vector_type(4 * AI)));
-  extern __shared__ __align__(16) uint8_t s_a[];  // [2][128 tokens][TL_PITCH]
-  asm volatile("" ::"s"(a.xq), "s"(a.gamma), "s"(a.w2), "s"(a.bias), "s"(a.beta), "s"(a.y), "s"(a.seq),
-               "s"(a.out), "s"(a.cols), "s"(a.wng), "s"(a.ystride), "s"(a.beta_per_row));
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int wm = w & 1, wn = w >> 1;  // wave's token half, row block (of WR)
-  const int li = lane & 31, lg = lane >> 5;
-  const uint32_t rbase = blockIdx.x * (32 * NB * WR) + wn * (32 * NB);
-  const uint32_t tok0 = blockIdx.y * 128;
-  // this slice's chunks: [cfirst, nchunks)
-  const uint32_t ntot = a.cols / TG_KC, ks = SPLIT ? gridDim.z : 1;
-  const uint32_t cfirst = SPLIT ? blockIdx.z * ntot / ks : 0, nchunks = SPLIT ? (blockIdx.z + 1) * ntot / ks : ntot;
-  // weight rows of this lane: rbase + 32 nt + li (clamped; dead rows masked
-  // at the store).  Row layout: the lane's 32 bytes of a chunk are 16-byte
-  // units 4c, 4c + 1 from word 8 lg of its row.  Tiled layout (a.w2 is the
-  // tiled copy): units 128c + lane and 128c + 64 + lane of its row block's
-  // run of 2 KiB tiles, so each load of the wave is 1 KiB contiguous.
-  uint32_t rw[NB], rc[NB];
-  const uint4 *wp[NB];
-#pragma unroll
-  for (int nt = 0; nt < NB; nt++) {
-    rw[nt] = rbase + 32 * nt + li;
-    rc[nt] = rw[nt] < a.out ? rw[nt] : a.out - 1;
-    if (TILED) {
-      const uint32_t nrb = (a.out + 31) / 32, rb = rbase / 32 + nt < nrb ? rbase / 32 + nt : nrb - 1;
-      wp[nt] = (const uint4 *)a.w2 + (size_t)rb * ntot * 128 + lane;
-    } else {
-      wp[nt] = (const uint4 *)(a.w2 + (size_t)rc[nt] * a.wng) + 2 * lg;
-    }
-  }
-  // activation staging: thread t copies token t/16 + 8 WR i (i < AI), slot t % 16
-  const uint32_t slot = threadIdx.x % 16u, tsub = threadIdx.x / 16u;
-  const uint8_t *xb[AI];
-#pragma unroll
-  for (int i = 0; i < AI; i++) {
-    const uint32_t tk = tok0 + tsub + 8 * WR * i < a.seq ? tok0 + tsub + 8 * WR * i : a.seq - 1;
-    xb[i] = a.xq + (size_t)tk * a.cols + 16 * slot;
-  }
-#define TL_LOADW(c, dst)                                                                   \
-  do {                                                                                     \
-    _Pragma("unroll") for (int nt = 0; nt < NB; nt++) {                                    \
-      const uint4 u0 = TILED ? wp[nt][128 * (c)] : wp[nt][4 * (c)];                         \
-      const uint4 u1 = TILED ? wp[nt][128 * (c) + 64] : wp[nt][4 * (c) + 1];                \
-      dst[8 * nt + 0] = u0.x; dst[8 * nt + 1] = u0.y; dst[8 * nt + 2] = u0.z;               \
-      dst[8 * nt + 3] = u0.w; dst[8 * nt + 4] = u1.x; dst[8 * nt + 5] = u1.y;               \
-      dst[8 * nt + 6] = u1.z; dst[8 * nt + 7] = u1.w;                                       \
-    }                                                                                      \
-  } while (0)
-#define TL_LOADA(c, dst)                                                                   \
-  do {                                                                                     \
-    _Pragma("unroll") for (int i = 0; i < AI; i++) {                                       \
-      const uint4 u = *(const uint4 *)(xb[i] + (size_t)(c) * TG_KC);                       \
-      dst[4 * i] = u.x; dst[4 * i + 1] = u.y; dst[4 * i + 2] = u.z; dst[4 * i + 3] = u.w;  \
-    }                                                                                      \
-  } while (0)
-#define TL_STOREA(buf, src)                                                                \
-  do {                                                                                     \
-    _Pragma("unroll") for (int i = 0; i < AI; i++)                                         \
-      *(uint4 *)(s_a + (size_t)(buf) * 128 * TL_PITCH + (tsub + 8 * WR * i) * TL_PITCH + 16 * slot) = \
-          make_uint4(src[4 * i], src[4 * i + 1], src[4 * i + 2], src[4 * i + 3]);          \
-  } while (0)
-  // Weights run two chunks ahead in three register sets that rotate through
-  // a three-chunk unrolled loop, so no set is ever copied (a copy would wait
-  // on the loads still in flight); activations run one chunk ahead.
-  wvec wA, wB, wC;
-  avec aX;
-  const uint32_t c1 = nchunks > cfirst + 1 ? cfirst + 1 : cfirst;
-  TL_LOADW(cfirst, wA);
-  TL_LOADA(cfirst, aX);
-  // gamma of the workgroup's 128 tokens, for the epilogue (to LDS below,
-  // ordered before the epilogue by the main loop's barriers)
-  __shared__ float s_gm[128];
-  __shared__ int32_t s_tp[EPI == NLG_EPI_QKV ? 128 : 1];
-  __shared__ uint64_t s_tb[EPI == NLG_EPI_QKV ? 128 : 1];
-  const float gm_t = a.gamma[tok0 + (threadIdx.x & 127u) < a.seq ? tok0 + (threadIdx.x & 127u) : a.seq - 1];
-  TL_LOADW(c1, wB);
-  float bo[NB], be[NB];
-#pragma unroll
-  for (int nt = 0; nt < NB; nt++) {
-    bo[nt] = a.bias ? a.bias[rc[nt]] : 0.0f;
-    be[nt] = a.beta[a.beta_per_row ? rc[nt] : 0];
-  }
-  TL_STOREA(cfirst & 1, aX);
-  if (threadIdx.x < 128) s_gm[threadIdx.x] = gm_t;
-  if (EPI == NLG_EPI_QKV && threadIdx.x < 128) {
-    // token t's cache position (decode rows: pos[0]; prompt rows: pos[0] +
-    // t % qper) and sequence, for the epilogue
-    const uint32_t tkc = tok0 + threadIdx.x < a.seq ? tok0 + threadIdx.x : a.seq - 1;
-    const int32_t pr = nlg_ld_uniform_i32(a.pos) + (a.qper ? (int32_t)(tkc % a.qper) : 0);
-    const bool ok = pr >= 0 && (uint32_t)pr < a.max_seq;
-    const uint32_t sq = a.qper ? tkc / a.qper : tkc;
-    s_tp[threadIdx.x] = ok ? pr : -1;
-    s_tb[threadIdx.x] = ((uint64_t)sq * a.kvheads * a.max_seq + (ok ? (uint32_t)pr : 0u)) * a.hd;
-  }
-  v16i acc[2][NB];  // [token block][row block]
-#pragma unroll
-  for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-    for (int nt = 0; nt < NB; nt++) acc[mt][nt] = (v16i){};
-  const uint8_t *sa0 = s_a + (size_t)(wm * 64 + li) * TL_PITCH + 16 * (8 * lg);
-  const uint8_t *sa1 = sa0 + 32 * TL_PITCH;
-  // each A fragment (a0, a1) feeds NB matrix-core steps, each decoded B operand two
-#define TL_MMA(buf, WCUR)                                                                    \
-  _Pragma("unroll") for (int t = 0; t < 8; t++) {                                             \
-    const uint4 av0 = *(const uint4 *)(sa0 + (buf) * 128 * TL_PITCH + 16 * t);                \
-    const uint4 av1 = *(const uint4 *)(sa1 + (buf) * 128 * TL_PITCH + 16 * t);                \
-    const v4i a0 = {(int)av0.x, (int)av0.y, (int)av0.z, (int)av0.w};                          \
-    const v4i a1 = {(int)av1.x, (int)av1.y, (int)av1.z, (int)av1.w};                          \
-    _Pragma("unroll") for (int nt = 0; nt < NB; nt++) {                                       \
-      const uint32_t x0 = WCUR[8 * nt + t];                                                   \
-      const v4i b0 = {(int)((x0 << 6) & 0xC0C0C0C0u), (int)((x0 << 4) & 0xC0C0C0C0u),         \
-                      (int)((x0 << 2) & 0xC0C0C0C0u), (int)(x0 & 0xC0C0C0C0u)};                \
-      acc[0][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc[0][nt], 0, 0, 0);        \
-      acc[1][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc[1][nt], 0, 0, 0);        \
-    }                                                                                         \
-  }
-  // chunk c: fetch chunk c + 1's activations, then chunk c + 2's weights
-  // (in that order: the staging store of the activations waits on its loads
-  // only), clamped so the last fetches repeat; multiply chunk c, stage c + 1
-#define TL_STEP(k, WCUR, WLOAD)                                                               \
-  {                                                                                           \
-    const uint32_t c = c0 + (k);                                                              \
-    TL_LOADA(c + 1 < nchunks ? c + 1 : nchunks - 1, aX);                                      \
-    TL_LOADW(c + 2 < nchunks ? c + 2 : nchunks - 1, WLOAD);                                   \
-    __syncthreads();                                                                          \
-    TL_MMA(c & 1, WCUR);                                                                      \
-    TL_STOREA((c + 1) & 1, aX);                                                               \
-  }
-  // whole groups of three chunks without branches (a conditional step would
-  // merge register sets at its join and copy them), then the last one or two
-  uint32_t c0 = cfirst;
-  for (; c0 + 3 <= nchunks; c0 += 3) {
-    TL_STEP(0, wA, wC)
-    TL_STEP(1, wB, wA)
-    TL_STEP(2, wC, wB)
-  }
-  if (c0 < nchunks) TL_STEP(0, wA, wC)
-  if (c0 + 1 < nchunks) TL_STEP(1, wB, wA)
-#undef TL_STEP
-#undef TL_MMA
-#undef TL_LOADW
-#undef TL_LOADA
-#undef TL_STOREA
-  if (SPLIT) {
-    __shared__ uint32_t s_last;
-    if (!tl_split_meet<2, NB>(a, acc, &s_last)) return;
-  }
-  tl_epilogue<2, NB, EPI>(a, acc, rw, rc, bo, be, s_gm, lane, wm, lg, tok0, s_tp, s_tb);
-}
-
 // Many tokens, wide waves: a workgroup owns 256 output rows x MT = 32 MB
 // tokens (the launcher runs MB = 2, or 1 for smaller grids), each of its 4
 // waves 64 rows (two 32-row blocks) x all MT tokens (MB 32-token blocks).
@@ -1149,7 +979,7 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
 // (Measured at 16,384 tokens, config-4 FFN, median of 20 interleaved
 // launches, the first form of this kernel -- MB = 4, 128-token tiles, two
 // workgroups per CU: gate|up 466.7 us, down 225.6 us, against the
-// token-half k_tgemm_l's 556.4 and 244.8; 64-token tiles then measured equal
+// token-half form it replaced, 556.4 and 244.8; 64-token tiles then measured equal
 // or faster at every size (the launcher's sweep).  Rejected variants: one
 // 8-wave workgroup of 512 rows per CU, 524.1 and 252.3; three stages,
 // activations two chunks ahead, 656.5 / 280.5 with 4 waves (one workgroup
@@ -1161,7 +991,7 @@ __global__ __launch_bounds__(128 * WR) void k_tgemm_l(GemmArgs a) {
 // a compiler-level fence: no memory operation moves across it
 #define TW_ORDER() asm volatile("" ::: "memory")
 
-template <int EPI, bool TILED = false, int MB = 4>
+template <int EPI, bool TILED = false, int MB = 4, bool SPLIT = false>
 __global__ __launch_bounds__(256, 2) void k_tgemm_w(GemmArgs a) {
   constexpr int WR = 4, NB = 2, MT = 32 * MB;  // MT tokens per workgroup
   constexpr int STAGE = MT * TG_KC;
@@ -1180,8 +1010,12 @@ __global__ __launch_bounds__(256, 2) void k_tgemm_w(GemmArgs a) {
   const int li = lane & 31, lg = lane >> 5;
   const uint32_t rbase = blockIdx.x * (64 * WR) + wn * 64;
   const uint32_t tok0 = blockIdx.y * MT;
-  const uint32_t nchunks = a.cols / TG_KC;
-  // weight rows of this lane, as in k_tgemm_l
+  // SPLIT: slice blockIdx.z of gridDim.z takes chunks cfirst .. + nchunks - 1
+  const uint32_t ntot = a.cols / TG_KC, ks = SPLIT ? gridDim.z : 1;
+  const uint32_t cfirst = SPLIT ? blockIdx.z * ntot / ks : 0;
+  const uint32_t nchunks = SPLIT ? (blockIdx.z + 1) * ntot / ks - cfirst : ntot;
+  // weight rows of this lane: lane group lg holds words 8 lg .. 8 lg + 7 of
+  // each chunk of rows rw[nt] (the tiled copy stores them in that order)
   uint32_t rw[NB], rc[NB];
   const uint4 *wp[NB];
 #pragma unroll
@@ -1190,9 +1024,9 @@ __global__ __launch_bounds__(256, 2) void k_tgemm_w(GemmArgs a) {
     rc[nt] = rw[nt] < a.out ? rw[nt] : a.out - 1;
     if (TILED) {
       const uint32_t nrb = (a.out + 31) / 32, rb = rbase / 32 + nt < nrb ? rbase / 32 + nt : nrb - 1;
-      wp[nt] = (const uint4 *)a.w2 + (size_t)rb * nchunks * 128 + lane;
+      wp[nt] = (const uint4 *)a.w2 + ((size_t)rb * ntot + cfirst) * 128 + lane;
     } else {
-      wp[nt] = (const uint4 *)(a.w2 + (size_t)rc[nt] * a.wng) + 2 * lg;
+      wp[nt] = (const uint4 *)(a.w2 + (size_t)rc[nt] * a.wng) + 2 * lg + 4 * cfirst;
     }
   }
   // Stage loads: wave wn's load i fills stage bytes [1024 b, 1024 b + 1024),
@@ -1206,7 +1040,7 @@ __global__ __launch_bounds__(256, 2) void k_tgemm_w(GemmArgs a) {
     const uint32_t k = 4 * (wn * PI + i) + lane / 16, tk = tok0 + k < a.seq ? tok0 + k : a.seq - 1;
     xo[i] = (tk - tok0) * a.cols + 16 * ((lane % 16) ^ (k % 16));
   }
-  const uint8_t *const xrow0 = a.xq + (size_t)tok0 * a.cols;
+  const uint8_t *const xrow0 = a.xq + (size_t)tok0 * a.cols + (size_t)cfirst * TG_KC;
 #define TW_LOADW(c, dst)                                                                   \
   do {                                                                                     \
     _Pragma("unroll") for (int nt = 0; nt < NB; nt++) {                                    \
@@ -1350,6 +1184,10 @@ __global__ __launch_bounds__(256, 2) void k_tgemm_w(GemmArgs a) {
   // the last (repeated) stage loads must land before the workgroup's LDS is
   // released
   TW_WAIT_VM(0);
+  if (SPLIT) {
+    __shared__ uint32_t s_last;
+    if (!tl_split_meet<MB, NB>(a, acc, &s_last)) return;
+  }
   tl_epilogue<MB, NB, EPI>(a, acc, rw, rc, bo, be, s_gm, lane, 0, lg, tok0, s_tp, s_tb);
 }
 #undef TW_ORDER
@@ -1392,15 +1230,15 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   if (a.seq >= 128 && epi != NLG_EPI_ARGMAX) {
     // 256-row tiles of the wide-wave kernel (k_tgemm_w), 64-token tiles
     // once there are 400 of them, else 32-token ones; a few tiles of long
-    // rows split their columns instead (k_tgemm_l, below).  From a sweep of
-    // the config-5 linears and config 4 at 128..16384 tokens, tiled weights,
-    // kernel trace, median of 6..20 interleaved launches of each form:
-    //  * 32-token tiles against k_tgemm_l's (then) choice, residual
-    //    epilogue: QKV at 128 / 256 / 512 / 1024 tokens 11.6 / 11.4 / 13.5 /
-    //    17.5 us against 13.6 / 14.9 / 16.0 / 22.2; O 11.0 / 10.8 / 12.0 /
-    //    16.0 against 12.8 / 13.8 / 15.4 / 19.5; down at 512 / 1024 20.6 /
-    //    30.1 against 22.8 (split) / 39.3; gate|up at 128 / 256 12.1 / 17.8
-    //    against 14.5 / 22.4.
+    // rows split their columns over gridDim.z slices.  From sweeps of the
+    // config-5 linears and config 4 at 128..16384 tokens, kernel trace,
+    // median of 6..20 interleaved launches of each form:
+    //  * 32-token tiles against the token-half 64-row-tile form this kernel
+    //    replaced, tiled weights, residual epilogue: QKV at 128 / 256 / 512 /
+    //    1024 tokens 11.6 / 11.4 / 13.5 / 17.5 us against 13.6 / 14.9 / 16.0
+    //    / 22.2; O 11.0 / 10.8 / 12.0 / 16.0 against 12.8 / 13.8 / 15.4 /
+    //    19.5; down at 1024 30.1 against 39.3; gate|up at 128 / 256 12.1 /
+    //    17.8 against 14.5 / 22.4.
     //  * 64-token tiles against 32-token ones: gate|up at 512 / 1024 / 2048 /
     //    4096 / 16384 tokens (432..13824 tiles) 26.0 / 51.4 / 99.4 / 176.2 /
     //    743 against 27.0 / 52.2 / 106.6 / 196.9 / 808; QKV at 2048 / 4096
@@ -1412,36 +1250,36 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
     //    at 1024 / 2048 / 4096 / 16384 tokens 40.3 / 75.6 / 156.5 / 550.4
     //    against 40.2 / 68.9 / 150.2 / 550.0, down (STORE) 49.8 / 54.7 /
     //    102.1 / 265.3 against 29.8 / 44.8 / 81.9 / 251.5: not kept.
-    //  * the column split (64-row tiles of k_tgemm_l) against 32-token tiles
-    //    for the down projection (27 chunks): 128 tokens (40 tiles) 15.4
-    //    against 18.6 us, 256 tokens (80) 19.4 against 19.2, 512 (160) 22.8
-    //    against 20.6.
+    //  * the column split of 32-token tiles, 2 / 3 / 4 slices against none,
+    //    tiled weights (row layout within 1 us of these): down projection
+    //    (2560 x 6912, 27 chunks) at 128 tokens (40 tiles) 15.0 / 14.3 /
+    //    14.4 against 19.4, 256 (80) 15.9 / 15.1 / 17.7 against 19.6, 384
+    //    (120) 17.2 / 19.2 / 18.2 against 20.0, 512 (160) 22.6 / 20.0 / 22.7
+    //    against 21.0, 640 (200) 23.2 / 24.9 / 26.1 against 21.5; 1024 x 6912
+    //    at 128 (16) 15.0 / 14.3 / 13.3 against 18.5; 2560 x 4096 at 128 (40)
+    //    12.8 / 12.1 / 12.5 against 14.2; but rows of 10 chunks never gain
+    //    (O 2560 x 2560 at 128 / 256 / 512 tokens 10.3 / 10.5 / 11.9 unsplit,
+    //    10.9 / 11.8 / 15.3 in 2 slices; QKV 3840 x 2560 likewise).  The
+    //    split form the kernel replaced (64-row tiles of token-half waves)
+    //    took 16.2 / 20.0 / 20.5 us for the down projection at 128 / 256 /
+    //    384 tokens.  Every slice leaves a 32 KB block of partial sums and
+    //    the last to arrive reads the others (tl_split_meet), so a slice
+    //    must carry enough chunks: rows of 16+ chunks only, and about one
+    //    workgroup per CU in all (two at 160 tiles).
     const uint32_t rt = nlg_blocks(a.out, 256);
-    const uint64_t t1 = (uint64_t)rt * ((a.seq + 31) / 32), t2 = (uint64_t)rt * ((a.seq + 63) / 64);
-    const uint32_t nch = a.cols / TG_KC, ty = (a.seq + 127) / 128, ntile = nlg_blocks(a.out, 64) * ty;
-    // The column split: 64-row tiles of 128 tokens over gridDim.z slices
-    // (about 384 workgroups in all), when the per-stream split workspace is
-    // to be had.  Row layout: slices of at least 3 chunks, at most 8
-    // (measured: down projection 2560 x 6912 at 512 tokens 29.5 -> 24.5 us
-    // with 3 slices, at 128 tokens 25 -> 15 us with 6).  Tiled copies, whose
-    // chunks cost less: only rows of 16+ chunks, in 2..4 slices (the down
-    // projection, 27 chunks, at 128 / 256 tokens 23.9 / 24.5 us unsplit,
-    // 14.9 in 4 slices / 16.9 in 3).  Split 128- and 256-row tiles lose (the
-    // last slice to arrive reads every other slice's partials).
+    const uint64_t n32 = (a.seq + 31) / 32, t1 = (uint64_t)rt * n32, t2 = (uint64_t)rt * ((a.seq + 63) / 64);
+    const uint32_t nch = a.cols / TG_KC;
     uint32_t ks = 1;
-    if (a.allow_split && t1 < 128 && ntile < 192 && nch >= (wt ? 16u : 8u)) {
-      ks = (384 + ntile - 1) / ntile;
-      if (wt) {
-        if (ks < 2) ks = 2;
-        if (ks > 4) ks = 4;
-      } else {
-        if (ks > nch / 3) ks = nch / 3;
-        if (ks > 8) ks = 8;
-      }
-      // the counters' region is the same for every launch (a split grid has
-      // fewer than 256 tiles), so partial sums never land on a counter
+    if (a.allow_split && nch >= 16) {
+      if (t1 <= 128) ks = 256 / (uint32_t)t1 < 4 ? 256 / (uint32_t)t1 : 4;  // >= 2
+      else if (t1 <= 170) ks = 3;
+    }
+    if (ks > 1) {
+      // partial sums: one 32-register block per (slice, tile, thread); the
+      // counters' region is the same for every launch (a split grid has at
+      // most 170 tiles), so partial sums never land on a counter
       const size_t ctr_bytes = 256 * 4;
-      uint8_t *w = (uint8_t *)nlg_scratch_try(ctr_bytes + (size_t)ks * ntile * 256 * 32 * 4, st, 1);
+      uint8_t *w = (uint8_t *)nlg_scratch_try(ctr_bytes + (size_t)ks * t1 * 256 * 32 * 4, st, 1);
       if (w) {
         a.kctr = (uint32_t *)w;
         a.ksum = (int32_t *)(w + ctr_bytes);
@@ -1449,32 +1287,13 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
         ks = 1;
       }
     }
-    if (ks > 1) {
-      const dim3 grid(nlg_blocks(a.out, 64), ty, ks);
-      if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
-      const size_t lds = (size_t)2 * 128 * TL_PITCH;
-#define TLG(E)                                                                                   \
-  do {                                                                                           \
-    if (wt) hipLaunchKernelGGL((k_tgemm_l<1, 2, E, true, true>), grid, dim3(256), lds, st, a);  \
-    else hipLaunchKernelGGL((k_tgemm_l<1, 2, E, true, false>), grid, dim3(256), lds, st, a);    \
-  } while (0)
-      switch (epi) {
-        case NLG_EPI_STORE: TLG(NLG_EPI_STORE); break;
-        case NLG_EPI_RESID: TLG(NLG_EPI_RESID); break;
-        case NLG_EPI_SWIGLU: TLG(NLG_EPI_SWIGLU); break;
-        case NLG_EPI_QKV: TLG(NLG_EPI_QKV); break;
-        default: return nlg_fail("ternary GEMM: unknown epilogue %d", epi);
-      }
-#undef TLG
-      NLG_LAUNCHED("ternary GEMM (int8 MFMA, column split)");
-      return NLG_OK;
-    }
-    const bool t64 = t2 >= 400;
-    const dim3 gw(rt, t64 ? (a.seq + 63) / 64 : (a.seq + 31) / 32);
+    const bool t64 = ks == 1 && t2 >= 400;
+    const dim3 gw(rt, t64 ? (a.seq + 63) / 64 : (uint32_t)n32, ks);
     if (gw.y > 65535) return nlg_fail("ternary GEMM: seq too large");
 #define TWT(E, T)                                                                                \
   do {                                                                                           \
-    if (t64) hipLaunchKernelGGL((k_tgemm_w<E, T, 2>), gw, dim3(256), 0, st, a);                 \
+    if (ks > 1) hipLaunchKernelGGL((k_tgemm_w<E, T, 1, true>), gw, dim3(256), 0, st, a);         \
+    else if (t64) hipLaunchKernelGGL((k_tgemm_w<E, T, 2>), gw, dim3(256), 0, st, a);            \
     else hipLaunchKernelGGL((k_tgemm_w<E, T, 1>), gw, dim3(256), 0, st, a);                     \
   } while (0)
 #define TWG(E)                                                                                   \
@@ -1491,7 +1310,7 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
     }
 #undef TWG
 #undef TWT
-    NLG_LAUNCHED("ternary GEMM (int8 MFMA, wide waves)");
+    NLG_LAUNCHED(ks > 1 ? "ternary GEMM (int8 MFMA, wide waves, column split)" : "ternary GEMM (int8 MFMA, wide waves)");
     return NLG_OK;
   }
   // up to 32 tokens per workgroup: the 32 x 2064-byte activation block
