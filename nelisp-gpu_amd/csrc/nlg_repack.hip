@@ -202,7 +202,7 @@ extern "C" int nlg_repack_packed_to_2bit(const float *wpk, uint32_t out, uint32_
 
 // ------------------------------------------------------------ tiled copies
 //
-// The prefill GEMM (k_tgemm_l) hands lane 32g + i of a wave the words
+// The prefill GEMM (k_tgemm_w) hands lane 32g + i of a wave the words
 // 8g..8g+7 of row i's 256-column chunk: 32 bytes of each of 32 rows, so a
 // load instruction over the row layout touches 32 cache lines and uses a
 // quarter of each.  The tiled copy stores each (32-row block, chunk) as one
