@@ -472,27 +472,49 @@ __global__ __launch_bounds__(512, 4) void k_attn_mfma(AttnArgs a) {
   // Rows past lim - 1 clamp to it.  Large caches (NT) read the position
   // first so that rows past it are never fetched; small ones fetch the whole
   // chunk while the position is in flight.
-  uint32_t lim = a.max_seq;
+  uint32_t lim = a.max_seq, len = rlen;
   if (NT && !RG) {
     const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(qr % a.qper) : 0);
     lim = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
+    len = lim;  // positions attended: 0 .. pr
   }
-  // K, A operand layout: lane (lg, li) position pw + 16 bb + li, dims 32 s + 8 lg
-  // (each row's four 64-byte runs come from four consecutive instructions).
-  // Large caches stream K and V non-temporally, as k_attn_part does: with
-  // plain loads the K rows evict what the step's linears re-read (measured
-  // at B = 32: the pass alone 14.05 -> 14.25 us, the decode step 1.773 ->
-  // 1.713 ms).
+  // K rows of the wave's 32 positions go straight into its tile (direct
+  // global-to-LDS loads, whole rows per instruction: instruction k, lane
+  // j = 16 rr + uu brings row 4 k + rr's 16-byte unit uu ^ (row % 16) to
+  // tile unit uu of that row, so the A-operand reads below -- row 16 bb +
+  // li, unit 4 s + lg -- hit 16 distinct units), read back in the matrix
+  // cores' layout: lane (lg, li) position pw + 16 bb + li, dims 32 s + 8 lg.
+  // (Fetched in that layout directly, each load instruction took a 64-byte
+  // piece of 16 rows: 13.78 -> 13.25 us for the B = 32 pass.)  Large caches
+  // stream K and V non-temporally, as k_attn_part does: with plain loads
+  // the K rows evict what the step's linears re-read (measured at B = 32:
+  // the pass alone 14.05 -> 14.25 us, the decode step 1.773 -> 1.713 ms).
+  // (Ring caches keep K in registers, fetched in the A-operand layout
+  // directly beside each row's rotation pairs: staged, that variant spills.)
+  constexpr bool KLDS = !RG;
+  uint8_t *const ktile = (uint8_t *)s_vt[w];
   uint4 kr[2][4];
   float4 rc[2][4], rs[2][4];  // ring: the rank's rotation pairs of the lane's 8 dims
+  if (KLDS) {
 #pragma unroll
-  for (int bb = 0; bb < 2; bb++) {
-    const uint32_t pp = pw + 16 * bb + li, pc = pp < lim ? pp : lim - 1;
-    const size_t ro = (size_t)slot_of(pc) * HD;
+    for (int k = 0; k < 8; k++) {
+      const uint32_t row = 4 * k + (lane >> 4), uu = lane & 15;
+      const uint32_t pp = pw + row, pc = pp < lim ? pp : lim - 1;
+      __builtin_amdgcn_global_load_lds((const void *)(kb + (size_t)pc * HD + 8 * (uu ^ (row % 16))),
+                                       (__attribute__((address_space(3))) void *)(ktile + 1024 * k), 16, 0,
+                                       NT ? 2 : 0);  // aux 2: non-temporal
+    }
+    // every later load counts after these in vmcnt
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  } else {
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-      kr[bb][s] = kv_ld<NT>(kb + ro + 32 * s + 8 * lg);
-      if (RG) {
+    for (int bb = 0; bb < 2; bb++) {
+      const uint32_t pp = pw + 16 * bb + li, pc = pp < lim ? pp : lim - 1;
+      const size_t ro = (size_t)slot_of(pc) * HD;
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        kr[bb][s] = kv_ld<NT>(kb + ro + 32 * s + 8 * lg);
         rc[bb][s] = *(const float4 *)(a.co + (size_t)pc * (HD / 2) + 16 * s + 4 * lg);
         rs[bb][s] = *(const float4 *)(a.si + (size_t)pc * (HD / 2) + 16 * s + 4 * lg);
       }
@@ -516,12 +538,13 @@ __global__ __launch_bounds__(512, 4) void k_attn_mfma(AttnArgs a) {
       qs[s] = *(const float4 *)(a.si + (size_t)qrank * (HD / 2) + 16 * s + 4 * lg);
     }
   }
-  uint32_t len = rlen;
-  if (!RG) {
+  if (!RG && !NT) {
     const int32_t pr = a.pos[0] + (a.qper ? (int32_t)(qr % a.qper) : 0);
     len = (pr < 0 ? 0u : ((uint32_t)pr >= a.max_seq ? a.max_seq - 1 : (uint32_t)pr)) + 1;
   }
   if (p0 >= len) {  // block-uniform: a chunk past the position adds nothing
+    // (the tile's direct loads land before the workgroup's LDS is released)
+    if (KLDS) __builtin_amdgcn_s_waitcnt(0);
     for (int i = threadIdx.x; i < G * HD; i += NW * 64) pctx[i] = 0.0f;
     if (threadIdx.x < G) {
       pmz[2 * threadIdx.x] = -1.0e30f;
@@ -549,6 +572,19 @@ __global__ __launch_bounds__(512, 4) void k_attn_mfma(AttnArgs a) {
       qh[s][e] = h;
       ql[s][e] = (_Float16)(x[e] - (float)h);
     }
+  }
+  if (KLDS) {
+    // the tile's K loads have landed once at most the 8 V loads issued after
+    // them are out: then read the A operands
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt((8 & 0xF) | (0x7 << 4) | ((8 >> 4) << 14));
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int bb = 0; bb < 2; bb++)
+#pragma unroll
+      for (int s = 0; s < 4; s++)
+        kr[bb][s] = *(const uint4 *)(ktile + (16 * bb + li) * 256 + 16 * ((4 * s + lg) ^ li));
   }
   // scores: lane (lg, li < 4) gets head li at positions pw + 16 bb + 4 lg + r
   v4f sc[2];
