@@ -204,6 +204,29 @@ struct GemmArgs {
 
 // One output element of the batched linear (every lane calls it: the SwiGLU
 // and RoPE pairs are exchanged across lanes l, l^1, which hold rows 2j, 2j+1).
+// Best (value, index) over the 16 lanes of each DPP row -- the larger value,
+// the lower index among equals; index -1: no candidate -- in every lane of
+// the row.  That order is total, so any pairing finds the same winner: the
+// quad swaps, then the half-row and row mirrors (each pairs every lane with
+// one of the other quad, then of the other half).  DPP moves, not LDS
+// permutes: each step is a few VALU cycles instead of an LDS round trip.
+__device__ __forceinline__ void row16_argmax(float &bv, int32_t &bi) {
+#define R16_STEP(C)                                                                          \
+  {                                                                                          \
+    const float ov = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(bv), C, 0xf, 0xf, true)); \
+    const int32_t oi = __builtin_amdgcn_mov_dpp(bi, C, 0xf, 0xf, true);                     \
+    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {                          \
+      bv = ov;                                                                               \
+      bi = oi;                                                                               \
+    }                                                                                        \
+  }
+  R16_STEP(0xB1)   // quad_perm [1,0,3,2]
+  R16_STEP(0x4E)   // quad_perm [2,3,0,1]
+  R16_STEP(0x141)  // row_half_mirror
+  R16_STEP(0x140)  // row_mirror
+#undef R16_STEP
+}
+
 // the epilogue operands of one (token, row), fetched before the main loop
 struct TgPre {
   float res, cs, sn;
@@ -404,12 +427,7 @@ __global__ __launch_bounds__(256) void k_tgemm(GemmArgs a) {
         // first maximum over the wave's 16 rows for this token
         float bv = live && val == val ? val : -INFINITY;
         int32_t bi = live && val == val ? (int32_t)row : -1;
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) {
-          const float ov = __shfl_xor(bv, off);
-          const int32_t oi = __shfl_xor(bi, off);
-          if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
-        }
+        row16_argmax(bv, bi);
         if (lr == 0) {
           s_bv[w][16 * m + 4 * lg + r] = bv;
           s_bi[w][16 * m + 4 * lg + r] = bi;
@@ -592,11 +610,7 @@ __global__ __launch_bounds__(512) void k_tgemm_r(GemmArgs a) {
           /* first maximum over the wave's 16 rows for this token */                                 \
           float bv = live && val == val ? val : -INFINITY;                                           \
           int32_t bi = live && val == val ? (int32_t)row : -1;                                       \
-          _Pragma("unroll") for (int off = 1; off < 16; off <<= 1) {                                 \
-            const float ov = __shfl_xor(bv, off);                                                    \
-            const int32_t oi = __shfl_xor(bi, off);                                                  \
-            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }       \
-          }                                                                                          \
+          row16_argmax(bv, bi);                                                                      \
           if (lr == 0) {                                                                             \
             s_bv[buf][w][16 * m + 4 * lg + r] = bv;                                                  \
             s_bi[buf][w][16 * m + 4 * lg + r] = bi;                                                  \
