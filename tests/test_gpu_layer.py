@@ -161,7 +161,7 @@ def test_qkv_rope_and_fp16_append(B, heads, kvh, hd, cols, max_seq, pos):
                                                 (16, 9000, 2560, False), (32, 9000, 2560, True),
                                                 (2, 40000, 1024, True), (1, 33000, 6144, True),
                                                 (3, 32800, 9216, False),
-                                                # 1,024+ 64-row tiles: the resident-activation GEMM
+                                                # 1,024+ 64-row tiles: the wide-wave GEMM in 32-token tiles
                                                 (20, 66000, 2560, True), (5, 70000, 512, True),
                                                 (40, 33000, 768, False)])
 def test_lm_head_argmax(seq, vocab, cols, dup):
