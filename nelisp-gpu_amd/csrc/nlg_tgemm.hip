@@ -46,6 +46,7 @@ struct ActQArgs {
   uint8_t *xq;          // [seq x cols] int8 in MFMA order
   float *gamma;         // [seq]
   uint32_t seq, cols;
+  uint32_t stream_x;    // non-temporal loads of x (large row blocks)
 };
 
 // 256 threads per token row; thread t holds the row's float4s t + 256 j
@@ -98,11 +99,24 @@ __global__ __launch_bounds__(256) void k_act_q(ActQArgs a) {
       v[j] = make_float4(acc.x / zz, acc.y / zz, acc.z / zz, acc.w / zz);
     }
   } else {
+    // A large row block is read once and streams from HBM: non-temporal
+    // loads (16,384 x 6,912: 105 -> 91 us, the GEMM after it unchanged).  A
+    // small one was just written by the previous launch and sits in the
+    // caches, where non-temporal loads were slower (batch-32 decode: the
+    // down projection's pair 9.93 -> 10.46 us).
     const float4 *x4 = (const float4 *)(a.x + (size_t)tok * a.cols);
+    if (a.stream_x) {
 #pragma unroll
-    for (int j = 0; j < J; j++) {
-      const uint32_t f0 = threadIdx.x + 256u * j;
-      v[j] = x4[f0 < nf4 ? f0 : nf4 - 1];
+      for (int j = 0; j < J; j++) {
+        const uint32_t f0 = threadIdx.x + 256u * j;
+        v[j] = nlg_ld_stream_f4(&x4[f0 < nf4 ? f0 : nf4 - 1]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < J; j++) {
+        const uint32_t f0 = threadIdx.x + 256u * j;
+        v[j] = x4[f0 < nf4 ? f0 : nf4 - 1];
+      }
     }
   }
   float4 gv[J];
@@ -1055,7 +1069,7 @@ int nlg_act_q_launch(const float *x, const float *gain, float eps, const float *
                      hipStream_t st) {
   if (!seq) return NLG_OK;
   if (cols % 64 || !cols || cols > 16384) return nlg_fail("act quant: cols must be a multiple of 64 in [64, 16384]");
-  ActQArgs a{x, gain, eps, attn_mz, attn_nc, hd, xq, gamma, seq, cols};
+  ActQArgs a{x, gain, eps, attn_mz, attn_nc, hd, xq, gamma, seq, cols, seq >= 2048u};
   const dim3 grid(seq), blk(256);
 #define AQ(P)                                                                                      \
   do {                                                                                             \
