@@ -1189,8 +1189,15 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   if (epi != NLG_EPI_ARGMAX && (uint64_t)nlg_blocks(a.out, 64) * ((a.seq + MT - 1) / MT) < 128) {
     // too few 64-row workgroups to fill half the CUs: 16-row ones with the
     // columns split over the waves (measured at 32 tokens: 2560..3840 rows
-    // gain, 13,824 rows lose to the extra activation reads)
-    const dim3 grid(nlg_blocks(a.out, 16), (a.seq + MT - 1) / MT), blk(256);
+    // gain, 13,824 rows lose to the extra activation reads), of 16 tokens up
+    // to 32 (each workgroup reads its token block of every chunk, 8x its
+    // weight bytes at 16 rows; twice the workgroups with half the block:
+    // B=32 decode QKV 8.44 -> 7.55 us, O with its merge 8.11 -> 7.66, down
+    // 9.88 -> 9.99, 19.9k -> 20.1k tok/s; k_tgemm's 64-row gate|up lost
+    // 1.0 us to the same change and keeps 32-token workgroups)
+    const int MBK = a.seq <= 32 ? 1 : 2;
+    const uint32_t MTK = 16u * MBK;
+    const dim3 grid(nlg_blocks(a.out, 16), (a.seq + MTK - 1) / MTK), blk(256);
     if (grid.y > 65535) return nlg_fail("ternary GEMM: seq too large");
     // weight chunks per wave: the smallest instantiated count >= ceil(chunks / 4)
     const uint32_t per = (a.cols / TG_KC + 3) / 4;
@@ -1210,7 +1217,7 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   } while (0)
 #define TKG(E)                                                                            \
   do {                                                                                    \
-    if (MB == 1) TKP(1, E);                                                               \
+    if (MBK == 1) TKP(1, E);                                                              \
     else TKP(2, E);                                                                       \
   } while (0)
     switch (epi) {
