@@ -1096,7 +1096,15 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   // replaces the row layout: the same words, in load order
   const uint32_t *wt = nlg_tiled_find(a.w2, a.out, a.cols);
   if (wt) a.w2 = wt;
-  if (a.seq >= 128 && epi != NLG_EPI_ARGMAX) {
+  // Rows of 9..10 chunks over 128..256 64-row x 32-token tiles take
+  // k_tgemm's single 10-chunk phase below at any token count: at 128..192
+  // tokens (QKV 3,840 rows at 128, O 2,560 rows up to 192) it beat the
+  // wide-wave kernel's 32-token tiles 6.2..6.4 against 10.2..10.4 us, while
+  // its two-phase forms (more tiles) lost or tied.
+  const uint32_t nch_all = a.cols / TG_KC;
+  const uint64_t t64x32 = (uint64_t)nlg_blocks(a.out, 64) * ((a.seq + 31) / 32);
+  const bool one_phase = nch_all > TG_PH && nch_all <= 10 && t64x32 >= 128 && t64x32 <= 256;
+  if (a.seq >= 128 && epi != NLG_EPI_ARGMAX && !one_phase) {
     // 256-row tiles of the wide-wave kernel (k_tgemm_w), 64-token tiles
     // once there are 400 of them, else 32-token ones; a few tiles of long
     // rows split their columns over gridDim.z slices.  From sweeps of the

@@ -15,7 +15,9 @@ Each shape is chosen so the GEMM runs a given form: the wide-wave kernel
 (k_tgemm_w: 256-row tiles, 4 waves of 64 rows x 64 tokens -- "w64" -- or x 32
 tokens -- "w32"; activations staged by direct global-to-LDS loads), whose
 cases cover every remainder of its six-chunk loop (1 to 10 chunks of 256
-columns, 27) and ragged rows and tokens for both tile heights, or its
+columns, 27) and ragged rows and tokens for both tile heights, the
+small-batch kernel's single 10-chunk phase where it wins at 128+ tokens
+("sb10"), or the wide-wave kernel's
 32-token tiles with the columns split over 2, 3 or 4 slices for few tiles of
 rows of 16+ chunks ("split": slices of 4..14 chunks, ragged rows and
 tokens).  Every case runs twice: with the weights' row layout, then with a
@@ -74,19 +76,22 @@ def with_tiled_copy(dw, rows, cols, run):
 
 def row_tile(seq, out, cols):
     """The batched GEMM's form for seq >= 128 tokens, either weight layout
-    (nlg_tgemm.hip's choice): "split" -- 32-token tiles with the columns
-    split over gridDim.z slices, for at most 170 tiles of rows of 16+ chunks
-    -- else 256-row tiles of 64 tokens ("w64", once there are 400 of them)
-    or 32 ("w32")."""
+    (nlg_tgemm.hip's choice): "sb10" -- the small-batch kernel's single
+    10-chunk phase, for rows of 9..10 chunks over 128..256 64-row x 32-token
+    tiles; "split" -- 32-token tiles with the columns split over gridDim.z
+    slices, for at most 170 tiles of rows of 16+ chunks -- else 256-row
+    tiles of 64 tokens ("w64", once there are 400 of them) or 32 ("w32")."""
     rt = (out + 255) // 256
     t1, t2 = rt * ((seq + 31) // 32), rt * ((seq + 63) // 64)
+    if 8 < cols // 256 <= 10 and 128 <= (out + 63) // 64 * ((seq + 31) // 32) <= 256:
+        return "sb10"
     if cols // 256 >= 16 and t1 <= 170:
         return "split"
     return "w64" if t2 >= 400 else "w32"
 
 
 SWIGLU = [(128, 6912, 2560, True, "w32"), (512, 6912, 2560, True, "w64"), (600, 6912, 2560, True, "w64"),
-          (512, 640, 4096, False, "split"), (400, 4096, 1024, True, "w32"), (512, 3072, 1024, True, "w32"),
+          (512, 640, 4096, False, "split"), (400, 4096, 1024, True, "w32"), (128, 1280, 2560, True, "sb10"), (512, 3072, 1024, True, "w32"),
           (300, 3840, 2560, False, "w32"),
           (1200, 6144, 1024, True, "w64"),   # 4 chunks
           (1100, 4096, 1536, False, "w64")]  # 6 chunks: one whole group
@@ -119,6 +124,7 @@ def test_batched_swiglu(seq, dff, cols, rms, tile):
 
 RESID = [(128, 2560, 6912, "split"), (512, 2560, 6912, "split"), (384, 2560, 6912, "split"),  # 4, 3, 2 slices
          (200, 1000, 4352, "split"),                          # 4 slices of 4..5 chunks, ragged rows and tokens
+         (160, 2560, 2560, "sb10"), (150, 2500, 2304, "sb10"),  # one 10- / 9-chunk phase, ragged
          (1024, 2560, 6912, "w32"), (512, 8192, 2560, "w32"), (600, 13824, 2560, "w64"),
          (200, 1000, 512, "w32"), (512, 6144, 2560, "w32"), (512, 2560, 2560, "w32"),
          (128, 2048, 256, "w32"), (256, 2048, 1536, "w32"), (300, 13800, 768, "w32"),  # 1, 6, 3 chunks
@@ -172,7 +178,7 @@ QKV = [(512, 512, 20, 5, 128, 2560, 768, 0, "w32"),     # config 5's prompt at B
        (512, 256, 32, 8, 128, 2560, 320, 40, "w32"),    # two prompts
        (512, 128, 64, 32, 128, 2560, 160, 20, "w64"),   # four prompts
        (128, 64, 8, 2, 64, 1024, 100, 50, "w32"),       # positions run past max_seq: no cache store there
-       (128, 0, 20, 5, 128, 2560, 16, 5, "w32"),        # 128 decode rows at one position
+       (128, 0, 20, 5, 128, 2560, 16, 5, "sb10"),       # 128 decode rows at one position
        (128, 0, 8, 2, 128, 4096, 16, 5, "split"),       # the same, rows of 16 chunks
        (256, 128, 8, 2, 128, 4352, 160, 20, "split"),   # two prompts, rows of 17 chunks
        (2304, 256, 20, 5, 128, 2560, 320, 10, "w64"),   # nine prompts (10 chunks)
