@@ -25,10 +25,10 @@
 // C[4(l/16) + r][l % 16].  Here i = token, j = output row, and lane group g
 // at step t of a chunk covers 2-bit word 4g + t of the chunk.
 //
-// 128 tokens and more: k_tgemm_w (32 x 32 x 32 MFMAs; 256-row workgroups
-// whose waves own 64 rows x 64 or 32 tokens, fed by direct global-to-LDS
-// activation loads), for a few tiles of long rows with their columns split
-// over gridDim.z slices.
+// 128 tokens and more (and 65+ tokens of many rows): k_tgemm_w (32 x 32 x
+// 32 MFMAs; 256-row workgroups whose waves own 64 rows x 64 or 32 tokens,
+// fed by direct global-to-LDS activation loads), for a few tiles of long
+// rows with their columns split over gridDim.z slices.
 #include <math.h>
 
 #include "nlg_quant.h"
@@ -1104,7 +1104,14 @@ int nlg_tgemm_launch(const GemmArgs &a0, int epi, hipStream_t st) {
   const uint32_t nch_all = a.cols / TG_KC;
   const uint64_t t64x32 = (uint64_t)nlg_blocks(a.out, 64) * ((a.seq + 31) / 32);
   const bool one_phase = nch_all > TG_PH && nch_all <= 10 && t64x32 >= 128 && t64x32 <= 256;
-  if (a.seq >= 128 && epi != NLG_EPI_ARGMAX && !one_phase) {
+  // From 65 tokens, more than 512 such tiles (k_tgemm holds two 64-row
+  // workgroups per CU, so a second round) go to the wide-wave kernel too:
+  // gate|up (13,824 x 2560) at 72 / 96 / 112 / 127 tokens 12.8 / 12.4 /
+  // 12.5 / 13.9 against 15.8 / 16.2 / 19.6 / 19.9 us, 13,824 x 1280 at 72
+  // 8.7 against 9.6; at 432 tiles k_tgemm kept the lead (gate|up at 64
+  // tokens 10.9 against 11.7, 6,912 x 2560 at 112 10.6 against 12.0).
+  const bool wide = a.seq >= 128 || (a.seq > 64 && t64x32 > 512);
+  if (wide && epi != NLG_EPI_ARGMAX && !one_phase) {
     // 256-row tiles of the wide-wave kernel (k_tgemm_w), 64-token tiles
     // once there are 400 of them, else 32-token ones; a few tiles of long
     // rows split their columns over gridDim.z slices.  From sweeps of the

@@ -75,15 +75,20 @@ def with_tiled_copy(dw, rows, cols, run):
 
 
 def row_tile(seq, out, cols):
-    """The batched GEMM's form for seq >= 128 tokens, either weight layout
-    (nlg_tgemm.hip's choice): "sb10" -- the small-batch kernel's single
-    10-chunk phase, for rows of 9..10 chunks over 128..256 64-row x 32-token
-    tiles; "split" -- 32-token tiles with the columns split over gridDim.z
-    slices, for at most 170 tiles of rows of 16+ chunks -- else 256-row
-    tiles of 64 tokens ("w64", once there are 400 of them) or 32 ("w32")."""
+    """The batched GEMM's form for seq >= 128 tokens, or 65+ tokens over more
+    than 512 64-row x 32-token tiles, either weight layout (nlg_tgemm.hip's
+    choice): "small" -- the small-batch kernels, below 65 tokens or 513
+    tiles; "sb10" -- the small-batch kernel's single 10-chunk phase, for
+    rows of 9..10 chunks over 128..256 such tiles; "split" -- 32-token tiles
+    with the columns split over gridDim.z slices, for at most 170 256-row
+    tiles of rows of 16+ chunks -- else 256-row tiles of 64 tokens ("w64",
+    once there are 400 of them) or 32 ("w32")."""
     rt = (out + 255) // 256
     t1, t2 = rt * ((seq + 31) // 32), rt * ((seq + 63) // 64)
-    if 8 < cols // 256 <= 10 and 128 <= (out + 63) // 64 * ((seq + 31) // 32) <= 256:
+    t64x32 = (out + 63) // 64 * ((seq + 31) // 32)
+    if seq < 128 and (seq <= 64 or t64x32 <= 512):
+        return "small"
+    if 8 < cols // 256 <= 10 and 128 <= t64x32 <= 256:
         return "sb10"
     if cols // 256 >= 16 and t1 <= 170:
         return "split"
@@ -94,7 +99,8 @@ SWIGLU = [(128, 6912, 2560, True, "w32"), (512, 6912, 2560, True, "w64"), (600, 
           (512, 640, 4096, False, "split"), (400, 4096, 1024, True, "w32"), (128, 1280, 2560, True, "sb10"), (512, 3072, 1024, True, "w32"),
           (300, 3840, 2560, False, "w32"),
           (1200, 6144, 1024, True, "w64"),   # 4 chunks
-          (1100, 4096, 1536, False, "w64")]  # 6 chunks: one whole group
+          (1100, 4096, 1536, False, "w64"),  # 6 chunks: one whole group
+          (96, 6912, 2560, True, "w32"), (72, 6912, 1280, False, "w32")]  # 65+ tokens, 648 64-row tiles
 
 
 @pytest.mark.parametrize("seq,dff,cols,rms,tile", SWIGLU)
@@ -124,6 +130,7 @@ def test_batched_swiglu(seq, dff, cols, rms, tile):
 
 RESID = [(128, 2560, 6912, "split"), (512, 2560, 6912, "split"), (384, 2560, 6912, "split"),  # 4, 3, 2 slices
          (200, 1000, 4352, "split"),                          # 4 slices of 4..5 chunks, ragged rows and tokens
+         (100, 9000, 6912, "split"),                          # 100 tokens over 564 64-row tiles: 3 slices, ragged
          (160, 2560, 2560, "sb10"), (150, 2500, 2304, "sb10"),  # one 10- / 9-chunk phase, ragged
          (1024, 2560, 6912, "w32"), (512, 8192, 2560, "w32"), (600, 13824, 2560, "w64"),
          (200, 1000, 512, "w32"), (512, 6144, 2560, "w32"), (512, 2560, 2560, "w32"),
@@ -181,6 +188,7 @@ QKV = [(512, 512, 20, 5, 128, 2560, 768, 0, "w32"),     # config 5's prompt at B
        (128, 0, 20, 5, 128, 2560, 16, 5, "sb10"),       # 128 decode rows at one position
        (128, 0, 8, 2, 128, 4096, 16, 5, "split"),       # the same, rows of 16 chunks
        (256, 128, 8, 2, 128, 4352, 160, 20, "split"),   # two prompts, rows of 17 chunks
+       (100, 0, 64, 16, 128, 2560, 16, 5, "w32"),       # 100 decode rows over 768 64-row tiles
        (2304, 256, 20, 5, 128, 2560, 320, 10, "w64"),   # nine prompts (10 chunks)
        (2304, 0, 20, 5, 128, 512, 8, 3, "w64")]         # 2304 decode rows (2 chunks)
 
@@ -340,14 +348,16 @@ def test_tiled_copy_dropped_with_its_memory():
     print(f"  same address handed back in {reused} of 4 attempts", flush=True)
 
 
-# 4..127 tokens: the 16x16x64 GEMM with 64-row workgroups (many rows) or the
-# 16-row column-split form (few rows), each on the row layout and on a tiled copy
+# 4..127 tokens (at 65+, up to 512 64-row x 32-token tiles): the 16x16x64 GEMM
+# with 64-row workgroups (many rows) or the 16-row column-split form (few rows),
+# each on the row layout and on a tiled copy
 SMALL = [(8, 13824, 2560), (32, 13824, 2560), (100, 6912, 1024), (32, 2560, 6912), (16, 3840, 2560),
          (32, 2560, 2560), (77, 1000, 512)]
 
 
 @pytest.mark.parametrize("seq,out,cols", SMALL)
 def test_small_batch_tiled_copy(seq, out, cols):
+    assert row_tile(seq, out, cols) == "small"
     print(f"[gpu] small batch seq={seq} out={out} cols={cols}", flush=True)
     x, res = nlgpu.normal(cols + seq + 1, seq * cols), nlgpu.normal(out + seq + 1, seq * out)
     w2, beta = weights(cols + out + 1, out, cols, per_row=True)
