@@ -53,6 +53,17 @@ struct PrefillArgs {
 
 __device__ __forceinline__ v8h f16x8(uint4 u) { return __builtin_bit_cast(v8h, u); }
 
+// The lo halves of two probabilities, x - hi rounded to f16 (hi = x rounded
+// to f16, the halves of h2), packed: one mixed-precision FMA each, x * 1 - hi
+// in f32 (exact: hi is x's nearest f16) rounded once -- the value the
+// convert / subtract / convert chain gives, in a third of the instructions.
+__device__ __forceinline__ uint32_t pa_lo2(float x0, float x1, uint32_t h2) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "=v"(r) : "v"(x0), "v"(h2));
+  asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "+v"(r) : "v"(x1), "v"(h2));
+  return r;
+}
+
 template <int HD, int GRP, bool SPLIT>
 __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_attn(PrefillArgs a) {
   constexpr int NT = 64 * GRP;
@@ -84,8 +95,14 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
   if (SPLIT && kbf >= nkb && piece) return;  // past the causal range (piece 0 always reports)
   const size_t cache0 = (size_t)(sq * a.kvheads + kvh) * a.max_seq * HD;
   const uint16_t *kb0 = a.kc + cache0, *vb0 = a.vc + cache0;
-  const uint32_t klast = a.max_seq - 1;
 
+  // Block kb's rows through a buffer resource starting at its first row
+  // (scalar arithmetic only): each thread's offset in a block is fixed, and
+  // rows past the cache read 0 -- never attended: their scores are masked
+  // and their V rows zeroed below.
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+#define PA_RES(base, kb) nlg_buffer_rsrc((base) + (size_t)(kb) * PA_KB * HD, (a.max_seq - (kb) * PA_KB) * HD * 2u)
   // K block: piece t = key t / (HD/8), 8 halves at (t % (HD/8)) * 8.
   // V block: tile t = 4 keys 4 (t / (HD/4)) .. +3 x 4 dims 4 (t % (HD/4)) .. +3.
   // staging registers as vectors (arrays assigned under a branch go to scratch)
@@ -95,20 +112,21 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
   vvec vr;
 #define PA_LOAD(kb)                                                                       \
   do {                                                                                    \
+    const __amdgpu_buffer_rsrc_t kres = PA_RES(kb0, kb), vres = PA_RES(vb0, kb);          \
     _Pragma("unroll") for (int u = 0; u < KI; u++) {                                      \
       const uint32_t t = threadIdx.x + NT * u;                                            \
-      const uint32_t key = min((kb) * PA_KB + t / (HD / 8), klast);                        \
       if ((PA_KB * HD / 8) % NT == 0 || t < PA_KB * HD / 8) {                             \
-        const uint4 x = *(const uint4 *)(kb0 + (size_t)key * HD + 8 * (t % (HD / 8)));     \
+        const v4u x = __builtin_amdgcn_raw_buffer_load_b128(                              \
+            kres, (int)(2 * ((t / (HD / 8)) * HD + 8 * (t % (HD / 8)))), 0, 0);             \
         kr[4 * u] = x.x; kr[4 * u + 1] = x.y; kr[4 * u + 2] = x.z; kr[4 * u + 3] = x.w;     \
       }                                                                                   \
     }                                                                                     \
     _Pragma("unroll") for (int u = 0; u < VI; u++) {                                      \
       const uint32_t t = threadIdx.x + NT * u;                                            \
       _Pragma("unroll") for (int e = 0; e < 4; e++) {                                     \
-        const uint32_t key = min((kb) * PA_KB + 4 * (t / (HD / 4)) + e, klast);            \
         if ((PA_KB / 4 * HD / 4) % NT == 0 || t < PA_KB / 4 * HD / 4) {                   \
-          const uint2 x = *(const uint2 *)(vb0 + (size_t)key * HD + 4 * (t % (HD / 4)));   \
+          const v2u x = __builtin_amdgcn_raw_buffer_load_b64(                             \
+              vres, (int)(2 * ((4 * (t / (HD / 4)) + e) * HD + 4 * (t % (HD / 4)))), 0, 0); \
           vr[8 * u + 2 * e] = x.x; vr[8 * u + 2 * e + 1] = x.y;                           \
         }                                                                                 \
       }                                                                                   \
@@ -131,14 +149,24 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
         const int32_t kk = (int32_t)((kb) * PA_KB + k4);                                   \
         const uint32_t m0 = kk <= plast ? 0xffffu : 0u, m1 = kk + 1 <= plast ? 0xffffu : 0u; \
         const uint32_t m2 = kk + 2 <= plast ? 0xffffu : 0u, m3 = kk + 3 <= plast ? 0xffffu : 0u; \
-        /* dims d4 + c: the 4 keys' halves c, low key first */                            \
-        _Pragma("unroll") for (int c = 0; c < 4; c++) {                                   \
-          const int sh = 16 * (c & 1);                                                    \
-          const uint32_t h0 = (vr[8 * u + 0 + c / 2] >> sh) & m0;                         \
-          const uint32_t h1 = (vr[8 * u + 2 + c / 2] >> sh) & m1;                         \
-          const uint32_t h2 = (vr[8 * u + 4 + c / 2] >> sh) & m2;                         \
-          const uint32_t h3 = (vr[8 * u + 6 + c / 2] >> sh) & m3;                         \
-          *(uint2 *)(&s_v[buf][(d4 + c) * VP + k4]) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16)); \
+        /* dims d4 + c: the 4 keys' halves c, low key first (a block wholly */          \
+        /* inside the prompt pairs them with byte permutes, nothing to zero) */           \
+        if ((int32_t)((kb) * PA_KB + PA_KB - 1) <= plast) {                               \
+          _Pragma("unroll") for (int c = 0; c < 4; c++) {                                 \
+            const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;                     \
+            *(uint2 *)(&s_v[buf][(d4 + c) * VP + k4]) =                                   \
+                make_uint2(__builtin_amdgcn_perm(vr[8 * u + 2 + c / 2], vr[8 * u + 0 + c / 2], sel), \
+                           __builtin_amdgcn_perm(vr[8 * u + 6 + c / 2], vr[8 * u + 4 + c / 2], sel)); \
+          }                                                                               \
+        } else {                                                                          \
+          _Pragma("unroll") for (int c = 0; c < 4; c++) {                                 \
+            const int sh = 16 * (c & 1);                                                  \
+            const uint32_t h0 = (vr[8 * u + 0 + c / 2] >> sh) & m0;                       \
+            const uint32_t h1 = (vr[8 * u + 2 + c / 2] >> sh) & m1;                       \
+            const uint32_t h2 = (vr[8 * u + 4 + c / 2] >> sh) & m2;                       \
+            const uint32_t h3 = (vr[8 * u + 6 + c / 2] >> sh) & m3;                       \
+            *(uint2 *)(&s_v[buf][(d4 + c) * VP + k4]) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16)); \
+          }                                                                               \
         }                                                                                 \
       }                                                                                   \
     }                                                                                     \
@@ -180,12 +208,22 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
       sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qh[s], sc, 0, 0, 0);
       sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ql[s], sc, 0, 0, 0);
     }
+    // (q.k / sqrt(hd)) * log2(e); keys past the lane's query masked, which
+    // only the blocks that reach past the block's first query need
     float mb = -INFINITY;
+    if ((int32_t)(kb * PA_KB + PA_KB - 1) <= pos0 + (int32_t)(qb * PA_QB)) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int32_t key = (int32_t)(kb * PA_KB + 8 * (r / 4) + 4 * lg + r % 4);
-      sc[r] = key <= pj ? sc[r] * a.coef : -INFINITY;  // (q.k / sqrt(hd)) * log2(e)
-      mb = fmaxf(mb, sc[r]);
+      for (int r = 0; r < 16; r++) {
+        sc[r] = sc[r] * a.coef;
+        mb = fmaxf(mb, sc[r]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int32_t key = (int32_t)(kb * PA_KB + 8 * (r / 4) + 4 * lg + r % 4);
+        sc[r] = key <= pj ? sc[r] * a.coef : -INFINITY;
+        mb = fmaxf(mb, sc[r]);
+      }
     }
     // lanes l and l ^ 32 hold the same query: v_permlane32_swap hands each
     // the other's value (the pair it returns is {x[l], x[l ^ 32]})
@@ -220,13 +258,14 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
     // 16 s2 + 8 (e/4) + 4 lg + e%4 in both operands
 #pragma unroll
     for (int s2 = 0; s2 < 2; s2++) {
-      v8h ph, pl;
+      v8h ph;
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const _Float16 h = (_Float16)sc[8 * s2 + e];
-        ph[e] = h;
-        pl[e] = (_Float16)(sc[8 * s2 + e] - (float)h);
-      }
+      for (int e = 0; e < 8; e++) ph[e] = (_Float16)sc[8 * s2 + e];
+      const uint4 hw = __builtin_bit_cast(uint4, ph);
+      const v8h pl = __builtin_bit_cast(v8h, make_uint4(pa_lo2(sc[8 * s2], sc[8 * s2 + 1], hw.x),
+                                                        pa_lo2(sc[8 * s2 + 2], sc[8 * s2 + 3], hw.y),
+                                                        pa_lo2(sc[8 * s2 + 4], sc[8 * s2 + 5], hw.z),
+                                                        pa_lo2(sc[8 * s2 + 6], sc[8 * s2 + 7], hw.w)));
 #pragma unroll
       for (int t = 0; t < HD / 32; t++) {
         const uint16_t *vrow = &s_v[buf][(32 * t + li) * VP + 16 * s2 + 4 * lg];
@@ -240,6 +279,7 @@ __global__ __launch_bounds__(64 * GRP, GRP >= 4 ? 8 / GRP : 1) void k_prefill_at
   }
 #undef PA_LOAD
 #undef PA_STORE
+#undef PA_RES
   // O^T tile t, register r: dim 32 t + 8 (r/4) + 4 lg + r%4 of query li
   if (SPLIT) {
     if (live) {
@@ -399,6 +439,8 @@ int nlg_prefill_attn(const float *q, const uint16_t *kc, const uint16_t *vc, con
   if (grp != 1 && grp != 2 && grp != 4 && grp != 8) return nlg_fail("prefill attn: heads/kvheads %u not 1, 2, 4 or 8", grp);
   if (!qper || rows % qper) return nlg_fail("prefill attn: rows %u not a multiple of rows per sequence %u", rows, qper);
   if (!max_seq) return nlg_fail("prefill attn: max_seq is 0");
+  if ((uint64_t)max_seq * head_dim * 2 >= (1ull << 31))
+    return nlg_fail("prefill attn: a cache slot of %u x %u halves exceeds 2 GiB", max_seq, head_dim);
   if (((uintptr_t)q & 15) || ((uintptr_t)kc & 15) || ((uintptr_t)vc & 15) || ((uintptr_t)ctx & 15))
     return nlg_fail("prefill attn: q, caches and ctx must be 16-byte aligned");
   const uint32_t nseq = rows / qper;
