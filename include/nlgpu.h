@@ -384,7 +384,8 @@ int nlg_attn_ternary_linear_residual(const void *workspace, size_t workspace_byt
  * [rows/qper][kvheads][max_seq][head_dim] that nlg_rms_ternary_qkv_rope
  * fills.  q and ctx are [rows][heads*head_dim] f32; row r is sequence
  * r / qper at position pos[0] + r % qper.  head_dim 64 or 128, heads/kvheads
- * in {1,2,4,8}, rows a multiple of qper; f16 matrix cores with q and the
+ * in {1,2,4,8}, rows a multiple of qper, one sequence's cache of one kv
+ * head (max_seq x head_dim halves) under 2 GiB; f16 matrix cores with q and the
  * probabilities split into hi + lo halves (f32-grade products).  One launch,
  * or -- when the grid would have fewer than 256 workgroups (a single prompt)
  * -- two: the keys of each query block in pieces, then their merge, with the

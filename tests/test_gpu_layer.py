@@ -509,6 +509,9 @@ def test_prefill_attention_rejects_bad_shapes():
         nlgpu.prefill_attn_f16(d, d, d, pos, 10, 4, 4, 2, 64, 16, d)
     with pytest.raises(nlgpu.NlgError, match="head_dim"):
         nlgpu.prefill_attn_f16(d, d, d, pos, 4, 4, 4, 2, 96, 16, d)
+    # a cache slot the key/value blocks' buffer resources cannot span (refused before any launch)
+    with pytest.raises(nlgpu.NlgError, match="2 GiB"):
+        nlgpu.prefill_attn_f16(d, d, d, pos, 4, 4, 4, 2, 128, 1 << 23, d)
 
 
 def test_folded_merge_rejects_too_many_chunks():
